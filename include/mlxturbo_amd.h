@@ -1,0 +1,110 @@
+/*
+ * mlxturbo_amd: C ABI of the MI355X (gfx950) quantized-matmul hot path.
+ *
+ * Plain C: caller-owned device buffers, sizes in elements, an explicit HIP
+ * stream (hipStream_t passed as void*, NULL = default stream), no
+ * allocation of user-visible memory, no stream synchronisation, every output
+ * element written.  Safe to call from several host threads on different
+ * streams.
+ *
+ * Formats (MLX affine quantization, the format the reference's kernels read:
+ * mlxturbo/fast_qmm.py:93-106, kernels/_steel_flat.py:1152-1256):
+ *   w       uint32 [N, K*bits/32]   code j of word i = element i*(32/bits)+j,
+ *                                   at bit bits*j (low bits first)
+ *   scales  T [N, K/group_size]     T = the activation dtype
+ *   biases  T [N, K/group_size]
+ *   deq     T(float(s)*q + float(b)), rounded to nearest even
+ * Gather banks add a leading expert dimension E.
+ *
+ * Status codes: 0 = ok; MQ_EINVAL (-1) = invalid argument (the caller raises
+ * ValueError, as MLX does); MQ_EUNSUPPORTED (-2) = valid but not implemented
+ * here (caller raises NotImplementedError); > 0 = a hipError_t.  The message
+ * of the last non-zero status on the calling thread is in mq_last_error().
+ */
+#ifndef MLXTURBO_AMD_H
+#define MLXTURBO_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_OK 0
+#define MQ_EINVAL (-1)
+#define MQ_EUNSUPPORTED (-2)
+
+/* dtype codes of x / scales / biases / out */
+#define MQ_BFLOAT16 0
+#define MQ_FLOAT16 1
+#define MQ_FLOAT32 2
+
+/* ABI version; bumped on any signature change. */
+int mq_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* mq_last_error(void);
+
+/* Number of kernel launches made by this process (all entry points).  The
+ * counterpart of the reference's "fire" counters (mlxturbo/kernels/_fire.py:
+ * 17-32) that prove a custom kernel actually ran. */
+uint64_t mq_launch_count(void);
+
+/*
+ * out[N, K] (T) = dequantize(w, scales, biases).
+ * Replaces mx.dequantize(w, scales, biases, group_size, bits, mode="affine"),
+ * the format definer the reference's fp32 references call
+ * (bench/test_qmm_wide_shapes.py:35-42, kernels/moe_verify_gather.py:932).
+ * bits in {4, 8}; group_size in {32, 64, 128}; dtype any of the three.
+ */
+int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, void* out,
+                  int64_t N, int64_t K, int group_size, int bits, int dtype, void* hip_stream);
+
+/*
+ * out[M, N] = x[M, K] . dequantize(w)^T       (transpose = 1)
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True,
+ * group_size, bits, mode="affine") as called by the reference's route layer
+ * (mlxturbo/kernels/dispatch.py:302-382, the stock() call at 317-327) and its
+ * drop-ins fast_qmm (mlxturbo/fast_qmm.py:334-374), qmv_small_m
+ * (kernels/qmv_small_m.py:289-335), qmv_wide_nocap (kernels/
+ * qmv_wide_nocap.py:240-288) and qmm_wide (kernels/qmm_wide.py:456-502).
+ * x and out are row-major with leading dimension K and N.
+ * bits in {4, 8}; group_size in {32, 64, 128}; dtype bfloat16 or float16;
+ * transpose = 0 returns MQ_EUNSUPPORTED (the reference never accelerates it).
+ */
+int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, int dtype, int transpose, void* hip_stream);
+
+/*
+ * Bytes of device workspace mq_gather_qmm needs for P index pairs.
+ */
+size_t mq_gather_qmm_workspace_size(int64_t P, int64_t M);
+
+/*
+ * out[p, M, N] = x[lhs[p], M, K] . dequantize(w[rhs[p]])^T   for p < P.
+ * Replaces mx.gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices,
+ * transpose=True, group_size, bits, mode="affine", sorted_indices) as called
+ * by mlx-lm's QuantizedSwitchLinear / SwitchGLU (fused.py:2389-2394,
+ * 2402-2418, 3105-3116) and by the reference's decode/verify gather kernels
+ * (kernels/moe_decode_fused.py:331-397, kernels/moe_verify_gather.py:453-875)
+ * and prefill grouped GEMM (kernels/moe_grouped_gemm.py:913-1066).
+ * x is [B, M, K]; w is [E, N, K*bits/32]; scales/biases [E, N, K/group_size];
+ * lhs_indices may be NULL (then lhs[p] = p, requiring B == P); indices are
+ * int32 device arrays of length P (the caller broadcasts them).  Pairs that
+ * share an expert are computed together so each expert's weights are read
+ * once per call.  sorted_indices = 1 promises rhs is non-decreasing.
+ * workspace must hold mq_gather_qmm_workspace_size(P, M) bytes.
+ */
+int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                  const int32_t* lhs_indices, const int32_t* rhs_indices, void* out, int64_t P,
+                  int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, int group_size, int bits,
+                  int dtype, int sorted_indices, void* workspace, size_t workspace_bytes,
+                  void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXTURBO_AMD_H */

@@ -1,0 +1,15 @@
+"""mlxturbo_amd: MI355X-native (gfx950) quantized-matmul hot path of mlxturbo.
+
+Drop-in operators with MLX's signatures over PyTorch-ROCm tensors, backed by
+hand-written HIP kernels behind a C ABI (``include/mlxturbo_amd.h``):
+
+* :func:`quantized_matmul` - decode (M=1), verify (M=2..16) and prefill widths
+* :func:`gather_qmm`       - MoE expert gather
+* :func:`dequantize`       - bit-exact MLX affine dequantization
+"""
+
+from .ops import dequantize, gather_qmm, launch_count, quantized_matmul
+
+__version__ = "0.1.0"
+
+__all__ = ["dequantize", "gather_qmm", "launch_count", "quantized_matmul", "__version__"]

@@ -1,0 +1,96 @@
+"""ctypes binding of ``libmlxturbo_amd.so`` (C ABI in ``include/mlxturbo_amd.h``).
+
+The library is built in-tree by :mod:`mlxturbo_amd.build`.  There is no
+fallback: if the library is missing every operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_NAME = "libmlxturbo_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+MQ_OK = 0
+MQ_EINVAL = -1
+MQ_EUNSUPPORTED = -2
+
+MQ_BFLOAT16 = 0
+MQ_FLOAT16 = 1
+MQ_FLOAT32 = 2
+
+# every symbol include/mlxturbo_amd.h declares
+EXPORTED = (
+    "mq_version",
+    "mq_last_error",
+    "mq_launch_count",
+    "mq_dequantize",
+    "mq_quantized_matmul",
+    "mq_gather_qmm_workspace_size",
+    "mq_gather_qmm",
+)
+
+_lock = threading.Lock()
+_lib = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def _bind(lib: ctypes.CDLL) -> None:
+    lib.mq_version.restype = _int
+    lib.mq_version.argtypes = []
+    lib.mq_last_error.restype = ctypes.c_char_p
+    lib.mq_last_error.argtypes = []
+    lib.mq_launch_count.restype = ctypes.c_uint64
+    lib.mq_launch_count.argtypes = []
+    lib.mq_dequantize.restype = _int
+    lib.mq_dequantize.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]
+    lib.mq_quantized_matmul.restype = _int
+    lib.mq_quantized_matmul.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
+                                        _int, _int, _vp]
+    lib.mq_gather_qmm_workspace_size.restype = ctypes.c_size_t
+    lib.mq_gather_qmm_workspace_size.argtypes = [_i64, _i64]
+    lib.mq_gather_qmm.restype = _int
+    lib.mq_gather_qmm.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                  _i64, _i64, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library once; raise :class:`LibraryMissing` if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise LibraryMissing(
+                    f"{LIB_PATH} is not built; run `python -m mlxturbo_amd.build` "
+                    "(hipcc for gfx950).  mlxturbo_amd has no CPU fallback.")
+            handle = ctypes.CDLL(LIB_PATH)
+            _bind(handle)
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map an ABI status to the exception MLX would raise."""
+    if rc == MQ_OK:
+        return
+    msg = lib().mq_last_error().decode(errors="replace")
+    if rc == MQ_EINVAL:
+        raise ValueError(f"[{what}] {msg}")
+    if rc == MQ_EUNSUPPORTED:
+        raise NotImplementedError(f"[{what}] {msg}")
+    raise RuntimeError(f"[{what}] HIP error {rc}: {msg}")
+
+
+def launch_count() -> int:
+    return int(lib().mq_launch_count())

@@ -1,0 +1,204 @@
+// C ABI of mlxturbo_amd (declared in include/mlxturbo_amd.h): argument
+// validation, route selection and kernel launches.  No allocation, no
+// synchronisation; every error is a status code plus a thread-local message.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mlxturbo_amd.h"
+#include "dequant.cuh"
+#include "gather.cuh"
+#include "qmm_skinny.cuh"
+#include "qmm_wide.cuh"
+
+namespace {
+
+thread_local std::string g_last_error;
+std::atomic<uint64_t> g_launches{0};
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail((int)e, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_launches.fetch_add(1, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(const void* w, const void* scales, const void* biases, int64_t N, int64_t K,
+                 int group_size, int bits, int dtype) {
+  if (!w || !scales) return fail(MQ_EINVAL, "w and scales must be non-null");
+  if (!biases) return fail(MQ_EINVAL, "affine mode requires biases");
+  if (N < 0 || K <= 0) return fail(MQ_EINVAL, "invalid sizes N=%lld K=%lld", (long long)N, (long long)K);
+  if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8)
+    return fail(MQ_EINVAL, "bits must be one of 2,3,4,5,6,8 (got %d)", bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(MQ_EINVAL, "group_size must be 32, 64 or 128 (got %d)", group_size);
+  if (K % group_size)
+    return fail(MQ_EINVAL, "K=%lld is not a multiple of group_size=%d", (long long)K, group_size);
+  if (dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16 && dtype != MQ_FLOAT32)
+    return fail(MQ_EINVAL, "unknown dtype code %d", dtype);
+  if (bits != 4 && bits != 8)
+    return fail(MQ_EUNSUPPORTED, "bits=%d is not implemented (4 and 8 are)", bits);
+  if (!aligned16(w)) return fail(MQ_EINVAL, "w must be 16-byte aligned");
+  return MQ_OK;
+}
+
+template <template <int, int, int> class Launcher, typename... Args>
+int dispatch_16(int dtype, int bits, int gs, Args... args) {
+#define MQ_CASE(DT, B, G)                                   \
+  if (dtype == DT && bits == B && gs == G) {                \
+    Launcher<DT, B, G>::run(args...);                       \
+    return MQ_OK;                                           \
+  }
+  MQ_CASE(mq::kBF16, 4, 64) MQ_CASE(mq::kBF16, 4, 32) MQ_CASE(mq::kBF16, 4, 128)
+  MQ_CASE(mq::kBF16, 8, 64) MQ_CASE(mq::kBF16, 8, 32) MQ_CASE(mq::kBF16, 8, 128)
+  MQ_CASE(mq::kF16, 4, 64) MQ_CASE(mq::kF16, 4, 32) MQ_CASE(mq::kF16, 4, 128)
+  MQ_CASE(mq::kF16, 8, 64) MQ_CASE(mq::kF16, 8, 32) MQ_CASE(mq::kF16, 8, 128)
+#undef MQ_CASE
+  return fail(MQ_EUNSUPPORTED, "no kernel for dtype=%d bits=%d group_size=%d", dtype, bits, gs);
+}
+
+int grid_for(int64_t work, int per_block) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+template <int DT, int BITS, int GS>
+struct DequantLaunch {
+  static void run(const uint32_t* w, const void* s, const void* b, void* out, int64_t N, int64_t K,
+                  hipStream_t st) {
+    const int64_t chunks = N * (K * BITS / 32) / 4;
+    hipLaunchKernelGGL((mq::dequantize16_kernel<DT, BITS, GS>), dim3(grid_for(chunks, 256)),
+                       dim3(256), 0, st, w, (const uint16_t*)s, (const uint16_t*)b,
+                       (uint16_t*)out, N, K);
+  }
+};
+
+template <int DT, int BITS, int GS>
+struct SkinnyLaunch {
+  static void run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
+                  int64_t M, int64_t N, int64_t K, hipStream_t st) {
+    for (int64_t m0 = 0; m0 < M; m0 += 16) {
+      const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
+      hipLaunchKernelGGL((mq::qmm_skinny_kernel<DT, BITS, GS>), dim3((unsigned)((N + 15) / 16)),
+                         dim3(256), 0, st, (const uint16_t*)x + m0 * K, w, (const uint16_t*)s,
+                         (const uint16_t*)b, (uint16_t*)out + m0 * N, mt, (int)N, (int)K,
+                         (int64_t)K, (int64_t)N);
+    }
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int mq_version(void) { return 1; }
+
+const char* mq_last_error(void) { return g_last_error.c_str(); }
+
+uint64_t mq_launch_count(void) { return g_launches.load(std::memory_order_relaxed); }
+
+int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, void* out,
+                  int64_t N, int64_t K, int group_size, int bits, int dtype, void* hip_stream) {
+  int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!out) return fail(MQ_EINVAL, "out must be non-null");
+  if (N == 0) return MQ_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  if (dtype == MQ_FLOAT32) {
+    const int64_t words = N * (K * bits / 32);
+#define MQ_D32(B, G)                                                                         \
+  if (bits == B && group_size == G) {                                                         \
+    hipLaunchKernelGGL((mq::dequantize32_kernel<B, G>), dim3(grid_for(words, 256)), dim3(256), \
+                       0, st, w, (const float*)scales, (const float*)biases, (float*)out, N, K); \
+    return check_launch("dequantize");                                                        \
+  }
+    MQ_D32(4, 32) MQ_D32(4, 64) MQ_D32(4, 128) MQ_D32(8, 32) MQ_D32(8, 64) MQ_D32(8, 128)
+#undef MQ_D32
+    return fail(MQ_EUNSUPPORTED, "dequantize: unsupported float32 configuration");
+  }
+  if (!aligned16(out)) return fail(MQ_EINVAL, "out must be 16-byte aligned");
+  rc = dispatch_16<DequantLaunch>(dtype, bits, group_size, w, scales, biases, out, N, K, st);
+  if (rc) return rc;
+  return check_launch("dequantize");
+}
+
+int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, int dtype, int transpose, void* hip_stream) {
+  int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !out) return fail(MQ_EINVAL, "x and out must be non-null");
+  if (M < 0) return fail(MQ_EINVAL, "invalid M=%lld", (long long)M);
+  if (!transpose)
+    return fail(MQ_EUNSUPPORTED, "transpose=False is not implemented on this path");
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (N > INT32_MAX || K > INT32_MAX || M > INT32_MAX)
+    return fail(MQ_EINVAL, "dimension exceeds int32 range");
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (M == 0 || N == 0) return MQ_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  if (mq::wide_eligible(M, N, K, bits, group_size)) {
+    rc = mq::launch_wide(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, st);
+    if (rc) return fail(rc, "quantized_matmul: no wide kernel for this configuration");
+    return check_launch("quantized_matmul(wide)");
+  }
+  rc = dispatch_16<SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K, st);
+  if (rc) return rc;
+  return check_launch("quantized_matmul(skinny)");
+}
+
+size_t mq_gather_qmm_workspace_size(int64_t P, int64_t M) {
+  return mq::gather_workspace_bytes(P, M);
+}
+
+int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                  const int32_t* lhs_indices, const int32_t* rhs_indices, void* out, int64_t P,
+                  int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, int group_size, int bits,
+                  int dtype, int sorted_indices, void* workspace, size_t workspace_bytes,
+                  void* hip_stream) {
+  int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !out || !rhs_indices) return fail(MQ_EINVAL, "x, out and rhs_indices must be non-null");
+  if (P < 0 || M < 0 || E <= 0 || B < 0)
+    return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
+                (long long)M, (long long)E, (long long)B);
+  if (!lhs_indices && B != P)
+    return fail(MQ_EINVAL, "lhs_indices=NULL requires B == P (B=%lld P=%lld)", (long long)B,
+                (long long)P);
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (N > INT32_MAX || K > INT32_MAX || P > INT32_MAX || E > INT32_MAX || M > 16)
+    return fail(MQ_EUNSUPPORTED, "gather_qmm supports M <= 16 rows per pair");
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (P == 0 || M == 0 || N == 0) return MQ_OK;
+  if (workspace_bytes < mq::gather_workspace_bytes(P, M) || !workspace)
+    return fail(MQ_EINVAL, "workspace too small: need %zu bytes",
+                mq::gather_workspace_bytes(P, M));
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  int nl = 0;
+  rc = mq::launch_gather(x, w, scales, biases, lhs_indices, rhs_indices, out, P, B, M, N, K, E,
+                         group_size, bits, dtype, sorted_indices, workspace, st, &nl);
+  if (rc) return fail(rc, "gather_qmm: no kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail((int)e, "gather_qmm: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
+}  // extern "C"

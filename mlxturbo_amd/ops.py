@@ -1,0 +1,253 @@
+"""MLX-signature operators on PyTorch-ROCm tensors, backed by the HIP library.
+
+Host side of the drop-in boundary.  Signatures and argument meaning follow
+MLX 0.32's operators as the reference calls them:
+
+* ``quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode)``
+  - mx.quantized_matmul, called at mlxturbo/kernels/dispatch.py:317-327
+* ``gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices, transpose,
+  group_size, bits, mode, sorted_indices)`` - mx.gather_qmm, called by mlx-lm's
+  QuantizedSwitchLinear (mlxturbo/fused.py:2389-2394, 3105-3116)
+* ``dequantize(w, scales, biases, group_size, bits, mode)`` - mx.dequantize
+  (bench/test_qmm_wide_shapes.py:35-42)
+
+Errors: genuinely invalid arguments raise ``ValueError`` as MLX does;
+configurations the reference never accelerates and this build does not
+implement (``transpose=False``, non-affine modes, bits other than 4/8,
+float32 activations) raise ``NotImplementedError``.  There is no CPU or
+PyTorch fallback: every result comes from a HIP kernel.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {
+    torch.bfloat16: _lib.MQ_BFLOAT16,
+    torch.float16: _lib.MQ_FLOAT16,
+    torch.float32: _lib.MQ_FLOAT32,
+}
+
+_GROUP_SIZES = (32, 64, 128)
+_BITS = (2, 3, 4, 5, 6, 8)
+
+
+def _stream_ptr(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected torch.Tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise ValueError(
+                "mlxturbo_amd operators run on a ROCm GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Row-contiguous with a 16-byte aligned base (copies only when needed)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _check_mode(mode: str, biases) -> None:
+    if mode != "affine":
+        raise NotImplementedError(
+            f"mode={mode!r}: only affine quantization is on this path")
+    if biases is None:
+        raise ValueError("affine quantization requires biases")
+
+
+def _check_quant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int, bits: int) -> int:
+    if w.dtype not in (torch.uint32, torch.int32):
+        raise ValueError(f"w must be uint32 packed codes, got {w.dtype}")
+    if group_size not in _GROUP_SIZES:
+        raise ValueError(f"group_size must be one of {_GROUP_SIZES}, got {group_size}")
+    if bits not in _BITS:
+        raise ValueError(f"bits must be one of {_BITS}, got {bits}")
+    if bits not in (4, 8):
+        raise NotImplementedError(f"bits={bits}: only 4- and 8-bit codes are on this path")
+    K = w.shape[-1] * 32 // bits
+    if scales.shape != biases.shape:
+        raise ValueError(f"scales {tuple(scales.shape)} and biases {tuple(biases.shape)} differ")
+    if scales.dtype != biases.dtype:
+        raise ValueError("scales and biases must have the same dtype")
+    want = (*w.shape[:-1], K // group_size)
+    if K % group_size or tuple(scales.shape) != want:
+        raise ValueError(
+            f"scales shape {tuple(scales.shape)} does not match w {tuple(w.shape)} "
+            f"with group_size={group_size}, bits={bits} (expected {want})")
+    return K
+
+
+def _dtype_code(x_dtype: torch.dtype, s_dtype: torch.dtype) -> int:
+    if x_dtype != s_dtype:
+        raise NotImplementedError(
+            f"x dtype {x_dtype} differs from scales dtype {s_dtype}; MLX would promote "
+            "both, this path computes in the shared 16-bit dtype only")
+    if x_dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"activation dtype {x_dtype}: bfloat16 and float16 only")
+    return _DTYPE_CODE[x_dtype]
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: Optional[torch.Tensor] = None,
+               group_size: int = 64, bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """``mx.dequantize``: ``T(float(s)*q + float(b))`` bit-exact, dtype of ``scales``."""
+    _check_mode(mode, biases)
+    dev = _require_gpu(w, scales, biases)
+    K = _check_quant(w, scales, biases, group_size, bits)
+    if scales.dtype not in _DTYPE_CODE:
+        raise ValueError(f"scales dtype {scales.dtype} is not a float type")
+    N = w.numel() // max(1, w.shape[-1]) if w.ndim else 0
+    out = torch.empty((*w.shape[:-1], K), dtype=scales.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    w_, s_, b_ = _aligned(w), _aligned(scales), _aligned(biases)
+    rc = _lib.lib().mq_dequantize(w_.data_ptr(), s_.data_ptr(), b_.data_ptr(), out.data_ptr(),
+                                  N, K, group_size, bits, _DTYPE_CODE[scales.dtype],
+                                  _stream_ptr(out))
+    _lib.check(rc, "dequantize")
+    return out
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: Optional[torch.Tensor] = None, transpose: bool = True,
+                     group_size: int = 64, bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """``mx.quantized_matmul``: ``x @ dequantize(w).T`` for ``x[..., K]``.
+
+    Leading dimensions of ``x`` are flattened to M and restored on the output
+    (as mlxturbo/kernels/dispatch.py:332-382 does around its kernels).
+    """
+    _check_mode(mode, biases)
+    dev = _require_gpu(x, w, scales, biases)
+    if w.ndim != 2:
+        raise NotImplementedError("batched w: only 2-D weights are on this path")
+    if not transpose:
+        raise NotImplementedError("transpose=False is not on this path")
+    K = _check_quant(w, scales, biases, group_size, bits)
+    if x.ndim < 1:
+        raise ValueError("x must have at least one dimension")
+    if x.shape[-1] != K:
+        raise ValueError(
+            f"x last dimension {x.shape[-1]} does not match the quantized weight K={K}")
+    code = _dtype_code(x.dtype, scales.dtype)
+    N = w.shape[0]
+    lead = tuple(x.shape[:-1])
+    M = math.prod(lead)
+    out = torch.empty((*lead, N), dtype=x.dtype, device=dev)
+    if M == 0 or N == 0:
+        return out
+    x_ = _aligned(x.reshape(M, K))
+    w_, s_, b_ = _aligned(w), _aligned(scales), _aligned(biases)
+    rc = _lib.lib().mq_quantized_matmul(x_.data_ptr(), w_.data_ptr(), s_.data_ptr(),
+                                        b_.data_ptr(), out.data_ptr(), M, N, K, group_size, bits,
+                                        code, 1, _stream_ptr(out))
+    _lib.check(rc, "quantized_matmul")
+    return out
+
+
+_WS_CACHE: dict = {}
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    key = (dev.type, dev.index)
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
+        _WS_CACHE[key] = buf
+    return buf
+
+
+def _as_index(t, dev) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(t)
+    if t.dtype.is_floating_point or t.dtype == torch.bool:
+        raise ValueError(f"indices must be integers, got {t.dtype}")
+    return t.to(device=dev)
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+               biases: Optional[torch.Tensor] = None, lhs_indices=None, rhs_indices=None,
+               transpose: bool = True, group_size: int = 64, bits: int = 4,
+               mode: str = "affine", sorted_indices: bool = False) -> torch.Tensor:
+    """``mx.gather_qmm``: per index pair, ``x[lhs] @ dequantize(w[rhs]).T``.
+
+    ``x`` is ``(..., M, K)`` and ``w`` ``(..., N, K*bits/32)``; ``lhs_indices``
+    index x's batch dims (default: all of them), ``rhs_indices`` index w's
+    batch dims (default: all of them); the two broadcast together and the
+    output is ``broadcast_shape + (M, N)``.
+    """
+    _check_mode(mode, biases)
+    dev = _require_gpu(x, w, scales, biases)
+    if not transpose:
+        raise NotImplementedError("transpose=False is not on this path")
+    if x.ndim < 2 or w.ndim < 3:
+        raise ValueError("gather_qmm needs x (..., M, K) and w (..., N, K*bits/32) with a batch dim")
+    K = _check_quant(w, scales, biases, group_size, bits)
+    if x.shape[-1] != K:
+        raise ValueError(
+            f"x last dimension {x.shape[-1]} does not match the quantized weight K={K}")
+    code = _dtype_code(x.dtype, scales.dtype)
+    M = x.shape[-2]
+    N = w.shape[-2]
+    bx = tuple(x.shape[:-2])
+    bw = tuple(w.shape[:-2])
+    B = math.prod(bx)
+    E = math.prod(bw)
+    lhs = (torch.arange(B, device=dev, dtype=torch.int32).reshape(bx) if lhs_indices is None
+           else _as_index(lhs_indices, dev))
+    rhs = (torch.arange(E, device=dev, dtype=torch.int32).reshape(bw) if rhs_indices is None
+           else _as_index(rhs_indices, dev))
+    try:
+        shape = torch.broadcast_shapes(lhs.shape, rhs.shape)
+    except RuntimeError as exc:
+        raise ValueError(f"lhs_indices {tuple(lhs.shape)} and rhs_indices "
+                         f"{tuple(rhs.shape)} do not broadcast") from exc
+    P = math.prod(shape)
+    out = torch.empty((*shape, M, N), dtype=x.dtype, device=dev)
+    if P == 0 or M == 0 or N == 0:
+        return out
+    if M > 16:
+        raise NotImplementedError(f"gather_qmm with M={M} rows per pair (> 16)")
+    lhs_f = lhs.expand(shape).reshape(-1).to(torch.int32).contiguous()
+    rhs_f = rhs.expand(shape).reshape(-1).to(torch.int32).contiguous()
+    x_ = _aligned(x.reshape(B, M, K))
+    w_ = _aligned(w.reshape(E, N, w.shape[-1]))
+    s_ = _aligned(scales.reshape(E, N, scales.shape[-1]))
+    b_ = _aligned(biases.reshape(E, N, biases.shape[-1]))
+    lib = _lib.lib()
+    nbytes = int(lib.mq_gather_qmm_workspace_size(P, M))
+    ws = _workspace(dev, nbytes) if nbytes else None
+    rc = lib.mq_gather_qmm(x_.data_ptr(), w_.data_ptr(), s_.data_ptr(), b_.data_ptr(),
+                           lhs_f.data_ptr(), rhs_f.data_ptr(), out.data_ptr(), P, B, M, N, K, E,
+                           group_size, bits, code, int(bool(sorted_indices)),
+                           ws.data_ptr() if ws is not None else None,
+                           ws.numel() if ws is not None else 0, _stream_ptr(out))
+    _lib.check(rc, "gather_qmm")
+    return out
+
+
+def launch_count() -> int:
+    """Kernel launches made through the library so far (proof the HIP path ran)."""
+    return _lib.launch_count()
+
+
+__all__: Sequence[str] = ("dequantize", "quantized_matmul", "gather_qmm", "launch_count")

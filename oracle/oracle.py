@@ -1,0 +1,290 @@
+"""CPU oracle for MLX-format affine quantized matmul.  TEST INFRASTRUCTURE ONLY.
+
+Nothing in the ``mlxturbo_amd`` package imports this module.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use it,
+and only as the checker of the HIP path, never as the thing measured or
+shipped.
+
+The algorithm restated here lives in MLX 0.32.2 (``mlx==0.32.2`` pinned in the
+reference's ``uv.lock:284-300``; not vendored, not importable here).  The
+reference's in-tree statements of it are cited per function.  Every function
+below is pinned by an independent check in ``tests/test_oracle.py``:
+
+=====================  ========================================================
+function               pinned by
+=====================  ========================================================
+pack / unpack          hand-written words (0x76543210 -> codes 0..7), round
+                       trip, and an independent bit-string construction
+bf16_bits / f16_bits   torch's own float->bf16/fp16 casts (RNE), exhaustive
+                       special values (ties, carries into the exponent, inf,
+                       subnormals)
+dequantize             closed form cases: q=0 -> b, s=0 -> b, exactness of
+                       s*q in fp32, and a float64 route rounded once
+quantized_matmul_ref   brute-force pure-Python loop on tiny shapes, linearity
+                       in x, row independence, column independence
+gather_qmm_ref         dense matmul on w[idx] per pair, sort invariance
+quantize               **parity unpinned**: MLX's quantizer source is not in
+                       the container; the restatement is checked only for
+                       its invariants (codes in range, |deq - w| <= |s|/2
+                       away from clipping, zero exactly representable)
+=====================  ========================================================
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+DTYPES = ("bfloat16", "float16", "float32")
+
+
+# --------------------------------------------------------------------- packing
+
+def pack(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Pack integer codes ``[..., K]`` into uint32 words, low bits first.
+
+    Code ``j`` of word ``i`` is element ``i*(32/bits) + j`` and sits at bit
+    ``bits*j`` (reference: mlxturbo/fast_qmm.py:96-106 reads nibble ``t`` of
+    word ``p0`` as element ``t``; _steel_flat.py:1251-1254 reads byte ``i`` as
+    element ``i`` for 8-bit).
+    """
+    if bits not in (2, 4, 8):
+        raise ValueError(f"bits={bits} not supported by the oracle packer")
+    codes = np.asarray(codes, dtype=np.uint64)
+    per = 32 // bits
+    if codes.shape[-1] % per:
+        raise ValueError("last dim must be a multiple of 32/bits")
+    if codes.size and int(codes.max()) >= (1 << bits):
+        raise ValueError("code out of range")
+    c = codes.reshape(*codes.shape[:-1], codes.shape[-1] // per, per)
+    shifts = (np.arange(per, dtype=np.uint64) * bits)
+    return (c << shifts).sum(axis=-1).astype(np.uint32)
+
+
+def unpack(w: np.ndarray, bits: int) -> np.ndarray:
+    """Inverse of :func:`pack`: uint32 ``[..., Kw]`` -> codes ``[..., Kw*32/bits]``."""
+    w = np.asarray(w, dtype=np.uint32)
+    per = 32 // bits
+    shifts = (np.arange(per, dtype=np.uint32) * bits)
+    c = (w[..., None] >> shifts) & np.uint32((1 << bits) - 1)
+    return c.reshape(*w.shape[:-1], w.shape[-1] * per).astype(np.uint32)
+
+
+# ------------------------------------------------------------ float formats
+
+def bf16_bits(f32: np.ndarray) -> np.ndarray:
+    """Round float32 to bfloat16 (round-to-nearest-even), returned as uint16 bits.
+
+    Integer formulation: add 0x7FFF plus the lowest kept bit, truncate.
+    NaN maps to a quiet NaN with the sign kept.
+    """
+    u = np.asarray(f32, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) & 0xFFFF
+    nan = np.isnan(np.asarray(f32, dtype=np.float32))
+    r = np.where(nan, ((u >> 16) & 0x8000) | 0x7FC0, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_bits(f32: np.ndarray) -> np.ndarray:
+    """Round float32 to IEEE half (RNE), as uint16 bits (numpy's cast is RNE)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(f32, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def to_f32(bits_or_vals: np.ndarray, dtype: str) -> np.ndarray:
+    """Decode storage (uint16 bits for 16-bit types, float32 otherwise) to float32."""
+    if dtype == "bfloat16":
+        return bf16_to_f32(bits_or_vals)
+    if dtype == "float16":
+        return f16_to_f32(bits_or_vals)
+    return np.asarray(bits_or_vals, dtype=np.float32)
+
+
+def from_f32(f32: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 values to ``dtype`` storage (uint16 bits, or float32)."""
+    if dtype == "bfloat16":
+        return bf16_bits(f32)
+    if dtype == "float16":
+        return f16_bits(f32)
+    return np.asarray(f32, dtype=np.float32)
+
+
+# ------------------------------------------------------------------ dequant
+
+def dequantize_f32(w: np.ndarray, scales: np.ndarray, biases: np.ndarray,
+                   group_size: int, bits: int, dtype: str) -> np.ndarray:
+    """``fp32(s*q + b)`` before the final rounding to ``dtype``.
+
+    MLX computes ``float s = float(scale); float b = float(bias);``
+    ``w = static_cast<T>(s*q + b)`` (_steel_flat.py:1179-1180, 1210-1215 for
+    4-bit, 1251-1254 for 8-bit).  ``s*q`` is exact in float32 for 16-bit
+    scale types (<= 11+8 significant bits), so the value is ``s*q+b`` rounded
+    once to float32, whether or not the hardware fuses the multiply-add.
+    """
+    codes = unpack(w, bits).astype(np.float32)
+    s = to_f32(scales, dtype)
+    b = to_f32(biases, dtype)
+    K = codes.shape[-1]
+    if K % group_size:
+        raise ValueError("K must be a multiple of group_size")
+    s = np.repeat(s, group_size, axis=-1)
+    b = np.repeat(b, group_size, axis=-1)
+    if s.shape != codes.shape:
+        raise ValueError(f"scales shape {scales.shape} does not match w {w.shape}")
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (s * codes + b).astype(np.float32)
+
+
+def dequantize(w, scales, biases, group_size: int = 64, bits: int = 4,
+               dtype: str = "bfloat16") -> np.ndarray:
+    """Bit-exact dequantized weights in ``dtype`` storage (uint16 bits or float32).
+
+    Reference: mx.dequantize / QuantizedBlockLoader (_steel_flat.py:1169-1256,
+    1324-1335: the prefill tile loader dequantizes to T=bfloat16 in
+    threadgroup memory).
+    """
+    return from_f32(dequantize_f32(w, scales, biases, group_size, bits, dtype), dtype)
+
+
+# ------------------------------------------------------------------- matmul
+
+def quantized_matmul_ref(x, w, scales, biases, group_size: int = 64, bits: int = 4,
+                         dtype: str = "bfloat16", transpose: bool = True) -> np.ndarray:
+    """fp32 reference ``x . deq(W)^T`` over ``dtype``-rounded dequantized weights.
+
+    ``x`` is ``dtype`` storage ``[M, K]``.  Accumulation is float64, rounded
+    once to float32 at the end.  This is the reference the reference's own
+    fp32 checks use: test_qmm_wide_shapes.py:35-42 (``mx.dequantize`` then
+    ``.astype(float32)`` then matmul), moe_verify_gather.py:923-939.
+    With ``transpose=False`` ``w`` is ``[K, N*bits/32]`` and the result is
+    ``x . deq(W)`` (MLX's non-transposed layout).
+    """
+    xf = to_f32(x, dtype).astype(np.float64)
+    deq = to_f32(dequantize(w, scales, biases, group_size, bits, dtype), dtype)
+    deq = deq.astype(np.float64)
+    if transpose:
+        out = xf @ deq.T
+    else:
+        out = xf @ deq
+    return out.astype(np.float32)
+
+
+def gather_qmm_ref(x, w, scales, biases, lhs_indices, rhs_indices,
+                   group_size: int = 64, bits: int = 4, dtype: str = "bfloat16",
+                   transpose: bool = True) -> np.ndarray:
+    """Per-pair loop: ``out[p] = x_b[lhs[p]] . deq(w_e[rhs[p]])^T``.
+
+    ``x`` is ``[B, M, K]`` (batch flattened), ``w`` ``[E, N, Kw]``; indices are
+    flat ``[P]``.  Semantics of ``mx.gather_qmm`` as used by mlx-lm's
+    ``QuantizedSwitchLinear`` (moe_verify_gather.py:11-27, fused.py:2389-2394).
+    Returns float32 ``[P, M, N]``.
+    """
+    lhs = np.asarray(lhs_indices).reshape(-1)
+    rhs = np.asarray(rhs_indices).reshape(-1)
+    out = []
+    cache = {}
+    for p in range(lhs.shape[0]):
+        e = int(rhs[p])
+        if e not in cache:
+            deq = to_f32(dequantize(w[e], scales[e], biases[e], group_size, bits, dtype), dtype)
+            cache[e] = deq.astype(np.float64)
+        xf = to_f32(x[int(lhs[p])], dtype).astype(np.float64)
+        out.append(xf @ cache[e].T if transpose else xf @ cache[e])
+    return np.stack(out).astype(np.float32)
+
+
+# ----------------------------------------------------------------- quantize
+
+def quantize(w_fp: np.ndarray, group_size: int = 64, bits: int = 4,
+             dtype: str = "bfloat16"):
+    """Affine quantizer in the form MLX documents (parity unpinned).
+
+    Per group: ``scale = max((max-min)/(2^bits-1), 1e-7)``, signed towards the
+    edge of larger magnitude; the edge maps to a code exactly
+    (``q0 = round(edge/scale)``, ``scale = edge/q0`` when ``q0 != 0``) and
+    ``bias = edge`` (0 when ``q0 == 0``); codes
+    ``q = clip(round((w-bias)/scale), 0, 2^bits-1)`` use the float32 scale and
+    bias, which are then rounded to ``dtype`` for storage.  Rounding is
+    half-to-even (``mx.round``).  MLX's exact source is not in the container,
+    so this is a test-data generator only: every parity check compares
+    kernels and oracle on the same packed tensors.
+    """
+    w = np.asarray(w_fp, dtype=np.float32)
+    K = w.shape[-1]
+    if K % group_size:
+        raise ValueError("K must be a multiple of group_size")
+    g = w.reshape(*w.shape[:-1], K // group_size, group_size)
+    wmax = g.max(axis=-1)
+    wmin = g.min(axis=-1)
+    n_bins = np.float32((1 << bits) - 1)
+    mask = np.abs(wmin) > np.abs(wmax)
+    scale = np.maximum((wmax - wmin) / n_bins, np.float32(1e-7)).astype(np.float32)
+    scale = np.where(mask, scale, -scale).astype(np.float32)
+    edge = np.where(mask, wmin, wmax).astype(np.float32)
+    q0 = np.rint(edge / scale).astype(np.float32)
+    scale = np.where(q0 != 0, edge / np.where(q0 != 0, q0, np.float32(1)), scale).astype(np.float32)
+    bias = np.where(q0 == 0, np.float32(0), edge).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.rint((g - bias[..., None]) / scale[..., None])
+    q = np.nan_to_num(q, nan=0.0)
+    q = np.clip(q, 0, n_bins).astype(np.uint32).reshape(w.shape)
+    return pack(q, bits), from_f32(scale, dtype), from_f32(bias, dtype)
+
+
+# ---------------------------------------------------------------- tolerance
+
+def ulp_bf16(a: np.ndarray) -> np.ndarray:
+    """Spacing of bfloat16 numbers at |a| (normal range)."""
+    a = np.maximum(np.abs(np.asarray(a, dtype=np.float64)), 2.0 ** -126)
+    e = np.floor(np.log2(a))
+    return 2.0 ** (e - 7)
+
+
+def ulp_f16(a: np.ndarray) -> np.ndarray:
+    a = np.maximum(np.abs(np.asarray(a, dtype=np.float64)), 2.0 ** -14)
+    e = np.floor(np.log2(a))
+    return 2.0 ** (e - 10)
+
+
+def check_output(out_f32: np.ndarray, ref_f32: np.ndarray, dtype: str = "bfloat16",
+                 rel_l2: float = 1e-3, max_ulp: float = 2.0) -> dict:
+    """The correctness contract for matmul outputs (the tolerance lives here).
+
+    * ``relL2(out, round_dtype(ref)) <= 1e-3`` and
+    * ``|out - ref| <= 2 ulp(max(|ref|, 2^-8 * rms(ref row)))`` elementwise,
+
+    where ``ref`` is the fp32-accumulated product over dtype-rounded
+    dequantized weights.  The rms floor keeps cancellation-near-zero outputs
+    from demanding sub-ulp accuracy (the reference moved to atol+rtol and RMS
+    normalisation for the same reason: moe_verify_gather.py:942-956,
+    bench/test_moe_combine_fold.py:35-40).
+    """
+    out = np.asarray(out_f32, dtype=np.float64)
+    ref = np.asarray(ref_f32, dtype=np.float64)
+    if out.shape != ref.shape:
+        raise AssertionError(f"shape {out.shape} != {ref.shape}")
+    ref_r = to_f32(from_f32(ref.astype(np.float32), dtype), dtype).astype(np.float64)
+    num = np.linalg.norm((out - ref_r).ravel())
+    den = np.linalg.norm(ref_r.ravel())
+    rl2 = float(num / den) if den > 0 else float(num)
+    if ref.ndim >= 1 and ref.size:
+        rows = ref.reshape(-1, ref.shape[-1])
+        rms = np.sqrt(np.mean(rows ** 2, axis=-1, keepdims=True))
+        floor = np.broadcast_to(rms * 2.0 ** -8, rows.shape).reshape(ref.shape)
+    else:
+        floor = np.zeros_like(ref)
+    mag = np.maximum(np.abs(ref), floor)
+    ulp = ulp_bf16(mag) if dtype == "bfloat16" else (ulp_f16(mag) if dtype == "float16"
+                                                      else np.abs(mag) * 2.0 ** -20 + 1e-30)
+    err_ulp = np.abs(out - ref) / ulp
+    worst = float(err_ulp.max()) if err_ulp.size else 0.0
+    ok = (rl2 <= rel_l2) and (worst <= max_ulp) and bool(np.all(np.isfinite(out)))
+    return {"ok": ok, "rel_l2": rl2, "max_ulp": worst}

@@ -1,0 +1,230 @@
+"""CPU tests of the C ABI and the host logic (no GPU compute).
+
+Mirrors the reference's Metal-free static tests (bench/test_dispatch_static.py:
+fake backend through the module's own seams, kwarg contract, leading-dim
+flatten/restore) for the HIP boundary: the library loads, exports every
+declared symbol, validates arguments before touching the GPU, and the Python
+host logic passes the right sizes and indices to the ABI.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import mlxturbo_amd
+from mlxturbo_amd import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mlxturbo_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mq_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from mlxturbo_amd import build
+        build.build()
+    return _lib.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    declared = _declared()
+    assert declared, "no mq_ declarations parsed from the header"
+    assert set(declared) == set(_lib.EXPORTED)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version(lib):
+    assert lib.mq_version() == 1
+
+
+FAKE = 256  # aligned, never dereferenced: validation fails before any HIP call
+
+
+def _qmm(lib, **kw):
+    args = dict(x=FAKE, w=FAKE, s=FAKE, b=FAKE, out=FAKE, M=1, N=16, K=256, gs=64, bits=4,
+                dtype=0, transpose=1)
+    args.update(kw)
+    return lib.mq_quantized_matmul(args["x"], args["w"], args["s"], args["b"], args["out"],
+                                   args["M"], args["N"], args["K"], args["gs"], args["bits"],
+                                   args["dtype"], args["transpose"], None)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(b=None), -1, "requires biases"),
+    (dict(w=None), -1, "non-null"),
+    (dict(gs=48), -1, "group_size"),
+    (dict(K=200), -1, "multiple of group_size"),
+    (dict(bits=7), -1, "bits"),
+    (dict(bits=3), -2, "not implemented"),
+    (dict(transpose=0), -2, "transpose"),
+    (dict(dtype=2), -2, "float32"),
+    (dict(dtype=9), -1, "dtype"),
+    (dict(w=FAKE + 8), -1, "aligned"),
+    (dict(x=FAKE + 4), -1, "aligned"),
+    (dict(M=-1), -1, "M"),
+])
+def test_qmm_argument_validation(lib, kw, code, needle):
+    rc = _qmm(lib, **kw)
+    assert rc == code
+    assert needle in lib.mq_last_error().decode()
+
+
+def test_empty_problem_is_a_noop(lib):
+    assert _qmm(lib, M=0) == 0
+    assert _qmm(lib, N=0) == 0
+
+
+def test_gather_argument_validation(lib):
+    f = lib.mq_gather_qmm
+    # lhs NULL needs B == P
+    rc = f(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, 4, 3, 1, 16, 256, 8, 64, 4, 0, 0, None, 0, None)
+    assert rc == -1 and "B == P" in lib.mq_last_error().decode()
+    # more than 16 rows per pair
+    rc = f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, 17, 16, 256, 8, 64, 4, 0, 0, None, 0, None)
+    assert rc == -2
+    assert lib.mq_gather_qmm_workspace_size(64, 1) == 0          # fused segment discovery
+    assert lib.mq_gather_qmm_workspace_size(4096, 1) >= 4 * (1 + 4 * 4096)
+
+
+def test_dequant_argument_validation(lib):
+    rc = lib.mq_dequantize(FAKE, FAKE, None, FAKE, 4, 256, 64, 4, 0, None)
+    assert rc == -1
+    rc = lib.mq_dequantize(FAKE, FAKE, FAKE, FAKE + 2, 4, 256, 64, 4, 0, None)
+    assert rc == -1 and "aligned" in lib.mq_last_error().decode()
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(1, 256, dtype=torch.bfloat16)
+    w = torch.zeros(16, 32, dtype=torch.int32)
+    s = torch.zeros(16, 4, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        mlxturbo_amd.quantized_matmul(x, w, s, s)
+
+
+# ---------------------------------------------------------------- fake backend
+
+class _FakeLib:
+    """Records ABI calls; reads index arrays back from host pointers."""
+
+    def __init__(self):
+        self.calls = []
+
+    def mq_quantized_matmul(self, x, w, s, b, out, M, N, K, gs, bits, dtype, transpose, stream):
+        self.calls.append(("qmm", dict(M=M, N=N, K=K, gs=gs, bits=bits, dtype=dtype,
+                                       transpose=transpose)))
+        return 0
+
+    def mq_gather_qmm_workspace_size(self, P, M):
+        return 0
+
+    def mq_gather_qmm(self, x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, gs, bits, dtype,
+                      sorted_, ws, wsb, stream):
+        read = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
+                                               shape=(P,)).copy()
+        self.calls.append(("gather", dict(P=P, B=B, M=M, N=N, K=K, E=E, lhs=read(lhs),
+                                          rhs=read(rhs), sorted=sorted_)))
+        return 0
+
+    def mq_dequantize(self, w, s, b, out, N, K, gs, bits, dtype, stream):
+        self.calls.append(("deq", dict(N=N, K=K, gs=gs, bits=bits, dtype=dtype)))
+        return 0
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    f = _FakeLib()
+    monkeypatch.setattr(_lib, "lib", lambda: f)
+    monkeypatch.setattr(ops, "_require_gpu", lambda *ts: torch.device("cpu"))
+    monkeypatch.setattr(ops, "_stream_ptr", lambda t: 0)
+    return f
+
+
+def _qweights(N, K, gs=64, bits=4, E=None):
+    lead = (E,) if E else ()
+    w = torch.zeros(*lead, N, K * bits // 32, dtype=torch.int32)
+    s = torch.zeros(*lead, N, K // gs, dtype=torch.bfloat16)
+    return w, s, s.clone()
+
+
+def test_leading_dims_flatten_and_restore(fake):
+    w, s, b = _qweights(48, 512)
+    x = torch.zeros(2, 3, 512, dtype=torch.bfloat16)
+    out = mlxturbo_amd.quantized_matmul(x, w, s, b, group_size=64, bits=4)
+    assert out.shape == (2, 3, 48)
+    kind, c = fake.calls[-1]
+    assert kind == "qmm" and c == dict(M=6, N=48, K=512, gs=64, bits=4, dtype=0, transpose=1)
+
+
+def test_qmm_contract_errors(fake):
+    w, s, b = _qweights(48, 512)
+    x = torch.zeros(4, 512, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="requires biases"):
+        mlxturbo_amd.quantized_matmul(x, w, s, None)
+    with pytest.raises(NotImplementedError):
+        mlxturbo_amd.quantized_matmul(x, w, s, b, transpose=False)
+    with pytest.raises(NotImplementedError):
+        mlxturbo_amd.quantized_matmul(x, w, s, b, mode="mxfp4")
+    with pytest.raises(ValueError, match="does not match"):
+        mlxturbo_amd.quantized_matmul(x[:, :256], w, s, b)
+    with pytest.raises(ValueError, match="scales shape"):
+        mlxturbo_amd.quantized_matmul(x, w, s, b, group_size=32)
+    with pytest.raises(NotImplementedError, match="differs"):
+        mlxturbo_amd.quantized_matmul(x.half(), w, s, b)
+    assert fake.calls == []
+
+
+def test_gather_broadcasts_like_switchglu(fake):
+    # mlx-lm SwitchGLU: x (T,1,1,K) with indices (T,top_k) -> out (T,top_k,1,N)
+    T, top, E, N, K = 3, 4, 8, 32, 256
+    w, s, b = _qweights(N, K, E=E)
+    x = torch.zeros(T, 1, 1, K, dtype=torch.bfloat16)
+    idx = torch.tensor([[0, 3, 5, 1], [3, 0, 2, 4], [3, 5, 0, 7]], dtype=torch.int32)
+    out = mlxturbo_amd.gather_qmm(x, w, s, b, rhs_indices=idx)
+    assert out.shape == (T, top, 1, N)
+    kind, c = fake.calls[-1]
+    assert kind == "gather" and c["P"] == T * top and c["B"] == T and c["M"] == 1 and c["E"] == E
+    np.testing.assert_array_equal(c["rhs"], idx.reshape(-1).numpy())
+    np.testing.assert_array_equal(c["lhs"], np.repeat(np.arange(T), top))
+
+
+def test_gather_sorted_layout(fake):
+    # mlx-lm _gather_sort: x (P,1,K) sorted rows, idx (P,) -> out (P,1,N)
+    P, E, N, K = 6, 8, 32, 256
+    w, s, b = _qweights(N, K, E=E)
+    x = torch.zeros(P, 1, K, dtype=torch.bfloat16)
+    idx = torch.tensor([0, 0, 2, 5, 5, 7], dtype=torch.int64)
+    out = mlxturbo_amd.gather_qmm(x, w, s, b, rhs_indices=idx, sorted_indices=True)
+    assert out.shape == (P, 1, N)
+    _, c = fake.calls[-1]
+    np.testing.assert_array_equal(c["lhs"], np.arange(P))
+    assert c["sorted"] == 1
+
+
+def test_gather_default_indices(fake):
+    # no indices: lhs over x's batch, rhs over w's batch, broadcast together
+    E, N, K = 4, 32, 256
+    w, s, b = _qweights(N, K, E=E)
+    x = torch.zeros(E, 2, K, dtype=torch.bfloat16)
+    out = mlxturbo_amd.gather_qmm(x, w, s, b)
+    assert out.shape == (E, 2, N)
+    _, c = fake.calls[-1]
+    np.testing.assert_array_equal(c["lhs"], np.arange(E))
+    np.testing.assert_array_equal(c["rhs"], np.arange(E))
+
+
+def test_dequantize_shapes(fake):
+    w, s, b = _qweights(48, 512, bits=8)
+    out = mlxturbo_amd.dequantize(w, s, b, group_size=64, bits=8)
+    assert out.shape == (48, 512) and out.dtype == torch.bfloat16
+    assert fake.calls[-1] == ("deq", dict(N=48, K=512, gs=64, bits=8, dtype=0))

@@ -1,0 +1,356 @@
+"""GPU parity tests: HIP kernels (through the C ABI) against the CPU oracle.
+
+Contract (tolerance in oracle.check_output): dequantize bit-exact; matmul
+outputs within relL2 <= 1e-3 of round(ref) and <= 2 ulp of the fp32-
+accumulated reference over dtype-rounded dequantized weights.  Full
+BASELINE sizes are checked exactly where the oracle is cheap, and through
+a sampled column subset plus size-independent properties (row independence
+across M, sort invariance of gather) where it is not.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import mlxturbo_amd as mq
+from mlxturbo_amd import _lib
+from oracle import oracle as O
+from qmm_helpers import (act, bits16, from_dev, quantized, random_packed, to_dev, uniform_routing,
+                         zipf_routing)
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(out_t, ref, dtype="bfloat16"):
+    res = O.check_output(from_dev(out_t), ref, dtype)
+    assert res["ok"], res
+    return res
+
+
+# ---------------------------------------------------------------- dequantize
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_bit_exact(bits, gs, dtype):
+    rng = np.random.default_rng(1000 + bits * 10 + gs)
+    N, K = 67, 1024
+    w, s, b = random_packed(rng, N, K, gs, bits, dtype)
+    s_f = O.to_f32(s, dtype)
+    s_f[0] = 0.0                                     # s = 0 -> b
+    s_f[1] = -s_f[1]                                 # negative scales
+    if dtype == "bfloat16":
+        s_f[2] = 2.0 ** 110                          # plain-path scales (|s| >= 2^100)
+        s_f[3, ::2] = 2.0 ** 101
+    s = O.from_f32(s_f, dtype)
+    w[4] = 0xFFFFFFFF                                # max codes
+    got = mq.dequantize(to_dev(w), to_dev(s, dtype), to_dev(b, dtype), gs, bits)
+    torch.cuda.synchronize()
+    want = O.dequantize(w, s, b, gs, bits, dtype)
+    np.testing.assert_array_equal(bits16(got), want)
+
+
+def test_dequantize_nonfinite_scales():
+    rng = np.random.default_rng(7)
+    N, K, gs, bits = 4, 256, 64, 4
+    w, s, b = random_packed(rng, N, K, gs, bits)
+    s_f = O.to_f32(s, "bfloat16")
+    s_f[0, 0] = np.inf
+    s_f[1, 1] = np.nan
+    s = O.from_f32(s_f, "bfloat16")
+    got = from_dev(mq.dequantize(to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"), gs, bits))
+    want = O.bf16_to_f32(O.dequantize(w, s, b, gs, bits))
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    np.testing.assert_array_equal(got[fin], want[fin])
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_float32(bits):
+    rng = np.random.default_rng(11)
+    N, K, gs = 33, 512, 64
+    w = rng.integers(0, 2**32, size=(N, K * bits // 32), dtype=np.uint64).astype(np.uint32)
+    s = (rng.standard_normal((N, K // gs)) * 0.01).astype(np.float32)
+    b = (rng.standard_normal((N, K // gs)) * 0.01).astype(np.float32)
+    got = mq.dequantize(to_dev(w), torch.from_numpy(s).cuda(), torch.from_numpy(b).cuda(), gs, bits)
+    want = O.dequantize(w, s, b, gs, bits, "float32")
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def test_dequantize_golden_fixture():
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "dequant.npz"))
+    for key in sorted({k.rsplit("_", 1)[0] for k in d.files}):
+        bits, gs, dtype = int(key.split("_")[0][1:]), int(key.split("_")[1][1:]), key.split("_")[2]
+        got = mq.dequantize(to_dev(d[key + "_w"]), to_dev(d[key + "_s"], dtype),
+                            to_dev(d[key + "_b"], dtype), gs, bits)
+        np.testing.assert_array_equal(bits16(got), d[key + "_deq"])
+
+
+# ------------------------------------------------------------ skinny matmul
+
+def test_qmm_golden_fixture():
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "qmm.npz"))
+    for key in sorted({k.rsplit("_", 1)[0] for k in d.files}):
+        M, N, K, gs, bits, dt = (int(v) for v in d[key + "_meta"])
+        dtype = "bfloat16" if dt == 0 else "float16"
+        out = mq.quantized_matmul(to_dev(d[key + "_x"], dtype), to_dev(d[key + "_w"]),
+                                  to_dev(d[key + "_s"], dtype), to_dev(d[key + "_b"], dtype),
+                                  group_size=gs, bits=bits)
+        _check(out, d[key + "_ref"], dtype)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 33])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_vs_oracle_ragged(M, bits):
+    """N not a multiple of 16 and K not a multiple of the k-block."""
+    rng = np.random.default_rng(M * 10 + bits)
+    N, K, gs = 1000, 4160, 64
+    w, s, b = quantized(rng, N, K, gs, bits)
+    x = act(rng, (M, K))
+    out = mq.quantized_matmul(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                              to_dev(b, "bfloat16"), group_size=gs, bits=bits)
+    _check(out, O.quantized_matmul_ref(x, w, s, b, gs, bits))
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_qmm_group_sizes_and_dtypes(gs, dtype):
+    rng = np.random.default_rng(gs)
+    M, N, K = 6, 300, 2048
+    for bits in (4, 8):
+        w, s, b = quantized(rng, N, K, gs, bits, dtype)
+        x = act(rng, (M, K), dtype)
+        out = mq.quantized_matmul(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
+                                  group_size=gs, bits=bits)
+        _check(out, O.quantized_matmul_ref(x, w, s, b, gs, bits, dtype), dtype)
+
+
+def test_qmm_leading_dims():
+    rng = np.random.default_rng(5)
+    N, K = 256, 1024
+    w, s, b = quantized(rng, N, K)
+    x = act(rng, (2, 3, K))
+    out = mq.quantized_matmul(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                              to_dev(b, "bfloat16"))
+    assert out.shape == (2, 3, N)
+    ref = O.quantized_matmul_ref(x.reshape(6, K), w, s, b).reshape(2, 3, N)
+    _check(out, ref)
+
+
+def test_qmm_rows_bit_identical_across_widths():
+    """Each row's answer does not depend on the verify width M (the property
+    the reference's qmv_small_m test pins: bench/test_qmm_smallm.py:70-85)."""
+    rng = np.random.default_rng(6)
+    N, K = 2048, 5120
+    w, s, b = random_packed(rng, N, K)
+    x = act(rng, (16, K), scale=0.1)
+    args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    xd = to_dev(x, "bfloat16")
+    full = bits16(mq.quantized_matmul(xd, *args))
+    for M in (1, 2, 5, 9, 16):
+        part = bits16(mq.quantized_matmul(xd[:M], *args))
+        np.testing.assert_array_equal(part, full[:M])
+    for v in (0, 7, 15):
+        one = bits16(mq.quantized_matmul(xd[v:v + 1], *args))
+        np.testing.assert_array_equal(one[0], full[v])
+
+
+def test_qmm_writes_every_element():
+    """Output poisoned with NaN before the call; no element may stay NaN."""
+    rng = np.random.default_rng(8)
+    M, N, K, gs, bits = 5, 1000, 1024, 64, 4
+    w, s, b = quantized(rng, N, K, gs, bits)
+    x = act(rng, (M, K))
+    xd, wd, sd, bd = to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16")
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    rc = _lib.lib().mq_quantized_matmul(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(),
+                                        out.data_ptr(), M, N, K, gs, bits, 0, 1,
+                                        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    np.testing.assert_array_equal(bits16(out), bits16(mq.quantized_matmul(xd, wd, sd, bd)))
+
+
+def test_launch_counter_moves():
+    rng = np.random.default_rng(9)
+    w, s, b = quantized(rng, 64, 512)
+    x = act(rng, (1, 512))
+    before = mq.launch_count()
+    mq.quantized_matmul(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    assert mq.launch_count() == before + 1
+
+
+# ------------------------------------------------------ BASELINE configs 1-2
+
+@pytest.fixture(scope="module")
+def cfg2_weights():
+    """K=5120 N=17408 and the transposed down-proj shape, MLX affine 4-bit g64."""
+    out = {}
+    for seed, (K, N) in ((1, (5120, 17408)), (2, (17408, 5120))):
+        rng = np.random.default_rng(seed)
+        w, s, b = quantized(rng, N, K)
+        deq = O.bf16_to_f32(O.dequantize(w, s, b, 64, 4)).astype(np.float64)
+        out[(K, N)] = (w, s, b, deq, (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16")))
+    return out
+
+
+def test_config1_qmv_4096():
+    rng = np.random.default_rng(0)
+    K = N = 4096
+    w, s, b = quantized(rng, N, K)
+    x = act(rng, (1, K))
+    out = mq.quantized_matmul(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                              to_dev(b, "bfloat16"))
+    _check(out, O.quantized_matmul_ref(x, w, s, b))
+
+
+@pytest.mark.parametrize("shape", [(5120, 17408), (17408, 5120)])
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_config2_skinny(cfg2_weights, shape, M):
+    K, N = shape
+    w, s, b, deq, dev = cfg2_weights[shape]
+    rng = np.random.default_rng(100 + M)
+    x = act(rng, (M, K))
+    out = mq.quantized_matmul(to_dev(x, "bfloat16"), *dev)
+    ref = (O.bf16_to_f32(x).astype(np.float64) @ deq.T).astype(np.float32)
+    _check(out, ref)
+
+
+# ------------------------------------------------------ BASELINE config 5
+
+@pytest.fixture(scope="module")
+def lm_head_8bit():
+    rng = np.random.default_rng(5)
+    N, K, gs = 248320, 5120, 64
+    w = rng.integers(0, 2**32, size=(N, K // 4), dtype=np.uint64).astype(np.uint32)
+    s = O.from_f32((rng.random((N, K // gs)) * 0.002).astype(np.float32), "bfloat16")
+    b = O.from_f32((rng.random((N, K // gs)) * 0.02 - 0.25).astype(np.float32), "bfloat16")
+    return w, s, b, (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_config5_lm_head_8bit(lm_head_8bit, M):
+    """8-bit K=5120 N=248320 (1.35 GB): full-size kernel run, oracle on 3000
+    sampled output columns, and the row-independence property."""
+    w, s, b, dev = lm_head_8bit
+    N, K, gs, bits = 248320, 5120, 64, 8
+    rng = np.random.default_rng(50 + M)
+    x = act(rng, (M, K))
+    out = mq.quantized_matmul(to_dev(x, "bfloat16"), *dev, group_size=gs, bits=bits)
+    assert out.shape == (M, N) and torch.isfinite(out).all()
+    cols = np.sort(rng.choice(N, size=3000, replace=False))
+    ref = O.quantized_matmul_ref(x, w[cols], s[cols], b[cols], gs, bits)
+    _check(out[:, torch.from_numpy(cols).cuda()], ref)
+    one = bits16(mq.quantized_matmul(to_dev(x[-1:], "bfloat16"), *dev, group_size=gs, bits=bits))
+    np.testing.assert_array_equal(one[0], bits16(out)[-1])
+
+
+# ---------------------------------------------------------------- gather_qmm
+
+def test_gather_golden_fixture():
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "gather.npz"))
+    E, N, K, gs, bits = (int(v) for v in d["meta"])
+    x = to_dev(d["x"], "bfloat16")                      # (T, 1, K)
+    out = mq.gather_qmm(x[:, None], to_dev(d["w"]), to_dev(d["s"], "bfloat16"),
+                        to_dev(d["b"], "bfloat16"), rhs_indices=torch.from_numpy(d["rhs"]).cuda(),
+                        group_size=gs, bits=bits)
+    T, top = d["rhs"].shape
+    assert out.shape == (T, top, 1, N)
+    _check(out.reshape(T * top, 1, N), d["ref"])
+
+
+@pytest.fixture(scope="module")
+def moe_banks():
+    """Config 4: E=512, gate/up [512,1024,2048] and down [512,2048,512], 4-bit g64."""
+    rng = np.random.default_rng(4)
+    E = 512
+    banks = {}
+    for name, (N, K) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
+        w = rng.integers(0, 2**32, size=(E, N, K // 8), dtype=np.uint64).astype(np.uint32)
+        s = O.from_f32((rng.random((E, N, K // 64)) * 0.004).astype(np.float32), "bfloat16")
+        b = O.from_f32((rng.random((E, N, K // 64)) * 0.01 - 0.03).astype(np.float32), "bfloat16")
+        banks[name] = (w, s, b, (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16")))
+    return banks
+
+
+@pytest.mark.parametrize("routing", ["zipf", "uniform"])
+@pytest.mark.parametrize("T", [1, 4, 8])
+@pytest.mark.parametrize("proj", ["gate_up", "down"])
+def test_config4_gather(moe_banks, proj, T, routing):
+    w, s, b, dev = moe_banks[proj]
+    E, N, Kw = w.shape
+    K = Kw * 8
+    rng = np.random.default_rng(40 + T)
+    idx = (zipf_routing if routing == "zipf" else uniform_routing)(rng, T, 8, E)
+    x = act(rng, (T, 1, 1, K))
+    out = mq.gather_qmm(to_dev(x, "bfloat16"), *dev, rhs_indices=torch.from_numpy(idx).cuda())
+    assert out.shape == (T, 8, 1, N)
+    lhs = np.repeat(np.arange(T), 8)
+    ref = O.gather_qmm_ref(x.reshape(T, 1, K), w, s, b, lhs, idx.reshape(-1))
+    _check(out.reshape(T * 8, 1, N), ref)
+
+
+def test_gather_sorted_matches_unsorted(moe_banks):
+    """mlx-lm's _gather_sort path (rows sorted by expert, sorted_indices=True)
+    gives bit-identical per-pair results (fused.py:2626-2628)."""
+    w, s, b, dev = moe_banks["gate_up"]
+    E, N, Kw = w.shape
+    K = Kw * 8
+    rng = np.random.default_rng(77)
+    T = 8
+    idx = zipf_routing(rng, T, 8, E)
+    x = act(rng, (T, 1, 1, K))
+    xd = to_dev(x, "bfloat16")
+    out = bits16(mq.gather_qmm(xd, *dev, rhs_indices=torch.from_numpy(idx).cuda()))
+    flat = idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    xs = xd.reshape(T, 1, K)[torch.from_numpy(order // 8).cuda()]      # (P, 1, K)
+    out_s = bits16(mq.gather_qmm(xs, *dev, rhs_indices=torch.from_numpy(flat[order]).cuda(),
+                                 sorted_indices=True))
+    np.testing.assert_array_equal(out_s.reshape(T * 8, N), out.reshape(T * 8, N)[order])
+
+
+def test_gather_adversarial_and_invalid():
+    rng = np.random.default_rng(12)
+    E, N, K = 8, 80, 512
+    banks = [quantized(rng, N, K) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    dev = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    # 40 pairs all on one expert (more than 16 pairs -> several segments)
+    x = act(rng, (40, 1, K))
+    idx = np.full(40, 3, np.int32)
+    out = mq.gather_qmm(to_dev(x, "bfloat16"), *dev, rhs_indices=torch.from_numpy(idx).cuda())
+    _check(out, O.gather_qmm_ref(x, w, s, b, np.arange(40), idx))
+    # out-of-range experts produce zero rows, the rest are unaffected
+    idx2 = np.array([1, -1, 8, 2], np.int32)
+    x2 = act(rng, (4, 1, K))
+    out2 = from_dev(mq.gather_qmm(to_dev(x2, "bfloat16"), *dev,
+                                  rhs_indices=torch.from_numpy(idx2).cuda()))
+    assert np.all(out2[1] == 0) and np.all(out2[2] == 0)
+    ok = np.array([0, 3])
+    ref = O.gather_qmm_ref(x2, w, s, b, ok, idx2[ok])
+    assert O.check_output(out2[ok], ref)["ok"]
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_gather_large_batch_prep_path(M):
+    """P > 256 pairs: segment tables built by the counting-sort prep kernel."""
+    rng = np.random.default_rng(13)
+    E, N, K, T, top = 16, 48, 256, 80, 4
+    banks = [quantized(rng, N, K) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    idx = zipf_routing(rng, T, top, E)
+    x = act(rng, (T, 1, M, K))
+    out = mq.gather_qmm(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                        to_dev(b, "bfloat16"), rhs_indices=torch.from_numpy(idx).cuda())
+    assert out.shape == (T, top, M, N)
+    ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, np.repeat(np.arange(T), top), idx.reshape(-1))
+    _check(out.reshape(T * top, M, N), ref)
