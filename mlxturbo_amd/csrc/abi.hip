@@ -187,7 +187,8 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
     return fail(MQ_EUNSUPPORTED, "gather_qmm supports M <= 16 rows per pair");
   if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
   if (P == 0 || M == 0 || N == 0) return MQ_OK;
-  if (workspace_bytes < mq::gather_workspace_bytes(P, M) || !workspace)
+  const size_t ws_need = mq::gather_workspace_bytes(P, M);
+  if (ws_need && (workspace_bytes < ws_need || !workspace))
     return fail(MQ_EINVAL, "workspace too small: need %zu bytes",
                 mq::gather_workspace_bytes(P, M));
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);

@@ -53,6 +53,7 @@ __global__ __launch_bounds__(256) void dequantize32_kernel(const uint32_t* __res
                                                            const float* __restrict__ b,
                                                            float* __restrict__ out, int64_t N,
                                                            int64_t K) {
+#pragma clang fp contract(off)
   constexpr int PER = 32 / BITS;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   const int64_t Kw = K * BITS / 32;
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(256) void dequantize32_kernel(const uint32_t* __res
     const float bf = b[n * G + k0 / GS];
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-      out[n * K + k0 + j] = __fadd_rn(__fmul_rn(sf, (float)((word >> (BITS * j)) & MASK)), bf);
+      out[n * K + k0 + j] = sf * (float)((word >> (BITS * j)) & MASK) + bf;
   }
 }
 

@@ -7,9 +7,9 @@
 //   deq     T(float(s)*q + float(b)), rounded to nearest even
 //
 // Exact dequantization trick used by every kernel here:
-//   A 4-bit code masked in place inside a 16-bit lane of a register, e.g.
-//   (w & 0x00F000F0) keeps code 1 at bits 4..7 of the low half, is the IEEE
-//   half subnormal (q << 4) * 2^-24 = q * 2^-20.  v_fma_mix_f32 converts the
+//   A code masked in place inside the mantissa bits (0..9) of a 16-bit lane
+//   of a register, e.g. (w & 0x00F000F0) keeps code 1 at bits 4..7 of the
+//   low half, is the IEEE half subnormal (q << 4) * 2^-24 = q * 2^-20.  v_fma_mix_f32 converts the
 //   half to float exactly (fp16 denormals are preserved in the kernel's mode
 //   register) and computes fma(q*2^-20, s*2^20, b) with one rounding, which
 //   equals float(s*q + b) because s*2^20 is exact whenever |s| < 2^100.
@@ -84,7 +84,7 @@ __device__ __forceinline__ float half_hi(uint32_t v) { return (float)bitcast<f16
 
 // Per-group dequant parameters for the fast path.
 struct GroupScale {
-  float s24, s20, s16;  // s * 2^24, s * 2^20, s * 2^16
+  float s24, s20;  // s * 2^24, s * 2^20
   float s, b;
 };
 
@@ -92,7 +92,6 @@ __device__ __forceinline__ GroupScale make_group(float s, float b) {
   GroupScale g;
   g.s24 = s * 16777216.0f;
   g.s20 = s * 1048576.0f;
-  g.s16 = s * 65536.0f;
   g.s = s;
   g.b = b;
   return g;
@@ -102,20 +101,23 @@ __device__ __forceinline__ GroupScale make_group(float s, float b) {
 __device__ __forceinline__ bool needs_plain(float s) { return __builtin_fabsf(s) >= 0x1p100f; }
 
 // 4-bit: one word (codes k0..k7) -> four packed T pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7).
+// Only bits 0..9 of a half are mantissa, so a code may sit at bits 0..3 or
+// 4..7 of each 16-bit lane; the upper byte of each lane is shifted down first.
 template <int DT>
 __device__ __forceinline__ void deq4_word(uint32_t w, const GroupScale& g, uint32_t o[4]) {
+  const uint32_t t = w >> 8;
   const uint32_t h0 = w & 0x000F000Fu;          // k0, k4  (x 2^-24)
   const uint32_t h1 = w & 0x00F000F0u;          // k1, k5  (x 2^-20)
-  const uint32_t h2 = w & 0x0F000F00u;          // k2, k6  (x 2^-16)
-  const uint32_t h3 = (w >> 4) & 0x0F000F00u;   // k3, k7  (x 2^-16)
+  const uint32_t h2 = t & 0x000F000Fu;          // k2, k6  (x 2^-24)
+  const uint32_t h3 = t & 0x00F000F0u;          // k3, k7  (x 2^-20)
   const float v0 = __builtin_fmaf(half_lo(h0), g.s24, g.b);
   const float v4 = __builtin_fmaf(half_hi(h0), g.s24, g.b);
   const float v1 = __builtin_fmaf(half_lo(h1), g.s20, g.b);
   const float v5 = __builtin_fmaf(half_hi(h1), g.s20, g.b);
-  const float v2 = __builtin_fmaf(half_lo(h2), g.s16, g.b);
-  const float v6 = __builtin_fmaf(half_hi(h2), g.s16, g.b);
-  const float v3 = __builtin_fmaf(half_lo(h3), g.s16, g.b);
-  const float v7 = __builtin_fmaf(half_hi(h3), g.s16, g.b);
+  const float v2 = __builtin_fmaf(half_lo(h2), g.s24, g.b);
+  const float v6 = __builtin_fmaf(half_hi(h2), g.s24, g.b);
+  const float v3 = __builtin_fmaf(half_lo(h3), g.s20, g.b);
+  const float v7 = __builtin_fmaf(half_hi(h3), g.s20, g.b);
   o[0] = T16<DT>::pack2(v0, v1);
   o[1] = T16<DT>::pack2(v2, v3);
   o[2] = T16<DT>::pack2(v4, v5);
