@@ -1,26 +1,25 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
 Metric: 4-bit qmv/qmm achieved HBM GB/s (% of peak) and
-µs/call at K=5120 N=17408 (configs[1]; configs[0] is the reference's
-CPU-runnable case).  One *step* is one quantized_matmul call at M=1 over
-one of R rotated copies of the 4-bit weights (R copies exceed the 256 MB
-Infinity Cache, so every step streams its weights from HBM, the reference's
-own "cold chain" rule).  The K timed steps are one HIP graph replay,
-bracketed by torch.cuda.synchronize(), so host launch overhead is out of
-the measurement; inputs are resident in HBM before the timed region.
+µs/call at K=5120 N=17408.  The headline workload is configs[1] at M=1 (the
+decode qmv): one *step* is one quantized_matmul call over one of R rotated
+copies of the 4-bit weights (R copies exceed the 256 MB Infinity Cache, so
+every step streams its weights from HBM -- the reference's own "cold chain"
+rule, CLAUDE.md:13-16).  Inputs are resident in HBM before timing starts.
 
-Printed JSON line (rank 0 only; one GPU):
-  value      whole-job algorithmic GB/s over the timed region
-  roofline   the dominant kernel's algorithmic bytes per launch over its
-             average launch duration, from HIP events recorded on the
-             launching stream around each launch in an eager pass that
-             mirrors the timed steps; peak = 8000 GB/s (MI355X HBM3E)
-  cpu_baseline  the C oracle (oracle/qmm_oracle.c, OpenMP) timed on this
-             host's cores over a bounded sample of the same workload
-  sweep      µs/call and GB/s for M = 1, 2, 4, 8, 16 on both config-2 shapes
+Timing: the K timed steps are captured in one HIP graph on a dedicated
+stream; HIP events recorded on that same stream bracket one replay, with
+torch.cuda.synchronize() on both sides.  One step is exactly one kernel
+launch, so ``ms_per_step`` is also the dominant kernel's average launch
+duration, the denominator of ``roofline.achieved``.
 
-Algorithmic bytes per call (M rows): packed weights N*K/2 + scales and
-biases 2*2*N*K/64 + x 2*M*K + out 2*M*N.
+Algorithmic bytes per call (M rows, K, N, b bits, group 64, 16-bit T):
+packed weights N*K*b/8 + scales and biases 2*2*N*K/64 + x 2*M*K + out 2*M*N.
+
+``sweep`` reports the same measurement for configs 1, 2 (both shapes,
+M = 1..16) and 5 (8-bit lm_head); ``cpu_baseline`` times the C restatement
+of the oracle (oracle/qmm_oracle.c, OpenMP) on this host's cores over a
+bounded sample of the headline workload.
 """
 
 from __future__ import annotations
@@ -35,6 +34,7 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "4-bit qmv/qmm achieved HBM GB/s (% peak) + µs/call, M=1..16, K=5120 N=17408"
+MALL_BYTES = 256 << 20
 
 
 def algo_bytes(M: int, N: int, K: int, bits: int = 4, gs: int = 64) -> int:
@@ -46,105 +46,96 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--copies", type=int, default=8, help="rotated weight copies (>256 MB total)")
+    p.add_argument("--copies", type=int, default=0,
+                   help="rotated weight copies (default: enough to exceed 2x the 256 MB MALL)")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     return p.parse_args()
 
 
-def make_weights(torch, N, K, copies, seed=1, bits=4, gs=64):
-    """R distinct random 4-bit weight copies on the GPU (synthetic, seeded).
+def copies_for(nbytes: int, requested: int = 0) -> int:
+    if requested:
+        return requested
+    return max(2, -(-2 * MALL_BYTES // nbytes))
 
-    Codes are uniform random words; scales/biases are small bf16 values.  The
-    kernel's work does not depend on the values, and the parity tests cover
-    MLX-quantized N(0, 0.02) weights of the same shape.
+
+def make_weights(torch, N, K, copies, seed=1, bits=4, gs=64):
+    """`copies` distinct random weight sets on the GPU (synthetic, seeded).
+
+    Codes are uniform random words; scales/biases are small bf16 values, the
+    magnitudes MLX's quantizer produces for N(0, 0.02) weights.  The kernel's
+    work does not depend on the values; the parity tests cover MLX-quantized
+    N(0, 0.02) weights of the same shapes.
     """
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     out = []
     for _ in range(copies):
-        w = torch.randint(-2**31, 2**31 - 1, (N, K * bits // 32), dtype=torch.int32, device="cuda",
-                          generator=g).view(torch.uint32)
+        w = torch.randint(-2**31, 2**31 - 1, (N, K * bits // 32), dtype=torch.int32,
+                          device="cuda", generator=g).view(torch.uint32)
         s = (torch.rand((N, K // gs), device="cuda", generator=g) * 0.002).to(torch.bfloat16)
         b = (torch.rand((N, K // gs), device="cuda", generator=g) * 0.02 - 0.01).to(torch.bfloat16)
         out.append((w, s, b))
     return out
 
 
-def time_graph(torch, mq, xs, ws, steps, warmup):
-    """Warmup eagerly, then capture `steps` calls (rotating weights) in one graph."""
-    R = len(ws)
+def time_graph(torch, fn, steps, warmup):
+    """Warm up eagerly, capture `steps` calls in one graph, time one replay.
+
+    Returns (elapsed seconds of the replay, per-step seconds).  Events are
+    recorded on the capture stream, the stream every launch in the graph runs
+    on.
+    """
     for i in range(warmup):
-        mq.quantized_matmul(xs[i % len(xs)], *ws[i % R])
+        fn(i)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
-    outs = []
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
             for i in range(steps):
-                outs.append(mq.quantized_matmul(xs[i % len(xs)], *ws[i % R]))
+                fn(i)
     torch.cuda.synchronize()
-    graph.replay()                       # untimed replay: graph upload / first-touch
+    with torch.cuda.stream(stream):
+        graph.replay()                      # untimed replay: upload, first touch
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    graph.replay()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    return (t1 - t0), graph, outs
-
-
-_SLEEP_CYCLES_PER_S = None
-
-
-def _sleep_rate(torch):
-    """Calibrate torch.cuda._sleep (a bounded spin kernel): cycles per second."""
-    global _SLEEP_CYCLES_PER_S
-    if _SLEEP_CYCLES_PER_S is None:
-        torch.cuda.synchronize()
-        torch.cuda._sleep(1_000_000)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        torch.cuda._sleep(10_000_000)
-        torch.cuda.synchronize()
-        _SLEEP_CYCLES_PER_S = 10_000_000 / max(time.perf_counter() - t0, 1e-6)
-    return _SLEEP_CYCLES_PER_S
-
-
-def time_events(torch, mq, xs, ws, launches):
-    """Per-launch durations from HIP events on the launching stream.
-
-    A bounded GPU sleep sized to three times the host's enqueue time is
-    queued first, so every launch and event is enqueued while the GPU is
-    still busy; the launches then run back to back and each event pair
-    brackets exactly one kernel.
-    """
-    R = len(ws)
-    st = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(launches + 1)]
-    # host enqueue cost per launch (measured, GPU idle afterwards is fine here)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(min(launches, 50)):
-        mq.quantized_matmul(xs[i % len(xs)], *ws[i % R])
-    per_launch = (time.perf_counter() - t0) / min(launches, 50)
-    torch.cuda.synchronize()
-    cycles = int(_sleep_rate(torch) * max(3 * per_launch * launches, 0.005))
-    torch.cuda._sleep(min(cycles, 2_000_000_000))
-    ev[0].record(st)
-    for i in range(launches):
-        mq.quantized_matmul(xs[i % len(xs)], *ws[i % R])
-        ev[i + 1].record(st)
-    torch.cuda.synchronize()
-    d = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(launches)]) * 1e3   # us
-    return d
+    elapsed = e0.elapsed_time(e1) * 1e-3
+    del graph
+    return elapsed, elapsed / steps
+
+
+def measure_qmm(torch, mq, M, N, K, bits, steps, warmup, copies=0, seed=1):
+    per = algo_bytes(M, N, K, bits)
+    R = copies_for(N * K * bits // 8, copies)
+    ws = make_weights(torch, N, K, R, seed=seed, bits=bits)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 100)
+    xs = [torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16) for _ in range(2)]
+
+    def fn(i):
+        w, s, b = ws[i % R]
+        mq.quantized_matmul(xs[i % 2], w, s, b, group_size=64, bits=bits)
+
+    elapsed, per_step = time_graph(torch, fn, steps, warmup)
+    del ws
+    torch.cuda.empty_cache()
+    return {"us": per_step * 1e6, "GBps": per / per_step / 1e9, "bytes": per, "copies": R,
+            "elapsed": elapsed}
 
 
 def cpu_baseline(N, K, seconds):
-    """The C oracle (same arithmetic as the oracle: bf16-exact dequant, fp32
-    accumulation) on this host's cores, bounded to ~`seconds`."""
+    """The C restatement of the oracle (bf16-exact dequant, fp32 accumulation,
+    OpenMP) on this host's cores, bounded to about `seconds`."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import cref
     threads = min(len(os.sched_getaffinity(0)), 16)
@@ -175,51 +166,37 @@ def cpu_baseline(N, K, seconds):
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{reps} full M=1 calls K={K} N={N} (C oracle, OpenMP {threads} threads, "
-                   f"{per * 1e3:.1f} ms/call) on {cpu_model or 'host CPU'}; MLX CPU "
-                   "quantized_matmul is not installable here"),
+        "sample": (f"{reps} full M=1 calls K={K} N={N} (C oracle oracle/qmm_oracle.c, OpenMP "
+                   f"{threads} threads, {per * 1e3:.1f} ms/call) on {cpu_model or 'host CPU'}; "
+                   "MLX's CPU quantized_matmul is not installable here"),
     }
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding of "
-                          "the quantized matmul is designed (N-split, no exchange) but not built",
+        print(json.dumps({"error": "this build measures one GPU only: the quantized matmul "
+                          "shards along N without exchange, and no multi-GPU path is built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     import mlxturbo_amd as mq
 
     K, N = 5120, 17408
-    ws = make_weights(torch, N, K, args.copies)
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0)
-    xs = [torch.randn((1, K), device="cuda", generator=g).to(torch.bfloat16) for _ in range(4)]
-    bytes_call = algo_bytes(1, N, K)
-
-    elapsed, graph, _ = time_graph(torch, mq, xs, ws, args.steps, args.warmup)
-    ms_per_step = elapsed * 1e3 / args.steps
-    value = bytes_call * args.steps / elapsed / 1e9
-
-    d = time_events(torch, mq, xs, ws, min(args.steps, 400))
-    avg_us = float(np.mean(d))
-    achieved = bytes_call / (avg_us * 1e-6) / 1e9
+    head = measure_qmm(torch, mq, 1, N, K, 4, args.steps, args.warmup, args.copies)
+    value = head["GBps"]
+    ms_per_step = head["us"] * 1e-3
 
     sweep = {}
     if not args.no_sweep:
-        for (KK, NN) in ((5120, 17408), (17408, 5120)):
-            wsw = ws if (KK, NN) == (K, N) else make_weights(torch, NN, KK, args.copies, seed=2)
-            for M in (1, 2, 4, 8, 16):
-                xm = [torch.randn((M, KK), device="cuda", generator=g).to(torch.bfloat16)]
-                dd = time_events(torch, mq, xm, wsw, 100)
-                us = float(np.median(dd))
-                sweep[f"K{KK}_N{NN}_M{M}"] = {
-                    "us": round(us, 2),
-                    "GBps": round(algo_bytes(M, NN, KK) / (us * 1e-6) / 1e9, 1),
-                }
-            del wsw
-            torch.cuda.empty_cache()
+        for (KK, NN, bits, Ms) in ((4096, 4096, 4, (1,)), (5120, 17408, 4, (2, 4, 8, 16)),
+                                   (17408, 5120, 4, (1, 2, 4, 8, 16)),
+                                   (5120, 248320, 8, (1, 2, 4))):
+            for M in Ms:
+                r = measure_qmm(torch, mq, M, NN, KK, bits, min(args.steps, 100), 5)
+                sweep[f"b{bits}_K{KK}_N{NN}_M{M}"] = {
+                    "us": round(r["us"], 2), "GBps": round(r["GBps"], 1),
+                    "pct_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}
 
     cpu = None if args.no_cpu else cpu_baseline(N, K, args.cpu_seconds)
 
@@ -237,24 +214,24 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": (f"config2 qmv: M=1 x K={K} -> N={N}, MLX affine 4-bit g64, bf16 "
-                         f"scales/biases/activations, {args.copies} rotated weight copies "
-                         f"({args.copies * bytes_call / 1e6:.0f} MB > 256 MB MALL), "
-                         "one HIP graph of `steps` launches"),
+            "workload": (f"configs[1] decode qmv: M=1 x K={K} -> N={N}, MLX affine 4-bit g64, "
+                         f"bf16 scales/biases/activations, {head['copies']} rotated weight copies "
+                         f"({head['copies'] * N * K // 2 / 1e6:.0f} MB > 256 MB MALL), one HIP graph "
+                         "of `steps` launches"),
             "M": 1, "K": K, "N": N, "bits": 4, "group_size": 64,
-            "bytes_per_call": bytes_call,
+            "bytes_per_call": head["bytes"],
             "pct_peak": round(100 * value / HBM_PEAK_GBS, 1),
-            "us_per_call": round(ms_per_step * 1e3, 3),
+            "us_per_call": round(head["us"], 3),
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": round(value, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "qmm_skinny_kernel<bf16,4,64>",
-            "avg_launch_us": round(avg_us, 3),
+            "kernel": "mq::qmv_kernel<bf16,4,64,...>",
+            "avg_launch_us": round(head["us"], 3),
         },
         "cpu_baseline": cpu,
         "sweep": sweep,
