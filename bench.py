@@ -33,6 +33,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "4-bit qmv/qmm achieved HBM GB/s (% peak) + µs/call, M=1..16, K=5120 N=17408"
 MALL_BYTES = 256 << 20
 
@@ -197,6 +198,14 @@ def main():
                 sweep[f"b{bits}_K{KK}_N{NN}_M{M}"] = {
                     "us": round(r["us"], 2), "GBps": round(r["GBps"], 1),
                     "pct_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}
+
+        # config 3: prefill widths on the MFMA tile kernel (compute-bound)
+        for M in (512, 2048, 8192):
+            r = measure_qmm(torch, mq, M, N, K, 4, 20, 3, copies=2)
+            tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
+            sweep[f"b4_K{K}_N{N}_M{M}"] = {
+                "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
+                "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
 
     cpu = None if args.no_cpu else cpu_baseline(N, K, args.cpu_seconds)
 

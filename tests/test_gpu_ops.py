@@ -221,6 +221,38 @@ def test_config2_skinny(cfg2_weights, shape, M):
     _check(out, ref)
 
 
+# ------------------------------------------------- BASELINE config 3 (wide)
+
+@pytest.mark.parametrize("M", [512, 2048, 8192])
+def test_config3_wide(cfg2_weights, M):
+    """Prefill widths through the MFMA tile kernel, full size; the oracle checks
+    64 sampled rows x 512 sampled columns."""
+    K, N = 5120, 17408
+    w, s, b, deq, dev = cfg2_weights[(K, N)]
+    rng = np.random.default_rng(300 + M)
+    x = act(rng, (M, K))
+    out = mq.quantized_matmul(to_dev(x, "bfloat16"), *dev)
+    assert out.shape == (M, N) and torch.isfinite(out).all()
+    rows = np.sort(rng.choice(M, size=64, replace=False))
+    cols = np.sort(rng.choice(N, size=512, replace=False))
+    ref = (O.bf16_to_f32(x[rows]).astype(np.float64) @ deq[cols].T).astype(np.float32)
+    got = out[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()]
+    _check(got, ref)
+
+
+@pytest.mark.parametrize("bits,gs,dtype", [(4, 64, "bfloat16"), (8, 64, "bfloat16"),
+                                           (4, 32, "float16"), (8, 128, "bfloat16")])
+def test_wide_ragged(bits, gs, dtype):
+    """M and N not multiples of the 256 x 128 tile, full oracle."""
+    rng = np.random.default_rng(31 + bits + gs)
+    M, N, K = 300, 200, 1024
+    w, s, b = quantized(rng, N, K, gs, bits, dtype)
+    x = act(rng, (M, K), dtype)
+    out = mq.quantized_matmul(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
+                              group_size=gs, bits=bits)
+    _check(out, O.quantized_matmul_ref(x, w, s, b, gs, bits, dtype), dtype)
+
+
 # ------------------------------------------------------ BASELINE config 5
 
 @pytest.fixture(scope="module")
