@@ -52,6 +52,8 @@ def parse():
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--copy-probe", type=int, default=0,
+                   help="run a plain copy of this many bytes first (counter calibration)")
     return p.parse_args()
 
 
@@ -134,6 +136,86 @@ def measure_qmm(torch, mq, M, N, K, bits, steps, warmup, copies=0, seed=1):
             "elapsed": elapsed}
 
 
+def recorded_traffic():
+    """HBM bytes per launch of the headline kernel from the committed counter
+    passes (profiles/qmv_b4_K5120_N17408_M1_traffic.md), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "qmv_b4_K5120_N17408_M1_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def zipf_routing(rng, T, top_k, E, s=1.1):
+    """top_k distinct experts per token drawn from Zipf(s) over E (rank -> id
+    through a fixed seeded permutation), as BASELINE configs[3] specifies."""
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    perm = np.random.default_rng(12345).permutation(E)
+    return np.stack([perm[rng.choice(E, size=top_k, replace=False, p=p)]
+                     for _ in range(T)]).astype(np.int32)
+
+
+def measure_gather(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, nroute=64, seed=4):
+    """gather_qmm over an E-expert 4-bit bank for T tokens x top_k
+    experts; `nroute` seeded routings rotate so weights stream from HBM.
+    Algorithmic bytes count each distinct expert's weights once per call."""
+    rng = np.random.default_rng(seed + T)
+    routes = [(zipf_routing(rng, T, top_k, E) if routing == "zipf" else
+               np.stack([rng.choice(E, size=top_k, replace=False) for _ in range(T)]).astype(np.int32))
+              for _ in range(nroute)]
+    (w, s, b), = make_weights(torch, E * N, K, 1, seed=seed)
+    w, s, b = w.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((T, 1, 1, K), device="cuda", generator=g).to(torch.bfloat16)
+    idx = [torch.from_numpy(r).cuda() for r in routes]
+    per_expert = N * K // 2 + 4 * N * (K // 64)
+    nbytes = [len(np.unique(r)) * per_expert + 2 * T * K + 2 * T * top_k * N for r in routes]
+
+    def fn(i):
+        mq.gather_qmm(x, w, s, b, rhs_indices=idx[i % nroute])
+
+    elapsed, per_step = time_graph(torch, fn, steps, warmup)
+    avg_bytes = sum(nbytes[i % nroute] for i in range(steps)) / steps
+    uniq = sum(len(np.unique(r)) for r in routes) / nroute
+    del w, s, b
+    torch.cuda.empty_cache()
+    return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
+            "distinct_experts": round(uniq, 1)}
+
+
+def measure_dequant(torch, mq, N, K, steps, warmup):
+    R = copies_for(N * K // 2)
+    ws = make_weights(torch, N, K, R, seed=7)
+    per = N * K // 2 + 4 * N * (K // 64) + 2 * N * K
+
+    def fn(i):
+        w, s, b = ws[i % R]
+        mq.dequantize(w, s, b, group_size=64, bits=4)
+
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    del ws
+    torch.cuda.empty_cache()
+    return {"us": round(per_step * 1e6, 2), "GBps": round(per / per_step / 1e9, 1)}
+
+
+def copy_probe(torch, nbytes, reps=4):
+    """A plain device copy of known size, for calibrating rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters against the bytes actually moved."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def cpu_baseline(N, K, seconds):
     """The C restatement of the oracle (bf16-exact dequant, fp32 accumulation,
     OpenMP) on this host's cores, bounded to about `seconds`."""
@@ -183,6 +265,8 @@ def main():
     import torch
     import mlxturbo_amd as mq
 
+    if args.copy_probe:
+        copy_probe(torch, args.copy_probe)
     K, N = 5120, 17408
     head = measure_qmm(torch, mq, 1, N, K, 4, args.steps, args.warmup, args.copies)
     value = head["GBps"]
@@ -206,6 +290,14 @@ def main():
             sweep[f"b4_K{K}_N{N}_M{M}"] = {
                 "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
                 "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+        # config 4: MoE gather at decode/verify widths (gate/up and down banks)
+        for routing in ("zipf", "uniform"):
+            for T in (1, 4, 8):
+                for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
+                    sweep[f"gather_{name}_{routing}_T{T}"] = measure_gather(
+                        torch, mq, T, NN, KK, routing, 100, 5)
+        sweep["dequant_b4_K5120_N17408"] = measure_dequant(torch, mq, N, K, 50, 3)
 
     cpu = None if args.no_cpu else cpu_baseline(N, K, args.cpu_seconds)
 
@@ -238,7 +330,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(),
             "kernel": "mq::qmv_kernel<bf16,4,64,...>",
             "avg_launch_us": round(head["us"], 3),
         },
