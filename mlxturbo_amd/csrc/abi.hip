@@ -9,7 +9,6 @@
 #include "../../include/mlxturbo_amd.h"
 #include "dequant.cuh"
 #include "gather.cuh"
-#include "qmm_skinny.cuh"
 #include "qmv.cuh"
 #include "qmm_wide.cuh"
 
@@ -89,24 +88,11 @@ struct DequantLaunch {
   }
 };
 
-// Launch geometry of the skinny kernel for one (bits, group_size): groups per
-// lane per step, waves per workgroup, pipeline stages.  Fixed per format (not
-// per M), so every output row is computed in the same order for every M.
-template <int BITS, int GS>
-struct QmvConf {
-  static constexpr int GPL = (BITS == 4 && GS == 32) ? 4 : (BITS == 8 && GS >= 64) ? 1 : 2;
-  static constexpr int NW = 4;
-  static constexpr int PF = 2;
-};
-
-// Largest x copy (M rows) kept in LDS; beyond it fragments are read from global memory.
-constexpr size_t kQmvMaxXLds = 64 * 1024;
-
 template <int DT, int BITS, int GS>
 struct SkinnyLaunch {
   static void run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
                   int64_t M, int64_t N, int64_t K, hipStream_t st) {
-    using C = QmvConf<BITS, GS>;
+    using C = mq::QmvConf<BITS, GS>;
     using Gm = mq::QmvGeom<BITS, GS, C::GPL>;
     const unsigned grid = (unsigned)((N + 15) / 16);
     for (int64_t m0 = 0; m0 < M; m0 += 16) {
@@ -114,7 +100,7 @@ struct SkinnyLaunch {
       const size_t lds = (size_t)mt * mq::qmv_x_stride((int)K, Gm::STEPK);
       const uint16_t* xp = (const uint16_t*)x + m0 * K;
       uint16_t* op = (uint16_t*)out + m0 * N;
-      if (lds <= kQmvMaxXLds) {
+      if (lds <= mq::kQmvMaxXLds) {
         hipLaunchKernelGGL((mq::qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, true>), dim3(grid),
                            dim3(64 * C::NW), lds, st, xp, w, (const uint16_t*)s,
                            (const uint16_t*)b, op, mt, (int)N, (int)K, (int64_t)K, (int64_t)N);

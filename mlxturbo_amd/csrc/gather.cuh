@@ -9,11 +9,12 @@
 // experts).
 //
 // CDNA4 design: pairs that use the same expert become the rows of the MFMA
-// A operand.  A "segment" is up to R = 16/M pairs sharing one expert; each
-// workgroup owns (segment, 16-column tile) and runs the skinny MFMA loop of
-// qmm_skinny.cuh over that expert's rows, so every expert's weights stream
-// from HBM once per call no matter how many tokens routed to it, and the
-// dequantization work scales with distinct experts, not with pairs.
+// A operand.  A "segment" is up to R pairs sharing one expert (R * M <= 16 A
+// rows, fewer when their x rows would not fit in LDS); each workgroup owns
+// (segment, 16-row weight tile) and runs the streaming tile of qmv.cuh over
+// that expert's rows, so every expert's weights stream from HBM once per call
+// no matter how many tokens routed to it, and dequantization work scales with
+// distinct experts, not with pairs.
 //
 // Segment discovery needs no host sync and no extra launch for P <= 256:
 // every workgroup ranks the pairs itself in LDS (pair p leads a segment when
@@ -22,7 +23,7 @@
 // one-workgroup counting-sort prep kernel into the caller's workspace first.
 // Pairs with an out-of-range expert or x index produce zero rows.
 #pragma once
-#include "qmm_skinny.cuh"
+#include "qmv.cuh"
 
 namespace mq {
 
@@ -38,8 +39,9 @@ inline size_t gather_workspace_bytes(int64_t P, int64_t M) {
   return (gather_ws_words(P) * 4 + 255) & ~(size_t)255;
 }
 
-__global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __restrict__ rhs, int P,
-                                                           int E, int R,
+__global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __restrict__ rhs,
+                                                           const int32_t* __restrict__ lhs, int P,
+                                                           int E, int B, int R,
                                                            int32_t* __restrict__ ws) {
   extern __shared__ int sh[];
   const int NE = E + 1;  // bucket E collects out-of-range experts
@@ -55,11 +57,12 @@ __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __rest
     cur[e] = 0;
   }
   __syncthreads();
-  for (int p = t; p < P; p += nt) {
-    int e = rhs[p];
-    e = (e >= 0 && e < E) ? e : E;
-    atomicAdd(&cnt[e], 1);
-  }
+  auto key_of = [&](int p) {
+    const int e = rhs[p];
+    const int xb = lhs ? lhs[p] : p;
+    return (e >= 0 && e < E && xb >= 0 && xb < B) ? e : E;
+  };
+  for (int p = t; p < P; p += nt) atomicAdd(&cnt[key_of(p)], 1);
   __syncthreads();
   // exclusive scans of cnt and ceil(cnt/R): chunk per thread, then Hillis-Steele.
   const int per = (NE + nt - 1) / nt;
@@ -99,8 +102,7 @@ __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __rest
   int32_t* seg_len = seg_start + P;
   int32_t* seg_exp = seg_len + P;
   for (int p = t; p < P; p += nt) {
-    int e = rhs[p];
-    e = (e >= 0 && e < E) ? e : E;
+    const int e = key_of(p);
     perm[base[e] + atomicAdd(&cur[e], 1)] = p;
   }
   for (int e = t; e < NE; e += nt) {
@@ -114,45 +116,99 @@ __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __rest
   }
 }
 
-template <int DT, int BITS, int GS>
-__global__ __launch_bounds__(256) void gather_skinny_kernel(
+// A rows of a gather segment: pair members[j] contributes rows j*Mi .. j*Mi+Mi-1.
+struct GatherRows {
+  const uint16_t* x;
+  uint16_t* out;
+  const int* members;      // LDS
+  const int* xbase;        // LDS: x batch index of each member
+  int Mi, K, N, n0;
+  __device__ __forceinline__ const uint16_t* xrow(int m) const {
+    const int j = m / Mi;
+    return x + ((int64_t)xbase[j] * Mi + (m - j * Mi)) * K;
+  }
+  __device__ __forceinline__ void store(int m, int nn, uint16_t v) const {
+    const int j = m / Mi;
+    out[((int64_t)members[j] * Mi + (m - j * Mi)) * N + n0 + nn] = v;
+  }
+};
+
+// grid = (segments upper bound, ceil(N / (16 * tpw))); block 64 * NW.  Each
+// workgroup runs tpw consecutive 16-row tiles of its expert, reusing the
+// segment and the LDS copy of its x rows.
+// Segment = up to R pairs that share an expert (R * Mi <= 16 A rows).
+// Pairs whose expert or x index is out of range form their own segments and
+// get zero outputs.  Dynamic LDS: XLDS ? R * Mi * qmv_x_stride(K, STEPK) : 0.
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, bool XLDS>
+__global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ ws, int P, int B, int M, int N, int K, int E) {
-  __shared__ int s_rhs[kGatherFusedMaxP];
+    const int32_t* __restrict__ ws, int P, int B, int Mi, int N, int K, int E, int R, int tpw) {
+  extern __shared__ __align__(16) unsigned char qmv_smem[];
+  __shared__ f32x4 red[NW][64];
+  __shared__ int s_key[kGatherFusedMaxP];
   __shared__ int s_cb[kGatherFusedMaxP];
   __shared__ int s_members[16];
+  __shared__ int s_xbase[16];
   __shared__ int s_expert;
   __shared__ int s_found;
   const int t = threadIdx.x;
   const int nt = blockDim.x;
-  const int R = 16 / M;
   const int seg = blockIdx.x;
+  // key of a pair: its expert, or E when the expert or the x index is invalid
+  auto key_of = [&](int p) {
+    const int e = rhs[p];
+    const int xb = lhs ? lhs[p] : p;
+    return (e >= 0 && e < E && xb >= 0 && xb < B) ? e : E;
+  };
 
-  if (t < 16) s_members[t] = -1;
-  if (t == 0) s_found = 0;
-  if (ws == nullptr) {
-    // In-workgroup segment discovery (P <= kGatherFusedMaxP).
-    for (int p = t; p < P; p += nt) {
-      const int e = rhs[p];
-      s_rhs[p] = (e >= 0 && e < E) ? e : E;
+  if (ws == nullptr && P <= 64) {
+    // Wave-level discovery (every wave computes the same answer; no barrier):
+    // lane p holds pair p's key and cb = number of earlier pairs with that key.
+    const int lane = t & 63;
+    const int key = lane < P ? key_of(lane) : -1;
+    int cb = 0;
+    for (int q = 0; q < P; ++q) {
+      const int kq = __builtin_amdgcn_readlane(key, q);
+      cb += (q < lane && kq == key) ? 1 : 0;
     }
+    const bool lead = lane < P && (cb % R) == 0;
+    const uint64_t lmask = __builtin_amdgcn_ballot_w64(lead);
+    const int rank = __builtin_popcountll(lmask & ((1ull << lane) - 1ull));
+    const uint64_t mine = __builtin_amdgcn_ballot_w64(lead && rank == seg);
+    if (mine == 0) return;                            // identical in every wave
+    const int leader = __builtin_ctzll(mine);
+    const int e = __builtin_amdgcn_readlane(key, leader);
+    const int cb0 = __builtin_amdgcn_readlane(cb, leader);
+    const int d = cb - cb0;
+    if (t < 16) s_members[t] = -1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (lane < P && key == e && d >= 0 && d < R) s_members[d] = lane;
+    if (t == 0) s_expert = e;
+    __syncthreads();
+  } else if (ws == nullptr) {
+    if (t < 16) s_members[t] = -1;
+    if (t == 0) s_found = 0;
+    // In-workgroup segment discovery (P <= kGatherFusedMaxP): pair p leads a
+    // segment when the number of earlier pairs with its key is a multiple of
+    // R; segments are numbered by leader position.
+    for (int p = t; p < P; p += nt) s_key[p] = key_of(p);
     __syncthreads();
     for (int p = t; p < P; p += nt) {
-      const int e = s_rhs[p];
+      const int e = s_key[p];
       int cb = 0;
-      for (int q = 0; q < p; ++q) cb += (s_rhs[q] == e);
+      for (int q = 0; q < p; ++q) cb += (s_key[q] == e);
       s_cb[p] = cb;
     }
     __syncthreads();
-    // the leader whose rank (number of earlier leaders) equals seg
     for (int p = t; p < P; p += nt) {
       if (s_cb[p] % R) continue;
       int rank = 0;
       for (int q = 0; q < p; ++q) rank += (s_cb[q] % R == 0);
       if (rank == seg) {
-        s_expert = s_rhs[p];
+        s_expert = s_key[p];
         s_found = 1;
         s_members[0] = p;
       }
@@ -164,7 +220,7 @@ __global__ __launch_bounds__(256) void gather_skinny_kernel(
     const int cb0 = s_cb[lead];
     for (int q = lead + 1 + t; q < P; q += nt) {
       const int d = s_cb[q] - cb0;
-      if (s_rhs[q] == e && d > 0 && d < R) s_members[d] = q;
+      if (s_key[q] == e && d > 0 && d < R) s_members[d] = q;
     }
     __syncthreads();
   } else {
@@ -173,46 +229,46 @@ __global__ __launch_bounds__(256) void gather_skinny_kernel(
     const int32_t* seg_start = perm + P;
     const int32_t* seg_len = seg_start + P;
     const int32_t* seg_exp = seg_len + P;
-    const int st = seg_start[seg];
+    const int st0 = seg_start[seg];
     const int ln = seg_len[seg];
-    if (t < ln) s_members[t] = perm[st + t];
+    if (t < 16) s_members[t] = t < ln ? perm[st0 + t] : -1;
     if (t == 0) s_expert = seg_exp[seg];
     __syncthreads();
   }
-
+  int nmem = 0;
+#pragma unroll 1
+  for (int j = 0; j < 16; ++j) nmem += (s_members[j] >= 0);
+  if (t < 16) {
+    const int p = s_members[t];
+    s_xbase[t] = p >= 0 ? (lhs ? lhs[p] : p) : 0;
+  }
+  __syncthreads();
   const int e = s_expert;
-  const int lane = t & 63;
-  const int wave = t >> 6;
-  const int nwaves = nt >> 6;
-  const int r = lane & 15;
-  const int c = lane >> 4;
-  const int n0 = blockIdx.y * 16;
-  const int n = n0 + r;
-  const bool nval = (n < N) && (e < E);
-  const int64_t Kw = (int64_t)K * BITS / 32;
-  const int G = K / GS;
-  const int64_t wrow_idx = nval ? ((int64_t)e * N + n) : 0;
-
-  // A row r: pair members[r / M], row r % M within the pair.
-  const int pi = r / M;
-  const int pr = r - pi * M;
-  const int q = (pi < R) ? s_members[pi] : -1;
-  int xb = -1;
-  if (q >= 0) xb = lhs ? lhs[q] : q;
-  const bool mval = (q >= 0) && (xb >= 0) && (xb < B);
-  const uint16_t* xrow = x + (mval ? ((int64_t)xb * M + pr) * K : 0);
-
-  const f32x4 acc = skinny_accumulate<DT, BITS, GS>(xrow, mval, w + wrow_idx * Kw,
-                                                    scales + wrow_idx * G, biases + wrow_idx * G,
-                                                    nval, K, wave, nwaves, c);
-  skinny_reduce(acc, nwaves, [&](int mm, int nn, float v) {
-    const int pj = mm / M;
-    if (pj >= R || n0 + nn >= N) return;
-    const int qq = s_members[pj];
-    if (qq < 0) return;
-    const int rr = mm - pj * M;
-    out[((int64_t)qq * M + rr) * N + n0 + nn] = T16<DT>::round1(v);
-  });
+  const int M = nmem * Mi;
+  const int nb = blockIdx.y * 16 * tpw;
+  if (e >= E) {
+    // invalid pairs: zero rows
+    const int cols = min(16 * tpw, N - nb);
+    for (int i = t; i < M * cols; i += nt) {
+      const int m = i / cols, nn = i - m * cols;
+      const int j = m / Mi;
+      out[((int64_t)s_members[j] * Mi + (m - j * Mi)) * N + nb + nn] = 0;
+    }
+    return;
+  }
+  const uint32_t rowB = (uint32_t)K * BITS / 8;
+  const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  for (int tt = 0; tt < tpw; ++tt) {
+    const int n0 = nb + 16 * tt;
+    if (n0 >= N) break;
+    const int64_t row0 = (int64_t)e * N + n0;
+    const GatherRows src{x, out, s_members, s_xbase, Mi, K, N, n0};
+    qmv_tile<DT, BITS, GS, GPL, NW, PF, XLDS>(
+        reinterpret_cast<const char*>(w) + row0 * rowB,
+        reinterpret_cast<const char*>(scales) + row0 * sRowB,
+        reinterpret_cast<const char*>(biases) + row0 * sRowB, min(16, N - n0), M, K, src,
+        qmv_smem, red, tt == 0);
+  }
 }
 
 template <int DT, int BITS, int GS>
@@ -220,25 +276,40 @@ inline void launch_gather_t(const void* x, const uint32_t* w, const void* s, con
                             const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
                             int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
                             hipStream_t st, int* nlaunch) {
-  using Gm = SkinnyGeom<BITS>;
-  const int R = (int)(16 / M);
-  const int nkb = (int)((K + Gm::KBLK - 1) / Gm::KBLK);
-  const int waves = nkb < kSkinnyMaxWaves ? nkb : kSkinnyMaxWaves;
+  using C = QmvConf<BITS, GS>;
+  using Gm = QmvGeom<BITS, GS, C::GPL>;
+  const size_t xs = (size_t)qmv_x_stride((int)K, Gm::STEPK);
+  int R = (int)(16 / M);
+  while (R > 1 && (size_t)R * M * xs > kQmvMaxXLds) --R;
+  const bool xlds = (size_t)R * M * xs <= kQmvMaxXLds;
   int64_t max_seg = P;
   const int32_t* wsp = nullptr;
   if (P > kGatherFusedMaxP) {
     const int64_t bound = (P + R - 1) / R + E + 1;
     if (bound < max_seg) max_seg = bound;
     const size_t shmem = 4 * sizeof(int) * (size_t)(E + 1);
-    hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, (int)P, (int)E, R,
-                       (int32_t*)ws);
+    hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, lhs, (int)P,
+                       (int)E, (int)B, R, (int32_t*)ws);
     wsp = (const int32_t*)ws;
     *nlaunch += 1;
   }
-  hipLaunchKernelGGL((gather_skinny_kernel<DT, BITS, GS>),
-                     dim3((unsigned)max_seg, (unsigned)((N + 15) / 16)), dim3(64 * waves), 0, st,
-                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs, rhs,
-                     (uint16_t*)out, wsp, (int)P, (int)B, (int)M, (int)N, (int)K, (int)E);
+  // tiles per workgroup: enough rows per workgroup to amortize discovery and
+  // the x copy, while keeping at least ~1024 workgroups for small problems
+  const int64_t tiles = (N + 15) / 16;
+  int tpw = 1;
+  while (tpw < 8 && tiles % (2 * tpw) == 0 && max_seg * (tiles / (2 * tpw)) >= 1024) tpw *= 2;
+  const dim3 grid((unsigned)max_seg, (unsigned)((tiles + tpw - 1) / tpw));
+  if (xlds) {
+    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, true>), grid,
+                       dim3(64 * C::NW), (size_t)R * M * xs, st, (const uint16_t*)x, w,
+                       (const uint16_t*)s, (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp,
+                       (int)P, (int)B, (int)M, (int)N, (int)K, (int)E, R, tpw);
+  } else {
+    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, false>), grid,
+                       dim3(64 * C::NW), 0, st, (const uint16_t*)x, w, (const uint16_t*)s,
+                       (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp, (int)P, (int)B, (int)M,
+                       (int)N, (int)K, (int)E, R, tpw);
+  }
   *nlaunch += 1;
 }
 

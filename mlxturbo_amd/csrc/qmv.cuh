@@ -86,13 +86,40 @@ __host__ __device__ inline int qmv_x_stride(int K, int stepk) {
   return 2 * (((K + stepk - 1) / stepk) * stepk) + 16;
 }
 
-template <int DT, int BITS, int GS, int GPL, int NW, int PF, bool XLDS>
-__global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict__ x,
-                                                      const uint32_t* __restrict__ w,
-                                                      const uint16_t* __restrict__ scales,
-                                                      const uint16_t* __restrict__ biases,
-                                                      uint16_t* __restrict__ out, int M, int N,
-                                                      int K, int64_t ldx, int64_t ldo) {
+// Launch geometry of the skinny kernel for one (bits, group_size): groups per
+// lane per step, waves per workgroup, pipeline stages.  Fixed per format (not
+// per M), so every output row is computed in the same order for every M.
+template <int BITS, int GS>
+struct QmvConf {
+  static constexpr int GPL = (BITS == 4 && GS == 32) ? 4 : (BITS == 8 && GS >= 64) ? 1 : 2;
+  static constexpr int NW = 4;
+  static constexpr int PF = 2;
+};
+
+// Largest x copy (M rows) kept in LDS; beyond it fragments are read from global memory.
+constexpr size_t kQmvMaxXLds = 64 * 1024;
+
+// Row sources of a tile: where the A rows (x) come from and where outputs go.
+// Dense: A row m is x row m; output (m, column n0 + nn).
+struct DenseRows {
+  const uint16_t* x;
+  uint16_t* out;
+  int64_t ldx, ldo;
+  int n0;
+  __device__ __forceinline__ const uint16_t* xrow(int m) const { return x + (int64_t)m * ldx; }
+  __device__ __forceinline__ void store(int m, int nn, uint16_t v) const {
+    out[(int64_t)m * ldo + n0 + nn] = v;
+  }
+};
+
+// One 16-row weight tile (rows n0 .. n0+rows-1 of a [*, K] quantized matrix
+// whose row n0 starts at wt / st / bt) times M <= 16 A rows.  Called by every
+// thread of a 64*NW-thread workgroup; dynamic LDS holds the x copy.
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, bool XLDS, class Rows>
+__device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char* __restrict__ st,
+                                         const char* __restrict__ bt, int rows, int M, int K,
+                                         const Rows& src, unsigned char* qmv_smem,
+                                         f32x4 (*red)[64], bool copy_x = true) {
   using Gm = QmvGeom<BITS, GS, GPL>;
   constexpr int GB = Gm::GB, LPG = Gm::LPG, STEPG = Gm::STEPG, STEPB = Gm::STEPB;
   constexpr int STEPK = Gm::STEPK, NSV = Gm::NSV, CPL = Gm::CPL, MPL = Gm::MPL;
@@ -101,20 +128,12 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
     u32x4 w[GPL][LPG];
     uint32_t s[NSV], b[NSV];
   };
-  extern __shared__ __align__(16) unsigned char qmv_smem[];
-  __shared__ f32x4 red[NW][64];
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, c = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int rows = min(16, N - n0);
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const int G = K / GS;
   const uint32_t sRowB = (uint32_t)G * 2;
-  const char* wt = reinterpret_cast<const char*>(w) + (int64_t)n0 * rowB;
-  const char* st = reinterpret_cast<const char*>(scales) + (int64_t)n0 * sRowB;
-  const char* bt = reinterpret_cast<const char*>(biases) + (int64_t)n0 * sRowB;
   const uint32_t w_nrec = (uint32_t)(rows - 1) * rowB + STEPB;
   const uint32_t s_nrec = (uint32_t)(rows - 1) * sRowB + STEPG * 2;
   const uint32_t wofs = (uint32_t)r * rowB + (uint32_t)c * GB;
@@ -156,10 +175,10 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
   const int kb = sb * STEPK, ke = se * STEPK;
   const int xr = min(r, M - 1);
   const lds_u8* xl = (const lds_u8*)qmv_smem + xr * xs;       // XLDS: A row of this lane
-  const uint16_t* xg = x + (int64_t)xr * ldx;                  // !XLDS: same, in global memory
+  const uint16_t* xg = src.xrow(xr);                           // !XLDS: same, in global memory
   constexpr int XB = 4;                                        // x pieces per lane per batch
   const int pw = (ke - kb) / 8;                                // 16-byte pieces per row
-  const int npieces = XLDS ? M * pw : 0;
+  const int npieces = (XLDS && copy_x) ? M * pw : 0;
   u32x4 xp[XB];
   auto x_fetch = [&](int base) {
 #pragma unroll
@@ -168,7 +187,7 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
       xp[q] = (u32x4){0u, 0u, 0u, 0u};
       if (i < npieces) {
         const int m = i / pw, k = kb + 8 * (i - m * pw);
-        if (k < K) xp[q] = *reinterpret_cast<const u32x4*>(x + (int64_t)m * ldx + k);
+        if (k < K) xp[q] = *reinterpret_cast<const u32x4*>(src.xrow(m) + k);
       }
     }
   };
@@ -188,7 +207,7 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
 #pragma unroll
   for (int i = 0; i < PF - 1; ++i) load(S[i], sb + i, sb + i < fe);
 
-  if constexpr (XLDS) {
+  if (XLDS && copy_x) {
     x_store(lane);
     for (int base = lane + XB * 64; base < npieces; base += XB * 64) {
       x_fetch(base);
@@ -293,20 +312,43 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * c + v;
-      if (m < M && r < rows) out[(int64_t)m * ldo + n0 + r] = T::round1(acc[v]);
+      if (m < M && r < rows) src.store(m, r, T::round1(acc[v]));
     }
   } else {
     red[wave][lane] = acc;
     __syncthreads();
     for (int tt = threadIdx.x; tt < 256; tt += 64 * NW) {
       const int mm = tt >> 4, nn = tt & 15;
-      const int src = ((mm >> 2) << 4) | nn, v = mm & 3;
-      float sum = red[0][src][v];
+      const int sl = ((mm >> 2) << 4) | nn, v = mm & 3;
+      float sum = red[0][sl][v];
 #pragma unroll
-      for (int q = 1; q < NW; ++q) sum += red[q][src][v];
-      if (mm < M && nn < rows) out[(int64_t)mm * ldo + n0 + nn] = T::round1(sum);
+      for (int q = 1; q < NW; ++q) sum += red[q][sl][v];
+      if (mm < M && nn < rows) src.store(mm, nn, T::round1(sum));
     }
+    __syncthreads();
   }
+}
+
+// grid.x = ceil(N / 16) tiles, block = 64 * NW threads.
+// Dynamic LDS: XLDS ? M * qmv_x_stride(K, STEPK) : 0 bytes.
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, bool XLDS>
+__global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict__ x,
+                                                      const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint16_t* __restrict__ biases,
+                                                      uint16_t* __restrict__ out, int M, int N,
+                                                      int K, int64_t ldx, int64_t ldo) {
+  extern __shared__ __align__(16) unsigned char qmv_smem[];
+  __shared__ f32x4 red[NW][64];
+  const int n0 = blockIdx.x * 16;
+  const uint32_t rowB = (uint32_t)K * BITS / 8;
+  const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  const DenseRows src{x, out, ldx, ldo, n0};
+  qmv_tile<DT, BITS, GS, GPL, NW, PF, XLDS>(
+      reinterpret_cast<const char*>(w) + (int64_t)n0 * rowB,
+      reinterpret_cast<const char*>(scales) + (int64_t)n0 * sRowB,
+      reinterpret_cast<const char*>(biases) + (int64_t)n0 * sRowB, min(16, N - n0), M, K, src,
+      qmv_smem, red);
 }
 
 }  // namespace mq
