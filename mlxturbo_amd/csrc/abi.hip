@@ -93,22 +93,27 @@ struct SkinnyLaunch {
   static void run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
                   int64_t M, int64_t N, int64_t K, hipStream_t st) {
     using C = mq::QmvConf<BITS, GS>;
-    using Gm = mq::QmvGeom<BITS, GS, C::GPL>;
     const unsigned grid = (unsigned)((N + 15) / 16);
     for (int64_t m0 = 0; m0 < M; m0 += 16) {
       const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
-      const size_t lds = (size_t)mt * mq::qmv_x_stride((int)K, Gm::STEPK);
       const uint16_t* xp = (const uint16_t*)x + m0 * K;
       uint16_t* op = (uint16_t*)out + m0 * N;
-      if (lds <= mq::kQmvMaxXLds) {
-        hipLaunchKernelGGL((mq::qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, true>), dim3(grid),
-                           dim3(64 * C::NW), lds, st, xp, w, (const uint16_t*)s,
-                           (const uint16_t*)b, op, mt, (int)N, (int)K, (int64_t)K, (int64_t)N);
-      } else {
-        hipLaunchKernelGGL((mq::qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, false>),
-                           dim3(grid), dim3(64 * C::NW), 0, st, xp, w, (const uint16_t*)s,
-                           (const uint16_t*)b, op, mt, (int)N, (int)K, (int64_t)K, (int64_t)N);
-      }
+      // x streams through LDS for up to 8 rows whose bytes a buffer range covers
+      const int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? mq::qmv_xm_for(mt) : 0;
+      const bool sbl = mq::qmv_sb_fits(K / GS, C::NW, s, b);
+      const size_t sb_lds = mq::qmv_sb_lds((int)(K / GS));
+      auto lds_for = [&](int xmax, bool with_sb) {
+        return mq::qmv_x_lds<BITS, GS, C::GPL>(C::NW, xmax) + (with_sb ? sb_lds : 0);
+      };
+#define MQ_SX(X, SB)                                                                          \
+      if (xm == X && sbl == SB)                                                               \
+        hipLaunchKernelGGL((mq::qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, X, SB>),         \
+                           dim3(grid), dim3(64 * C::NW), lds_for(X, SB), st, xp, w,           \
+                           (const uint16_t*)s, (const uint16_t*)b, op, mt, (int)N, (int)K,    \
+                           (int64_t)K, (int64_t)N);
+      MQ_SX(0, true) MQ_SX(1, true) MQ_SX(2, true) MQ_SX(4, true) MQ_SX(8, true)
+      MQ_SX(0, false) MQ_SX(1, false) MQ_SX(2, false) MQ_SX(4, false) MQ_SX(8, false)
+#undef MQ_SX
     }
   }
 };

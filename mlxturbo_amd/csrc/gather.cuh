@@ -119,13 +119,14 @@ __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __rest
 // A rows of a gather segment: pair members[j] contributes rows j*Mi .. j*Mi+Mi-1.
 struct GatherRows {
   const uint16_t* x;
+  uint32_t x_nrec;
   uint16_t* out;
   const int* members;      // LDS
   const int* xbase;        // LDS: x batch index of each member
   int Mi, K, N, n0;
-  __device__ __forceinline__ const uint16_t* xrow(int m) const {
+  __device__ __forceinline__ int64_t xoff(int m) const {
     const int j = m / Mi;
-    return x + ((int64_t)xbase[j] * Mi + (m - j * Mi)) * K;
+    return ((int64_t)xbase[j] * Mi + (m - j * Mi)) * K;
   }
   __device__ __forceinline__ void store(int m, int nn, uint16_t v) const {
     const int j = m / Mi;
@@ -135,11 +136,14 @@ struct GatherRows {
 
 // grid = (segments upper bound, ceil(N / (16 * tpw))); block 64 * NW.  Each
 // workgroup runs tpw consecutive 16-row tiles of its expert, reusing the
-// segment and the LDS copy of its x rows.
+// segment found once.
 // Segment = up to R pairs that share an expert (R * Mi <= 16 A rows).
 // Pairs whose expert or x index is out of range form their own segments and
-// get zero outputs.  Dynamic LDS: XLDS ? R * Mi * qmv_x_stride(K, STEPK) : 0.
-template <int DT, int BITS, int GS, int GPL, int NW, int PF, bool XLDS>
+// get zero outputs.  XM > 0: x streams through LDS (qmv_x_lds(NW, XM) bytes of
+// dynamic LDS), R * Mi <= XM and B * Mi * K * 2 < 2^31; a segment of one pair
+// with Mi == 1 runs the one-row variant of the tile.  SBL: tile scales/biases
+// are copied to LDS (qmv_sb_lds(K / GS) more bytes, qmv_sb_fits holds).
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL>
 __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -258,16 +262,23 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   }
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  const uint32_t x_nrec = XM > 0 ? (uint32_t)((int64_t)B * Mi * K * 2) : 0u;
   for (int tt = 0; tt < tpw; ++tt) {
     const int n0 = nb + 16 * tt;
     if (n0 >= N) break;
     const int64_t row0 = (int64_t)e * N + n0;
-    const GatherRows src{x, out, s_members, s_xbase, Mi, K, N, n0};
-    qmv_tile<DT, BITS, GS, GPL, NW, PF, XLDS>(
-        reinterpret_cast<const char*>(w) + row0 * rowB,
-        reinterpret_cast<const char*>(scales) + row0 * sRowB,
-        reinterpret_cast<const char*>(biases) + row0 * sRowB, min(16, N - n0), M, K, src,
-        qmv_smem, red, tt == 0);
+    const GatherRows src{x, x_nrec, out, s_members, s_xbase, Mi, K, N, n0};
+    const char* wt = reinterpret_cast<const char*>(w) + row0 * rowB;
+    const char* st = reinterpret_cast<const char*>(scales) + row0 * sRowB;
+    const char* bt = reinterpret_cast<const char*>(biases) + row0 * sRowB;
+    // the one-row variant uses a prefix of the launch's x region; its scale
+    // copy lands inside the XM-row launch's allocation too
+    if (XM > 1 && M == 1)
+      qmv_tile<DT, BITS, GS, GPL, NW, PF, (XM > 1 ? 1 : XM), SBL>(wt, st, bt, min(16, N - n0), M,
+                                                                 K, src, qmv_smem, red);
+    else
+      qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL>(wt, st, bt, min(16, N - n0), M, K, src,
+                                                   qmv_smem, red);
   }
 }
 
@@ -277,11 +288,15 @@ inline void launch_gather_t(const void* x, const uint32_t* w, const void* s, con
                             int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
                             hipStream_t st, int* nlaunch) {
   using C = QmvConf<BITS, GS>;
-  using Gm = QmvGeom<BITS, GS, C::GPL>;
-  const size_t xs = (size_t)qmv_x_stride((int)K, Gm::STEPK);
-  int R = (int)(16 / M);
-  while (R > 1 && (size_t)R * M * xs > kQmvMaxXLds) --R;
-  const bool xlds = (size_t)R * M * xs <= kQmvMaxXLds;
+  // Segments of up to R pairs; R * M <= 8 A rows stream x through LDS, one
+  // pair of more than 8 rows reads x fragments from global memory.
+  const int R = M <= kQmvMaxXM ? (int)(kQmvMaxXM / M) : 1;
+  const int XM = (B * M * K * 2 < ((int64_t)1 << 31)) ? qmv_xm_for(R * M) : 0;
+  const bool sbl = qmv_sb_fits(K / GS, C::NW, s, b);
+  const size_t sb_lds = qmv_sb_lds((int)(K / GS));
+  auto lds_for = [&](int xmax, bool with_sb) {
+    return qmv_x_lds<BITS, GS, C::GPL>(C::NW, xmax) + (with_sb ? sb_lds : 0);
+  };
   int64_t max_seg = P;
   const int32_t* wsp = nullptr;
   if (P > kGatherFusedMaxP) {
@@ -293,23 +308,22 @@ inline void launch_gather_t(const void* x, const uint32_t* w, const void* s, con
     wsp = (const int32_t*)ws;
     *nlaunch += 1;
   }
-  // tiles per workgroup: enough rows per workgroup to amortize discovery and
-  // the x copy, while keeping at least ~1024 workgroups for small problems
+  // tiles per workgroup: enough rows per workgroup to amortize segment
+  // discovery, while keeping at least ~1024 workgroups for small problems
   const int64_t tiles = (N + 15) / 16;
   int tpw = 1;
   while (tpw < 8 && tiles % (2 * tpw) == 0 && max_seg * (tiles / (2 * tpw)) >= 1024) tpw *= 2;
   const dim3 grid((unsigned)max_seg, (unsigned)((tiles + tpw - 1) / tpw));
-  if (xlds) {
-    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, true>), grid,
-                       dim3(64 * C::NW), (size_t)R * M * xs, st, (const uint16_t*)x, w,
-                       (const uint16_t*)s, (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp,
-                       (int)P, (int)B, (int)M, (int)N, (int)K, (int)E, R, tpw);
-  } else {
-    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, false>), grid,
-                       dim3(64 * C::NW), 0, st, (const uint16_t*)x, w, (const uint16_t*)s,
-                       (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp, (int)P, (int)B, (int)M,
-                       (int)N, (int)K, (int)E, R, tpw);
+#define MQ_GX(X, SB)                                                                        \
+  if (XM == X && sbl == SB) {                                                               \
+    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, X, SB>), grid,  \
+                       dim3(64 * C::NW), lds_for(X, SB), st, (const uint16_t*)x, w,         \
+                       (const uint16_t*)s, (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp, \
+                       (int)P, (int)B, (int)M, (int)N, (int)K, (int)E, R, tpw);             \
   }
+  MQ_GX(0, true) MQ_GX(1, true) MQ_GX(2, true) MQ_GX(4, true) MQ_GX(8, true)
+  MQ_GX(0, false) MQ_GX(1, false) MQ_GX(2, false) MQ_GX(4, false) MQ_GX(8, false)
+#undef MQ_GX
   *nlaunch += 1;
 }
 
