@@ -1,8 +1,9 @@
 """Build ``libmlxturbo_amd.so`` in-tree with hipcc for gfx950.
 
 Usage: ``python -m mlxturbo_amd.build``.  The library is plain C ABI over HIP
-(no torch headers), so one hipcc invocation over ``csrc/abi.hip`` (which
-includes every kernel header) produces it.
+(no torch headers): ``csrc/abi.hip`` (argument checks and routing) plus
+``csrc/inst.hip`` compiled once per (dtype, bits) pair, in parallel, then
+linked into one shared object.
 """
 
 from __future__ import annotations
@@ -11,6 +12,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -38,22 +40,52 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm required to build mlxturbo_amd)")
 
 
+# (source, extra defines) of each translation unit
+UNITS = [("abi.hip", [])] + [
+    ("inst.hip", [f"-DMQ_INST_DT={dt}", f"-DMQ_INST_BITS={bits}"])
+    for dt in (0, 1) for bits in (4, 8)
+]
+
+_NOISE = ("packed-fp32-ops", "warning generated", "warnings generated")
+
+
 def sources() -> list[str]:
-    return [os.path.join(CSRC, "abi.hip")]
+    return sorted({os.path.join(CSRC, src) for src, _ in UNITS})
+
+
+def _filtered(stderr: str) -> str:
+    return "\n".join(l for l in stderr.splitlines() if not any(n in l for n in _NOISE))
 
 
 def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *sources()]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = ("packed-fp32-ops", "warning generated", "warnings generated")
-    err = "\n".join(l for l in res.stderr.splitlines() if not any(n in l for n in noise))
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if err.strip() and verbose:
-        print(err, file=sys.stderr)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="mq_build_") as tmpdir:
+        procs = []
+        for i, (src, defs) in enumerate(UNITS):
+            obj = os.path.join(tmpdir, f"unit{i}.o")
+            cmd = [hipcc(), *compile_flags, *defs, "-c", "-o", obj, os.path.join(CSRC, src)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((obj, cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                     stderr=subprocess.PIPE, text=True)))
+        objs = []
+        failed = []
+        for obj, cmd, proc in procs:
+            _, err = proc.communicate()
+            if proc.returncode != 0:
+                failed.append(f"{' '.join(cmd)}\n{_filtered(err)}")
+            elif verbose and _filtered(err).strip():
+                print(_filtered(err), file=sys.stderr)
+            objs.append(obj)
+        if failed:
+            raise RuntimeError("hipcc failed:\n" + "\n\n".join(failed))
+        tmp = OUT + ".tmp"
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed ({res.returncode}):\n{_filtered(res.stderr)}")
     os.replace(tmp, OUT)
     return OUT
 

@@ -8,9 +8,7 @@
 
 #include "../../include/mlxturbo_amd.h"
 #include "dequant.cuh"
-#include "gather.cuh"
-#include "qmv.cuh"
-#include "qmm_wide.cuh"
+#include "launch.h"
 
 namespace {
 
@@ -58,65 +56,14 @@ int check_common(const void* w, const void* scales, const void* biases, int64_t 
 template <template <int, int, int> class Launcher, typename... Args>
 int dispatch_16(int dtype, int bits, int gs, Args... args) {
 #define MQ_CASE(DT, B, G)                                   \
-  if (dtype == DT && bits == B && gs == G) {                \
-    Launcher<DT, B, G>::run(args...);                       \
-    return MQ_OK;                                           \
-  }
+  if (dtype == DT && bits == B && gs == G) return Launcher<DT, B, G>::run(args...);
   MQ_CASE(mq::kBF16, 4, 64) MQ_CASE(mq::kBF16, 4, 32) MQ_CASE(mq::kBF16, 4, 128)
   MQ_CASE(mq::kBF16, 8, 64) MQ_CASE(mq::kBF16, 8, 32) MQ_CASE(mq::kBF16, 8, 128)
   MQ_CASE(mq::kF16, 4, 64) MQ_CASE(mq::kF16, 4, 32) MQ_CASE(mq::kF16, 4, 128)
   MQ_CASE(mq::kF16, 8, 64) MQ_CASE(mq::kF16, 8, 32) MQ_CASE(mq::kF16, 8, 128)
 #undef MQ_CASE
-  return fail(MQ_EUNSUPPORTED, "no kernel for dtype=%d bits=%d group_size=%d", dtype, bits, gs);
+  return mq::kStatusUnsupported;
 }
-
-int grid_for(int64_t work, int per_block) {
-  int64_t g = (work + per_block - 1) / per_block;
-  if (g > 65536) g = 65536;
-  if (g < 1) g = 1;
-  return (int)g;
-}
-
-template <int DT, int BITS, int GS>
-struct DequantLaunch {
-  static void run(const uint32_t* w, const void* s, const void* b, void* out, int64_t N, int64_t K,
-                  hipStream_t st) {
-    const int64_t chunks = N * (K * BITS / 32) / 4;
-    hipLaunchKernelGGL((mq::dequantize16_kernel<DT, BITS, GS>), dim3(grid_for(chunks, 256)),
-                       dim3(256), 0, st, w, (const uint16_t*)s, (const uint16_t*)b,
-                       (uint16_t*)out, N, K);
-  }
-};
-
-template <int DT, int BITS, int GS>
-struct SkinnyLaunch {
-  static void run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
-                  int64_t M, int64_t N, int64_t K, hipStream_t st) {
-    using C = mq::QmvConf<BITS, GS>;
-    const unsigned grid = (unsigned)((N + 15) / 16);
-    for (int64_t m0 = 0; m0 < M; m0 += 16) {
-      const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
-      const uint16_t* xp = (const uint16_t*)x + m0 * K;
-      uint16_t* op = (uint16_t*)out + m0 * N;
-      // x streams through LDS for up to 8 rows whose bytes a buffer range covers
-      const int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? mq::qmv_xm_for(mt) : 0;
-      const bool sbl = mq::qmv_sb_fits(K / GS, C::NW, s, b);
-      const size_t sb_lds = mq::qmv_sb_lds((int)(K / GS));
-      auto lds_for = [&](int xmax, bool with_sb) {
-        return mq::qmv_x_lds<BITS, GS, C::GPL>(C::NW, xmax) + (with_sb ? sb_lds : 0);
-      };
-#define MQ_SX(X, SB)                                                                          \
-      if (xm == X && sbl == SB)                                                               \
-        hipLaunchKernelGGL((mq::qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, X, SB>),         \
-                           dim3(grid), dim3(64 * C::NW), lds_for(X, SB), st, xp, w,           \
-                           (const uint16_t*)s, (const uint16_t*)b, op, mt, (int)N, (int)K,    \
-                           (int64_t)K, (int64_t)N);
-      MQ_SX(0, true) MQ_SX(1, true) MQ_SX(2, true) MQ_SX(4, true) MQ_SX(8, true)
-      MQ_SX(0, false) MQ_SX(1, false) MQ_SX(2, false) MQ_SX(4, false) MQ_SX(8, false)
-#undef MQ_SX
-    }
-  }
-};
 
 }  // namespace
 
@@ -139,7 +86,7 @@ int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, voi
     const int64_t words = N * (K * bits / 32);
 #define MQ_D32(B, G)                                                                         \
   if (bits == B && group_size == G) {                                                         \
-    hipLaunchKernelGGL((mq::dequantize32_kernel<B, G>), dim3(grid_for(words, 256)), dim3(256), \
+    hipLaunchKernelGGL((mq::dequantize32_kernel<B, G>), dim3(mq::dequant_grid(words, 256)), dim3(256), \
                        0, st, w, (const float*)scales, (const float*)biases, (float*)out, N, K); \
     return check_launch("dequantize");                                                        \
   }
@@ -148,8 +95,9 @@ int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, voi
     return fail(MQ_EUNSUPPORTED, "dequantize: unsupported float32 configuration");
   }
   if (!aligned16(out)) return fail(MQ_EINVAL, "out must be 16-byte aligned");
-  rc = dispatch_16<DequantLaunch>(dtype, bits, group_size, w, scales, biases, out, N, K, st);
-  if (rc) return rc;
+  rc = dispatch_16<mq::DequantLaunch>(dtype, bits, group_size, w, scales, biases, out, N, K, st);
+  if (rc) return fail(rc, "dequantize: no kernel for dtype=%d bits=%d group_size=%d", dtype, bits,
+                      group_size);
   return check_launch("dequantize");
 }
 
@@ -170,12 +118,15 @@ int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
   if (M == 0 || N == 0) return MQ_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   if (mq::wide_eligible(M, N, K, bits, group_size)) {
-    rc = mq::launch_wide(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, st);
+    rc = dispatch_16<mq::WideLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
+                                     st);
     if (rc) return fail(rc, "quantized_matmul: no wide kernel for this configuration");
     return check_launch("quantized_matmul(wide)");
   }
-  rc = dispatch_16<SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K, st);
-  if (rc) return rc;
+  rc = dispatch_16<mq::SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
+                                     st);
+  if (rc) return fail(rc, "quantized_matmul: no kernel for dtype=%d bits=%d group_size=%d", dtype,
+                      bits, group_size);
   return check_launch("quantized_matmul(skinny)");
 }
 
@@ -209,8 +160,9 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
                 mq::gather_workspace_bytes(P, M));
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   int nl = 0;
-  rc = mq::launch_gather(x, w, scales, biases, lhs_indices, rhs_indices, out, P, B, M, N, K, E,
-                         group_size, bits, dtype, sorted_indices, workspace, st, &nl);
+  (void)sorted_indices;  // segments are discovered either way; sortedness only orders them
+  rc = dispatch_16<mq::GatherLaunch>(dtype, bits, group_size, x, w, scales, biases, lhs_indices,
+                                     rhs_indices, out, P, B, M, N, K, E, workspace, st, &nl);
   if (rc) return fail(rc, "gather_qmm: no kernel for this configuration");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail((int)e, "gather_qmm: launch failed: %s", hipGetErrorString(e));

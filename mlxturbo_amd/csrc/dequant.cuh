@@ -5,7 +5,7 @@
 // packed codes (32 codes at 4 bits, 16 at 8 bits; always inside one group
 // because group_size >= 32) into 2-4 16-byte stores.
 #pragma once
-#include "mq_common.h"
+#include "launch.h"
 
 namespace mq {
 
@@ -71,6 +71,23 @@ __global__ __launch_bounds__(256) void dequantize32_kernel(const uint32_t* __res
     for (int j = 0; j < PER; ++j)
       out[n * K + k0 + j] = sf * (float)((word >> (BITS * j)) & MASK) + bf;
   }
+}
+
+inline int dequant_grid(int64_t work, int per_block) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+template <int DT, int BITS, int GS>
+int DequantLaunch<DT, BITS, GS>::run(const uint32_t* w, const void* s, const void* b, void* out,
+                                     int64_t N, int64_t K, hipStream_t st) {
+  const int64_t chunks = N * (K * BITS / 32) / 4;
+  hipLaunchKernelGGL((dequantize16_kernel<DT, BITS, GS>), dim3(dequant_grid(chunks, 256)),
+                     dim3(256), 0, st, w, (const uint16_t*)s, (const uint16_t*)b,
+                     (uint16_t*)out, N, K);
+  return 0;
 }
 
 }  // namespace mq

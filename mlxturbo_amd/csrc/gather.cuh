@@ -23,23 +23,15 @@
 // one-workgroup counting-sort prep kernel into the caller's workspace first.
 // Pairs with an out-of-range expert or x index produce zero rows.
 #pragma once
+#include "launch.h"
 #include "qmv.cuh"
 
 namespace mq {
 
-constexpr int kGatherFusedMaxP = 256;
-constexpr int kGatherPrepMaxE = 2048;
-
-// Workspace (int32): [0] nseg | perm[P] | seg_start[P] | seg_len[P] | seg_expert[P]
-__host__ __device__ inline size_t gather_ws_words(int64_t P) { return 1 + 4 * (size_t)P; }
-
-inline size_t gather_workspace_bytes(int64_t P, int64_t M) {
-  (void)M;
-  if (P <= kGatherFusedMaxP) return 0;
-  return (gather_ws_words(P) * 4 + 255) & ~(size_t)255;
-}
-
-__global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __restrict__ rhs,
+// Counting sort of the pairs by key (expert, or E for invalid pairs) into
+// segments of up to R pairs; one workgroup.  Internal linkage: every
+// translation unit that launches it has its own copy.
+static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __restrict__ rhs,
                                                            const int32_t* __restrict__ lhs, int P,
                                                            int E, int B, int R,
                                                            int32_t* __restrict__ ws) {
@@ -134,16 +126,23 @@ struct GatherRows {
   }
 };
 
-// grid = (segments upper bound, ceil(N / (16 * tpw))); block 64 * NW.  Each
-// workgroup runs tpw consecutive 16-row tiles of its expert, reusing the
-// segment found once.
-// Segment = up to R pairs that share an expert (R * Mi <= 16 A rows).
-// Pairs whose expert or x index is out of range form their own segments and
-// get zero outputs.  XM > 0: x streams through LDS (qmv_x_lds(NW, XM) bytes of
-// dynamic LDS), R * Mi <= XM and B * Mi * K * 2 < 2^31; a segment of one pair
-// with Mi == 1 runs the one-row variant of the tile.  SBL: tile scales/biases
-// are copied to LDS (qmv_sb_lds(K / GS) more bytes, qmv_sb_fits holds).
-template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL>
+// Dynamic LDS of one wave group of the gather kernel (see below).
+template <int BITS, int GS, int GPL>
+__host__ __device__ inline size_t gather_group_lds(int NWT, int XM, bool sbl, int G) {
+  return qmv_x_lds<BITS, GS, GPL>(NWT, XM) + (sbl ? qmv_sb_lds(G) : 0);
+}
+
+// grid = (segments upper bound, ceil(N / (16 * NW / NWT * tpw))); block 64 * NW.
+// Segment = up to R pairs that share an expert (R * Mi <= 16 A rows); pairs
+// whose expert or x index is out of range form their own segments and get
+// zero outputs.  The workgroup's NW waves form NW / NWT groups of NWT waves;
+// in each of tpw rounds every group computes its own 16-row tile of the
+// expert (NWT = 1 when K is a single step, so short-K experts do not leave
+// three of four waves idle).  Dynamic LDS: NW / NWT x gather_group_lds.
+// XM > 0: x streams through LDS, R * Mi <= XM and B * Mi * K * 2 < 2^31; a
+// segment of one pair with Mi == 1 runs the one-row variant of the tile.
+// SBL: tile scales/biases are copied to LDS (qmv_sb_fits holds).
+template <int DT, int BITS, int GS, int GPL, int NW, int NWT, int PF, int XM, bool SBL>
 __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -189,7 +188,10 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     if (t < 16) s_members[t] = -1;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    if (lane < P && key == e && d >= 0 && d < R) s_members[d] = lane;
+    if (lane < P && key == e && d >= 0 && d < R) {
+      s_members[d] = lane;
+      s_xbase[d] = lhs ? lhs[lane] : lane;       // loaded with rhs by key_of: cache hit
+    }
     if (t == 0) s_expert = e;
     __syncthreads();
   } else if (ws == nullptr) {
@@ -242,17 +244,20 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   int nmem = 0;
 #pragma unroll 1
   for (int j = 0; j < 16; ++j) nmem += (s_members[j] >= 0);
-  if (t < 16) {
-    const int p = s_members[t];
-    s_xbase[t] = p >= 0 ? (lhs ? lhs[p] : p) : 0;
+  if (!(ws == nullptr && P <= 64)) {
+    if (t < 16) {
+      const int p = s_members[t];
+      s_xbase[t] = p >= 0 ? (lhs ? lhs[p] : p) : 0;
+    }
+    __syncthreads();
   }
-  __syncthreads();
+  constexpr int NG = NW / NWT;                 // tile groups per workgroup
   const int e = s_expert;
   const int M = nmem * Mi;
-  const int nb = blockIdx.y * 16 * tpw;
+  const int nb = blockIdx.y * 16 * NG * tpw;
   if (e >= E) {
     // invalid pairs: zero rows
-    const int cols = min(16 * tpw, N - nb);
+    const int cols = min(16 * NG * tpw, N - nb);
     for (int i = t; i < M * cols; i += nt) {
       const int m = i / cols, nn = i - m * cols;
       const int j = m / Mi;
@@ -263,39 +268,59 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const uint32_t sRowB = (uint32_t)(K / GS) * 2;
   const uint32_t x_nrec = XM > 0 ? (uint32_t)((int64_t)B * Mi * K * 2) : 0u;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int g = wave / NWT, kw = wave - g * NWT;
+  unsigned char* gsm = qmv_smem + g * gather_group_lds<BITS, GS, GPL>(NWT, XM, SBL, K / GS);
   for (int tt = 0; tt < tpw; ++tt) {
-    const int n0 = nb + 16 * tt;
-    if (n0 >= N) break;
-    const int64_t row0 = (int64_t)e * N + n0;
+    const int n00 = nb + 16 * NG * tt;
+    if (n00 >= N) break;                       // uniform in the workgroup
+    // a group past N runs an empty tile (rows <= 0) to keep the barriers
+    const int n0 = n00 + 16 * g;
+    const int rows = min(16, N - n0);
+    const int64_t row0 = (int64_t)e * N + (rows > 0 ? n0 : 0);
     const GatherRows src{x, x_nrec, out, s_members, s_xbase, Mi, K, N, n0};
     const char* wt = reinterpret_cast<const char*>(w) + row0 * rowB;
     const char* st = reinterpret_cast<const char*>(scales) + row0 * sRowB;
     const char* bt = reinterpret_cast<const char*>(biases) + row0 * sRowB;
-    // the one-row variant uses a prefix of the launch's x region; its scale
-    // copy lands inside the XM-row launch's allocation too
+    // the one-row variant uses a prefix of the group's x region; its scale
+    // copy lands inside the group's region too
     if (XM > 1 && M == 1)
-      qmv_tile<DT, BITS, GS, GPL, NW, PF, (XM > 1 ? 1 : XM), SBL>(wt, st, bt, min(16, N - n0), M,
-                                                                 K, src, qmv_smem, red);
+      qmv_tile<DT, BITS, GS, GPL, NWT, PF, (XM > 1 ? 1 : XM), SBL>(
+          wt, st, bt, rows, M, K, src, gsm, red + g * NWT, kw, t - 64 * NWT * g);
     else
-      qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL>(wt, st, bt, min(16, N - n0), M, K, src,
-                                                   qmv_smem, red);
+      qmv_tile<DT, BITS, GS, GPL, NWT, PF, XM, SBL>(wt, st, bt, rows, M, K, src, gsm,
+                                                    red + g * NWT, kw, t - 64 * NWT * g);
   }
 }
 
 template <int DT, int BITS, int GS>
-inline void launch_gather_t(const void* x, const uint32_t* w, const void* s, const void* b,
-                            const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
-                            int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
-                            hipStream_t st, int* nlaunch) {
+int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
+                                    const void* b, const int32_t* lhs, const int32_t* rhs,
+                                    void* out, int64_t P, int64_t B, int64_t M, int64_t N,
+                                    int64_t K, int64_t E, void* ws, hipStream_t st,
+                                    int* nlaunch) {
+  if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
+  if ((N + 15) / 16 > 65535) return kStatusUnsupported;
   using C = QmvConf<BITS, GS>;
+  using Gm = QmvGeom<BITS, GS, C::GPL>;
   // Segments of up to R pairs; R * M <= 8 A rows stream x through LDS, one
-  // pair of more than 8 rows reads x fragments from global memory.
-  const int R = M <= kQmvMaxXM ? (int)(kQmvMaxXM / M) : 1;
+  // pair of more than 8 rows reads x fragments from global memory.  A segment
+  // holds at most one pair per x batch in the usual MoE call (each token
+  // picks distinct experts), so R <= B wastes nothing; more pairs of one
+  // expert simply form more segments.
+  int R = M <= kQmvMaxXM ? (int)(kQmvMaxXM / M) : 1;
+  if (R > B) R = (int)(B > 0 ? B : 1);
   const int XM = (B * M * K * 2 < ((int64_t)1 << 31)) ? qmv_xm_for(R * M) : 0;
-  const bool sbl = qmv_sb_fits(K / GS, C::NW, s, b);
-  const size_t sb_lds = qmv_sb_lds((int)(K / GS));
-  auto lds_for = [&](int xmax, bool with_sb) {
-    return qmv_x_lds<BITS, GS, C::GPL>(C::NW, xmax) + (with_sb ? sb_lds : 0);
+  // waves per tile: the K split only pays when each wave gets a step
+  const int64_t nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
+  const int nwt = nsteps >= 4 ? 4 : nsteps >= 2 ? 2 : 1;
+  const int ng = C::NW / nwt;
+  const bool sbl = qmv_sb_fits(K / GS, nwt, s, b);
+  // without the scale copy only the 8-row streamed-x variant is built
+  const int xml = (sbl || XM == 0) ? XM : kQmvMaxXM;
+  auto lds_for = [&](int xmax, int wpt, bool with_sb) {
+    return (size_t)(C::NW / wpt) *
+           gather_group_lds<BITS, GS, C::GPL>(wpt, xmax, with_sb, (int)(K / GS));
   };
   int64_t max_seg = P;
   const int32_t* wsp = nullptr;
@@ -308,43 +333,27 @@ inline void launch_gather_t(const void* x, const uint32_t* w, const void* s, con
     wsp = (const int32_t*)ws;
     *nlaunch += 1;
   }
-  // tiles per workgroup: enough rows per workgroup to amortize segment
+  // tile rounds per workgroup: enough rows per workgroup to amortize segment
   // discovery, while keeping at least ~1024 workgroups for small problems
-  const int64_t tiles = (N + 15) / 16;
+  const int64_t slots = (N + 16 * ng - 1) / (16 * ng);
   int tpw = 1;
-  while (tpw < 8 && tiles % (2 * tpw) == 0 && max_seg * (tiles / (2 * tpw)) >= 1024) tpw *= 2;
-  const dim3 grid((unsigned)max_seg, (unsigned)((tiles + tpw - 1) / tpw));
-#define MQ_GX(X, SB)                                                                        \
-  if (XM == X && sbl == SB) {                                                               \
-    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, X, SB>), grid,  \
-                       dim3(64 * C::NW), lds_for(X, SB), st, (const uint16_t*)x, w,         \
-                       (const uint16_t*)s, (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp, \
-                       (int)P, (int)B, (int)M, (int)N, (int)K, (int)E, R, tpw);             \
+  while (tpw < 8 && slots % (2 * tpw) == 0 && max_seg * (slots / (2 * tpw)) >= 1024) tpw *= 2;
+  const dim3 grid((unsigned)max_seg, (unsigned)((slots + tpw - 1) / tpw));
+#define MQ_GX(WPT, X, SB)                                                                    \
+  if (nwt == WPT && xml == X && sbl == SB) {                                                  \
+    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, WPT, C::PF, X, SB>),    \
+                       grid, dim3(64 * C::NW), lds_for(X, WPT, SB), st, (const uint16_t*)x, w, \
+                       (const uint16_t*)s, (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp,  \
+                       (int)P, (int)B, (int)M, (int)N, (int)K, (int)E, R, tpw);              \
   }
-  MQ_GX(0, true) MQ_GX(1, true) MQ_GX(2, true) MQ_GX(4, true) MQ_GX(8, true)
-  MQ_GX(0, false) MQ_GX(1, false) MQ_GX(2, false) MQ_GX(4, false) MQ_GX(8, false)
+#define MQ_GXW(WPT)                                                                          \
+  MQ_GX(WPT, 0, true) MQ_GX(WPT, 1, true) MQ_GX(WPT, 2, true) MQ_GX(WPT, 4, true)            \
+  MQ_GX(WPT, 8, true) MQ_GX(WPT, 0, false) MQ_GX(WPT, 8, false)
+  MQ_GXW(1) MQ_GXW(2) MQ_GXW(4)
+#undef MQ_GXW
 #undef MQ_GX
   *nlaunch += 1;
-}
-
-inline int launch_gather(const void* x, const uint32_t* w, const void* s, const void* b,
-                         const int32_t* lhs, const int32_t* rhs, void* out, int64_t P, int64_t B,
-                         int64_t M, int64_t N, int64_t K, int64_t E, int gs, int bits, int dtype,
-                         int sorted, void* ws, hipStream_t st, int* nlaunch) {
-  (void)sorted;  // segments are discovered either way; sortedness only orders them
-  if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
-  if ((N + 15) / 16 > 65535) return kStatusUnsupported;
-#define MQ_G(DT, BB, G)                                                                  \
-  if (dtype == DT && bits == BB && gs == G) {                                            \
-    launch_gather_t<DT, BB, G>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st, nlaunch); \
-    return 0;                                                                            \
-  }
-  MQ_G(kBF16, 4, 64) MQ_G(kBF16, 4, 32) MQ_G(kBF16, 4, 128)
-  MQ_G(kBF16, 8, 64) MQ_G(kBF16, 8, 32) MQ_G(kBF16, 8, 128)
-  MQ_G(kF16, 4, 64) MQ_G(kF16, 4, 32) MQ_G(kF16, 4, 128)
-  MQ_G(kF16, 8, 64) MQ_G(kF16, 8, 32) MQ_G(kF16, 8, 128)
-#undef MQ_G
-  return kStatusUnsupported;
+  return 0;
 }
 
 }  // namespace mq

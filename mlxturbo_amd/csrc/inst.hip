@@ -1,0 +1,28 @@
+// Kernel instantiations of one (dtype, bits) pair for every group size.  The
+// build compiles this file once per pair with -DMQ_INST_DT=<0|1> and
+// -DMQ_INST_BITS=<4|8>; abi.hip calls the launchers through launch.h.
+#include "launch.h"
+#include "dequant.cuh"
+#include "gather.cuh"
+#include "qmm_wide.cuh"
+#include "qmv.cuh"
+
+#if !defined(MQ_INST_DT) || !defined(MQ_INST_BITS)
+#error "compile with -DMQ_INST_DT=<0|1> -DMQ_INST_BITS=<4|8>"
+#endif
+
+namespace mq {
+
+#define MQ_INST(GS)                                                  \
+  template struct DequantLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;       \
+  template struct SkinnyLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;        \
+  template struct WideLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;          \
+  template struct GatherLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
+
+MQ_INST(32)
+MQ_INST(64)
+MQ_INST(128)
+
+#undef MQ_INST
+
+}  // namespace mq

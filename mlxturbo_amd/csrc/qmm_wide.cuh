@@ -18,7 +18,7 @@
 //  * Each weight is dequantized once per 256 output rows, so the VALU work is
 //    ~1/8 of the MFMA time; x tiles are re-read from L2 once per 128 columns.
 #pragma once
-#include "mq_common.h"
+#include "launch.h"
 
 namespace mq {
 
@@ -36,11 +36,6 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   else
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0,
                                                   0);
-}
-
-inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
-  (void)N;
-  return M > 16 && K % kWideBK == 0 && (bits == 4 || bits == 8) && gs >= 32 && gs % 32 == 0;
 }
 
 template <int DT, int BITS, int GS>
@@ -168,27 +163,18 @@ __global__ __launch_bounds__(256) void qmm_wide_kernel(const uint16_t* __restric
     }
 }
 
-inline int launch_wide(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
-                       int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype,
-                       hipStream_t st) {
+template <int DT, int BITS, int GS>
+int WideLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s, const void* b,
+                                  void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
   const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)((M + kWideBM - 1) / kWideBM));
-#define MQ_W(DT, B, G)                                                                         \
-  if (dtype == DT && bits == B && gs == G) {                                                   \
-    static const hipError_t attr = hipFuncSetAttribute(                                        \
-        reinterpret_cast<const void*>(&qmm_wide_kernel<DT, B, G>),                             \
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLds);                            \
-    if (attr != hipSuccess) return (int)attr;                                                  \
-    hipLaunchKernelGGL((qmm_wide_kernel<DT, B, G>), grid, dim3(256), kWideLds, st,             \
-                       (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b,          \
-                       (uint16_t*)out, (int)M, (int)N, (int)K);                                \
-    return 0;                                                                                  \
-  }
-  MQ_W(kBF16, 4, 64) MQ_W(kBF16, 4, 32) MQ_W(kBF16, 4, 128)
-  MQ_W(kBF16, 8, 64) MQ_W(kBF16, 8, 32) MQ_W(kBF16, 8, 128)
-  MQ_W(kF16, 4, 64) MQ_W(kF16, 4, 32) MQ_W(kF16, 4, 128)
-  MQ_W(kF16, 8, 64) MQ_W(kF16, 8, 32) MQ_W(kF16, 8, 128)
-#undef MQ_W
-  return kStatusUnsupported;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_wide_kernel<DT, BITS, GS>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLds);
+  if (attr != hipSuccess) return (int)attr;
+  hipLaunchKernelGGL((qmm_wide_kernel<DT, BITS, GS>), grid, dim3(256), kWideLds, st,
+                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b,
+                     (uint16_t*)out, (int)M, (int)N, (int)K);
+  return 0;
 }
 
 }  // namespace mq

@@ -47,7 +47,7 @@
 //    each output row is bit-identical for every M (the property the
 //    reference tests for its small-M kernel: bench/test_qmm_smallm.py:70-85).
 #pragma once
-#include "mq_common.h"
+#include "launch.h"
 
 namespace mq {
 
@@ -154,15 +154,18 @@ struct DenseRows {
 };
 
 // One 16-row weight tile (rows n0 .. n0+rows-1 of a [*, K] quantized matrix
-// whose row n0 starts at wt / st / bt) times M <= 16 A rows.  Called by every
-// thread of a 64*NW-thread workgroup with qmv_x_lds(NW, XM) (+ qmv_sb_lds(G)
-// when SBL) bytes of dynamic LDS; requires M <= XM when XM > 0, and
-// qmv_sb_fits when SBL.
+// whose row n0 starts at wt / st / bt; rows <= 0 is an empty tile that only
+// joins the barriers) times M <= 16 A rows, computed by a group of NW waves:
+// kw is the (wave-uniform) wave index in the group, gt = 64 kw + lane.  The
+// group owns qmv_x_lds(NW, XM) (+ qmv_sb_lds(G) when SBL) bytes of LDS at
+// qmv_smem and red[0 .. NW-1].  Every wave of the workgroup calls it the same
+// number of times (it holds workgroup barriers); requires M <= XM when XM >
+// 0, and qmv_sb_fits when SBL.
 template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, class Rows>
 __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char* __restrict__ st,
                                          const char* __restrict__ bt, int rows, int M, int K,
                                          const Rows& src, unsigned char* qmv_smem,
-                                         f32x4 (*red)[64]) {
+                                         f32x4 (*red)[64], int kw, int gt) {
   using Gm = QmvGeom<BITS, GS, GPL>;
   constexpr int STEPG = Gm::STEPG, STEPB = Gm::STEPB, STEPK = Gm::STEPK, NSV = Gm::NSV;
   constexpr int NL = Gm::NL, CPL = Gm::CPL, MPL = Gm::MPL, SH = Gm::SH;
@@ -178,13 +181,13 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
     u32x4 xq[XPL];
   };
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = kw;
   const int r = lane & 15, c = lane >> 4;
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const int G = K / GS;
   const uint32_t sRowB = (uint32_t)G * 2;
-  const uint32_t w_nrec = (uint32_t)(rows - 1) * rowB + STEPB;
-  const uint32_t s_nrec = (uint32_t)(rows - 1) * sRowB + STEPG * 2;
+  const uint32_t w_nrec = rows > 0 ? (uint32_t)(rows - 1) * rowB + STEPB : 0u;
+  const uint32_t s_nrec = rows > 0 ? (uint32_t)(rows - 1) * sRowB + STEPG * 2 : 0u;
   const uint32_t wofs = (uint32_t)r * rowB + (uint32_t)c * 16;
   const uint32_t sofs = (uint32_t)r * sRowB;
   // scale of load L: half ((4 L + c) >> SH) & 3 of dword pair ((4 L) >> SH) >> 2
@@ -354,13 +357,13 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   Stage S[PF];
   u32x4 sbq[2][SBL ? kQmvSbChunks : 1];
   const int cpr = G / 8;                      // 16-byte chunks per scale row (SBL)
-  const int nch = rows * cpr;                 // chunks of each of s and b
+  const int nch = max(rows, 0) * cpr;         // chunks of each of s and b
   if constexpr (SBL) {
     const auto rs0 = make_rsrc(st, (uint32_t)nch * 16u);
     const auto rb0 = make_rsrc(bt, (uint32_t)nch * 16u);
 #pragma unroll
     for (int u = 0; u < kQmvSbChunks; ++u) {
-      const uint32_t i = threadIdx.x + u * 64 * NW;
+      const uint32_t i = gt + u * 64 * NW;
       sbq[0][u] = __builtin_amdgcn_raw_buffer_load_b128(rs0, i * 16u, 0, 0);
       sbq[1][u] = __builtin_amdgcn_raw_buffer_load_b128(rb0, i * 16u, 0, 0);
     }
@@ -371,7 +374,7 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   if constexpr (SBL) {
 #pragma unroll
     for (int u = 0; u < kQmvSbChunks; ++u) {
-      const int i = threadIdx.x + u * 64 * NW;
+      const int i = gt + u * 64 * NW;
       if (i < nch) {
         const int rr = i / cpr, cc = i - rr * cpr;
         *(lds_u32x4*)(sbl_s + rr * SBS + cc * 16) = sbq[0][u];
@@ -409,7 +412,7 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   } else {
     red[wave][lane] = acc;
     __syncthreads();
-    for (int tt = threadIdx.x; tt < 256; tt += 64 * NW) {
+    for (int tt = gt; tt < 256; tt += 64 * NW) {
       const int mm = tt >> 4, nn = tt & 15;
       const int sl = ((mm >> 2) << 4) | nn, v = mm & 3;
       float sum = red[0][sl][v];
@@ -442,7 +445,36 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
       reinterpret_cast<const char*>(w) + (int64_t)n0 * rowB,
       reinterpret_cast<const char*>(scales) + (int64_t)n0 * sRowB,
       reinterpret_cast<const char*>(biases) + (int64_t)n0 * sRowB, min(16, N - n0), M, K, src,
-      qmv_smem, red);
+      qmv_smem, red, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x);
+}
+
+template <int DT, int BITS, int GS>
+int SkinnyLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
+                                    const void* b, void* out, int64_t M, int64_t N, int64_t K,
+                                    hipStream_t st) {
+  using C = QmvConf<BITS, GS>;
+  const unsigned grid = (unsigned)((N + 15) / 16);
+  const bool sbl = qmv_sb_fits(K / GS, C::NW, s, b);
+  const size_t sb_lds = qmv_sb_lds((int)(K / GS));
+  auto lds_for = [&](int xmax, bool with_sb) {
+    return qmv_x_lds<BITS, GS, C::GPL>(C::NW, xmax) + (with_sb ? sb_lds : 0);
+  };
+  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
+    const uint16_t* xp = (const uint16_t*)x + m0 * K;
+    uint16_t* op = (uint16_t*)out + m0 * N;
+    // x streams through LDS for up to 8 rows whose bytes a buffer range covers
+    const int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? qmv_xm_for(mt) : 0;
+#define MQ_SX(X, SB)                                                                        \
+    if (xm == X && sbl == SB)                                                               \
+      hipLaunchKernelGGL((qmv_kernel<DT, BITS, GS, C::GPL, C::NW, C::PF, X, SB>), dim3(grid), \
+                         dim3(64 * C::NW), lds_for(X, SB), st, xp, w, (const uint16_t*)s,   \
+                         (const uint16_t*)b, op, mt, (int)N, (int)K, (int64_t)K, (int64_t)N);
+    MQ_SX(0, true) MQ_SX(1, true) MQ_SX(2, true) MQ_SX(4, true) MQ_SX(8, true)
+    MQ_SX(0, false) MQ_SX(1, false) MQ_SX(2, false) MQ_SX(4, false) MQ_SX(8, false)
+#undef MQ_SX
+  }
+  return 0;
 }
 
 }  // namespace mq
