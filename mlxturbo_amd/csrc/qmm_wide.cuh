@@ -1,32 +1,48 @@
-// Wide (prefill) quantized matmul: out[M,N] = x[M,K] . deq(W[N,K])^T for M > 16.
+// Wide (prefill) quantized matmul: out[M,N] = x[M,K] . deq(W[N,K])^T for M > 16,
+// and the same tile over expert-grouped rows for prefill gather_qmm.
 //
 // Reference behaviour: mlxturbo/kernels/qmm_wide.py:456-502 (MLX steel
 // qmm_t with a 64-row tile), reached from fused._qmm_wide_dispatch
 // (fused.py:3477-3499) for prefill chunks; the MLX loader dequantizes each W
-// tile to T in threadgroup memory (_steel_flat.py:1324-1335).
+// tile to T in threadgroup memory (_steel_flat.py:1324-1335).  The grouped
+// form follows moe_grouped_gemm.qmm_segmented (moe_grouped_gemm.py:913-1066):
+// rows sorted by expert, each tile belongs to one expert.
 //
 // CDNA4 design (compute-bound: arithmetic intensity 1247-3483 FLOP/B at
 // M = 512..8192, above the ~312 FLOP/B ridge):
-//  * Block tile BM x BN = 256 x 128, BK = 64 codes, 256 threads (4 waves in a
-//    2 x 2 grid, 128 x 64 outputs each = 4 x 2 tiles of v_mfma_f32_32x32x16).
-//  * Per k-step the workgroup stages x[256 x 64] and the dequantized W[128 x
-//    64] (T, exact MLX dequant, one group per row per step at gs = 64) in LDS,
-//    rows padded to 144 bytes so the 8-lane groups of ds_read_b128 hit
-//    distinct banks.  Two LDS buffers: the global loads of step k+1 are in
-//    flight (registers) while step k runs its MFMAs, then are dequantized
-//    into the other buffer.
-//  * Each weight is dequantized once per 256 output rows, so the VALU work is
-//    ~1/8 of the MFMA time; x tiles are re-read from L2 once per 128 columns.
+//  * Block tile BM x 256, BK = 64 codes, 512 threads = 8 waves, two per SIMD
+//    (one wave per SIMD left the LDS reads latency-bound: measured 213 B/ns
+//    per CU with one wave per SIMD against 430 with four).  BM = 256: waves
+//    in a 4 x 2 grid of 64 x 128 outputs (2 x 4 tiles of v_mfma_f32_32x32x16);
+//    BM = 128 / 64 for shorter row counts.
+//  * Per k-step the workgroup stages x[BM x 64] and the dequantized W[256 x
+//    64] (T, exact MLX dequant) in LDS, rows padded to 144 bytes so the
+//    16-lane phases of ds_read_b128 hit distinct banks (no bank conflicts in
+//    SQ_LDS_BANK_CONFLICT).  Two LDS buffers and two register stages: the
+//    global loads of step k+2 are issued while step k runs its MFMAs and the
+//    data of step k+1, loaded a whole step earlier, is dequantized into the
+//    other buffer; the loop body is straight-line so the compiler can
+//    interleave the stores with the MFMAs.  With one register stage, 44% of
+//    wave cycles waited on global loads (SQ_WAIT_INST_ANY).
+//  * x, W, scales and biases are read with buffer loads; rows past M (or past
+//    N) are past the buffer range and read zeros, so no row clamping.
+//  * Each weight is dequantized once per BM output rows; a whole tile whose
+//    scales include |s| >= 2^100 (never in real checkpoints) takes the plain
+//    float dequantization route, chosen once per tile by a scan of its scales.
 #pragma once
+#include <type_traits>
+
 #include "launch.h"
 
 namespace mq {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kWideBM = 256, kWideBN = 128, kWideBK = 64;
+constexpr int kWideBN = 256, kWideBK = 64, kWideNT = 512;
 constexpr int kWideLD = kWideBK + 8;  // LDS row stride in 16-bit elements (144 bytes)
-constexpr size_t kWideLds = 2 * (size_t)(kWideBM + kWideBN) * kWideLD * 2;
+
+template <int BM>
+constexpr size_t wide_lds_bytes() { return 2 * (size_t)(BM + kWideBN) * kWideLD * 2; }
 
 template <int DT>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -38,143 +54,249 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                   0);
 }
 
-template <int DT, int BITS, int GS>
-__global__ __launch_bounds__(256) void qmm_wide_kernel(const uint16_t* __restrict__ x,
-                                                       const uint32_t* __restrict__ w,
-                                                       const uint16_t* __restrict__ scales,
-                                                       const uint16_t* __restrict__ biases,
-                                                       uint16_t* __restrict__ out, int M, int N,
-                                                       int K) {
-  constexpr int BM = kWideBM, BN = kWideBN, BK = kWideBK, LD = kWideLD;
-  constexpr int WCH = BK * BITS / 128;          // 16-byte weight chunks per row per step (2 or 4)
-  constexpr int WPT = BN * WCH / 256;           // weight chunks per thread (1 or 2)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
+
+// One BM x 256 output tile.  x rows come from xrsrc at per-row byte offsets
+// xrow_off(r) (past the range for rows that do not exist); w / scales /
+// biases point at the tile's first weight row, of which nrows (<= 256) exist;
+// store(r, c, v) writes row r, tile column c (< nrows) of the output.
+template <int DT, int BITS, int GS, int BM, class XRowOff, class Store>
+__device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff xrow_off,
+                                          const uint32_t* __restrict__ w,
+                                          const uint16_t* __restrict__ scales,
+                                          const uint16_t* __restrict__ biases, int nrows, int K,
+                                          Store store, uint16_t* wide_smem) {
+  constexpr int BN = kWideBN, BK = kWideBK, LD = kWideLD, NT = kWideNT;
+  constexpr int WGM = BM == 256 ? 4 : 2;        // waves along M
+  constexpr int WGN = 8 / WGM;                  // waves along N
+  constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
+  constexpr int WCH = BK * BITS / 128;          // 16-byte weight chunks per row per step
+  constexpr int WCT = BN * WCH;                 // weight chunks per step
+  static_assert(WCT % NT == 0, "whole weight chunks per thread");
+  constexpr int WPT = WCT / NT;                 // weight chunks per thread
+  constexpr int XPT = BM * 8 / NT;              // x chunks per thread
+  constexpr int XROWS = NT / 8;                 // tile rows between a thread's x chunks
   constexpr int CPC = 128 / BITS;               // codes per chunk
-  extern __shared__ __align__(16) uint16_t wide_smem[];
+  constexpr int KS = BK / 16;                   // MFMA k-substeps per step
+  static_assert(XPT >= 1 && (XPT % KS == 0 || KS % XPT == 0), "x chunks spread over substeps");
+  using T = T16<DT>;
   uint16_t* As = wide_smem;                     // [2][BM*LD]
   uint16_t* Bs = wide_smem + 2 * BM * LD;       // [2][BN*LD]
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int64_t Kw = (int64_t)K * BITS / 32;
   const int G = K / GS;
   const int nk = K / BK;
 
-  // global -> register staging of one k-step
-  u32x4 ra[8];
-  u32x4 rw[WPT];
-  uint16_t rs[WPT], rb[WPT];
-  auto gload = [&](int kt) {
+  // rows past nrows are past the weight range and read zeros
+  const auto rwd = wide_rsrc(w, (int64_t)nrows * Kw * 4);
+  const auto rsd = wide_rsrc(scales, (int64_t)nrows * G * 2);
+  const auto rbd = wide_rsrc(biases, (int64_t)nrows * G * 2);
+  uint32_t xo[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const uint32_t ro = xrow_off((t >> 3) + XROWS * i);
+    xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
+  }
+  const int xl0 = (t >> 3) * LD + 8 * (t & 7);
+  uint32_t wo[WPT], so[WPT];
+  int wl[WPT], wch[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    const int id = t + NT * i;
+    const int row = id / WCH, ch = id % WCH;
+    wo[i] = (uint32_t)(((int64_t)row * Kw + ch * CPC * BITS / 32) * 4);
+    so[i] = (uint32_t)((int64_t)min(row, nrows - 1) * G * 2);
+    wl[i] = row * LD + ch * CPC;
+    wch[i] = ch;
+  }
+
+  struct Set {
+    u32x4 xa[XPT];
+    u32x4 wv[WPT];
+    uint16_t s[WPT], b[WPT];
+  };
+  Set S0, S1;
+  auto gload = [&](Set& st, int kt) {
     const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int id = t + 256 * i;
-      const int row = id >> 3, kc = id & 7;
-      const int gm = min(m0 + row, M - 1);
-      ra[i] = *reinterpret_cast<const u32x4*>(x + (int64_t)gm * K + k0 + 8 * kc);
-    }
+    for (int i = 0; i < XPT; ++i)
+      st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, xo[i], k0 * 2, 0);
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-      const int id = t + 256 * i;
-      const int row = id / WCH, ch = id % WCH;
-      const int gn = min(n0 + row, N - 1);
-      const int kc = k0 + ch * CPC;
-      rw[i] = *reinterpret_cast<const u32x4*>(w + (int64_t)gn * Kw + (int64_t)kc * BITS / 32);
-      rs[i] = scales[(int64_t)gn * G + kc / GS];
-      rb[i] = biases[(int64_t)gn * G + kc / GS];
+      st.wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rwd, wo[i], k0 * BITS / 8, 0);
+      const uint32_t go = so[i] + 2u * (uint32_t)((k0 + wch[i] * CPC) / GS);
+      st.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rsd, go, 0, 0);
+      st.b[i] = __builtin_amdgcn_raw_buffer_load_b16(rbd, go, 0, 0);
     }
   };
-  auto sstore = [&](int buf) {
+  // part ks of storing register stage st into LDS buffer buf
+  auto spart = [&](const Set& st, int buf, int ks, auto plainc) {
+    constexpr bool PLAIN = decltype(plainc)::value;
     uint16_t* A = As + buf * BM * LD;
     uint16_t* B = Bs + buf * BN * LD;
+    if constexpr (XPT >= KS) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int id = t + 256 * i;
-      const int row = id >> 3, kc = id & 7;
-      *reinterpret_cast<u32x4*>(A + row * LD + 8 * kc) = ra[i];
+      for (int i = ks * (XPT / KS); i < (ks + 1) * (XPT / KS); ++i)
+        *reinterpret_cast<u32x4*>(A + xl0 + i * XROWS * LD) = st.xa[i];
+    } else {
+      if (ks < XPT) *reinterpret_cast<u32x4*>(A + xl0 + ks * XROWS * LD) = st.xa[ks];
     }
-    using T = T16<DT>;
+    constexpr int WW = 4 * WPT;                 // weight words per thread
 #pragma unroll
-    for (int i = 0; i < WPT; ++i) {
-      const int id = t + 256 * i;
-      const int row = id / WCH, ch = id % WCH;
-      const float sf = T::to_f32(rs[i]);
-      const GroupScale g = make_group(sf, T::to_f32(rb[i]));
-      uint32_t o[CPC / 2];
-      if (needs_plain(sf)) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) deq_word_plain<DT, BITS>(rw[i][j], g, o + j * (CPC / 8));
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) deq_word<DT, BITS>(rw[i][j], g, o + j * (CPC / 8));
-      }
-      u32x4* dst = reinterpret_cast<u32x4*>(B + row * LD + ch * CPC);
-#pragma unroll
-      for (int j = 0; j < CPC / 8; ++j) dst[j] = (u32x4){o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+    for (int q = ks * WW / KS; q < (ks + 1) * WW / KS; ++q) {
+      const int i = q / 4, j = q % 4;
+      const GroupScale g = make_group(T::to_f32(st.s[i]), T::to_f32(st.b[i]));
+      uint32_t o[CPC / 8];
+      if constexpr (PLAIN) deq_word_plain<DT, BITS>(st.wv[i][j], g, o);
+      else deq_word<DT, BITS>(st.wv[i][j], g, o);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(B + wl[i] + j * (CPC / 4));
+      if constexpr (CPC / 8 == 4) *reinterpret_cast<u32x4*>(dst) = (u32x4){o[0], o[1], o[2], o[3]};
+      else *reinterpret_cast<u32x2*>(dst) = (u32x2){o[0], o[1]};
     }
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int lr = lane & 31, lk = 8 * (lane >> 5);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-    const uint16_t* A = As + buf * BM * LD + (128 * wm + lr) * LD + lk;
-    const uint16_t* B = Bs + buf * BN * LD + (64 * wn + lr) * LD + lk;
+  auto mma = [&](int buf) {
+    const uint16_t* A = As + buf * BM * LD + (32 * TM * wm + lr) * LD + lk;
+    const uint16_t* B = Bs + buf * BN * LD + (32 * TN * wn + lr) * LD + lk;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      u32x4 a[4], b[2];
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 a[TM], b[TN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4*>(A + 32 * i * LD + 16 * ks);
+      for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const u32x4*>(A + 32 * i * LD + 16 * ks);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const u32x4*>(B + 32 * j * LD + 16 * ks);
+      for (int j = 0; j < TN; ++j) b[j] = *reinterpret_cast<const u32x4*>(B + 32 * j * LD + 16 * ks);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<DT>(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<DT>(a[i], b[j], acc[i][j]);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
-    __syncthreads();
+  };
+
+  bool big = false;
+  {
+    const uint32_t nbytes = (uint32_t)nrows * G * 2;
+    const auto rs = wide_rsrc(scales, nbytes);
+    for (uint32_t off = t * 16u; off < nbytes; off += NT * 16u) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        big |= needs_plain(T::to_f32((uint16_t)v[e])) || needs_plain(T::to_f32((uint16_t)(v[e] >> 16)));
+    }
   }
+  auto run = [&](auto plainc) {
+    auto stage_store = [&](const Set& st, int buf) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) spart(st, buf, ks, plainc);
+    };
+    gload(S0, 0);
+    gload(S1, min(1, nk - 1));
+    stage_store(S0, 0);
+    __syncthreads();
+    // The last iterations reload step nk - 1 (valid memory, unused) so the
+    // body stays free of load conditions.
+    for (int kt = 0; kt < nk; kt += 2) {
+      // buffer 0 holds step kt, S1 step kt + 1, S0 is free
+      gload(S0, min(kt + 2, nk - 1));
+      mma(0);
+      stage_store(S1, 1);
+      __syncthreads();
+      if (kt + 1 < nk) {
+        // buffer 1 holds step kt + 1, S0 step kt + 2, S1 is free
+        gload(S1, min(kt + 3, nk - 1));
+        mma(1);
+        stage_store(S0, 0);
+        __syncthreads();
+      }
+    }
+  };
+  if (__syncthreads_or(big)) run(std::integral_constant<bool, true>{});
+  else run(std::integral_constant<bool, false>{});
 
   // D[row][col] of a 32x32 tile: col = lane & 31, row = 8*(e/4) + 4*(lane>>5) + e%4
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + 64 * wn + 32 * j + lr;
+    for (int j = 0; j < TN; ++j) {
+      const int c = 32 * TN * wn + 32 * j + lr;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int row = m0 + 128 * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (row < M && col < N) out[(int64_t)row * N + col] = T16<DT>::round1(acc[i][j][e]);
+        const int r = 32 * TM * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (c < nrows) store(r, c, T::round1(acc[i][j][e]));
       }
     }
+}
+
+// Dense rows: grid (ceil(N / 256), ceil(M / BM)), 512 threads, dynamic LDS
+// wide_lds_bytes<BM>(); 256 * K * 2 < 2^31 and 256 * K * BITS / 8 < 2^31.
+template <int DT, int BITS, int GS, int BM>
+__global__ __launch_bounds__(kWideNT) void qmm_wide_kernel(const uint16_t* __restrict__ x,
+                                                           const uint32_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint16_t* __restrict__ biases,
+                                                           uint16_t* __restrict__ out, int M,
+                                                           int N, int K) {
+  extern __shared__ __align__(16) uint16_t wide_smem[];
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kWideBN;
+  const int mrows = min(BM, M - m0);
+  const int64_t G = K / GS;
+  // descriptors cover this tile's rows only: rows past M read zeros, no
+  // 64-bit offsets inside the tile
+  const auto xr = wide_rsrc(x + (int64_t)m0 * K, (int64_t)mrows * K * 2);
+  auto xrow_off = [&](int r) { return (uint32_t)r * (uint32_t)K * 2u; };
+  uint16_t* ot = out + (int64_t)m0 * N + n0;
+  auto store = [&](int r, int c, uint16_t v) {
+    if (r < mrows) ot[(int64_t)r * N + c] = v;
+  };
+  wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + (int64_t)n0 * K * BITS / 32, scales + n0 * G,
+                              biases + n0 * G, min(kWideBN, N - n0), K, store, wide_smem);
+}
+
+// Row-tile height by row count: 256-row tiles leave most of the 256 CUs idle
+// on short matrices.
+inline int wide_bm_for(int64_t M) { return M <= 64 ? 64 : M <= 128 ? 128 : 256; }
+
+template <int DT, int BITS, int GS, int BM>
+inline int wide_launch_bm(const void* x, const uint32_t* w, const void* s, const void* b,
+                          void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_wide_kernel<DT, BITS, GS, BM>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds_bytes<BM>());
+  if (attr != hipSuccess) return (int)attr;
+  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)((M + BM - 1) / BM));
+  hipLaunchKernelGGL((qmm_wide_kernel<DT, BITS, GS, BM>), grid, dim3(kWideNT),
+                     wide_lds_bytes<BM>(), st, (const uint16_t*)x, w, (const uint16_t*)s,
+                     (const uint16_t*)b, (uint16_t*)out, (int)M, (int)N, (int)K);
+  return 0;
 }
 
 template <int DT, int BITS, int GS>
 int WideLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s, const void* b,
                                   void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
-  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)((M + kWideBM - 1) / kWideBM));
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_wide_kernel<DT, BITS, GS>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLds);
-  if (attr != hipSuccess) return (int)attr;
-  hipLaunchKernelGGL((qmm_wide_kernel<DT, BITS, GS>), grid, dim3(256), kWideLds, st,
-                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b,
-                     (uint16_t*)out, (int)M, (int)N, (int)K);
-  return 0;
+  // one tile's x rows and weight rows must fit a 31-bit buffer range
+  if (K * 2 * 256 >= ((int64_t)1 << 31) || M > ((int64_t)1 << 31) / 256 * 256)
+    return kStatusUnsupported;
+  switch (wide_bm_for(M)) {
+    case 64: return wide_launch_bm<DT, BITS, GS, 64>(x, w, s, b, out, M, N, K, st);
+    case 128: return wide_launch_bm<DT, BITS, GS, 128>(x, w, s, b, out, M, N, K, st);
+    default: return wide_launch_bm<DT, BITS, GS, 256>(x, w, s, b, out, M, N, K, st);
+  }
 }
 
 }  // namespace mq
