@@ -189,6 +189,37 @@ def measure_gather(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, n
             "distinct_experts": round(uniq, 1)}
 
 
+def measure_gather_prefill(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, seed=5):
+    """The prefill form of configs[3]: T tokens x top_k experts as one
+    gather_qmm (x (P, 1, K) sorted by expert, sorted_indices=True, as mlx-lm's
+    _gather_sort does); runs the expert-grouped MFMA tile kernel.  Reported
+    as dense-equivalent TFLOP/s (2 * P * N * K per call)."""
+    rng = np.random.default_rng(seed + T)
+    idx = (zipf_routing(rng, T, top_k, E) if routing == "zipf" else
+           np.stack([rng.choice(E, size=top_k, replace=False) for _ in range(T)]).astype(np.int32))
+    (w, s, b), = make_weights(torch, E * N, K, 1, seed=seed)
+    w, s, b = w.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
+    flat = idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((T, 1, K), device="cuda", generator=g).to(torch.bfloat16)
+    xs = x[torch.from_numpy(order // top_k).cuda()].contiguous()
+    rhs = torch.from_numpy(flat[order].copy()).cuda()
+    P = T * top_k
+
+    def fn(i):
+        mq.gather_qmm(xs, w, s, b, rhs_indices=rhs, sorted_indices=True)
+
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    del w, s, b
+    torch.cuda.empty_cache()
+    tflops = 2.0 * P * N * K / per_step / 1e12
+    return {"us": round(per_step * 1e6, 2), "TFLOPs": round(tflops, 1),
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "distinct_experts": int(len(np.unique(flat)))}
+
+
 def measure_dequant(torch, mq, N, K, steps, warmup):
     R = copies_for(N * K // 2)
     ws = make_weights(torch, N, K, R, seed=7)
@@ -297,6 +328,11 @@ def main():
                 for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
                     sweep[f"gather_{name}_{routing}_T{T}"] = measure_gather(
                         torch, mq, T, NN, KK, routing, 100, 5)
+        # config 4 banks at prefill width (2048 tokens): expert-grouped MFMA tiles
+        for routing in ("zipf", "uniform"):
+            for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
+                sweep[f"gather_prefill_{name}_{routing}_T2048"] = measure_gather_prefill(
+                    torch, mq, 2048, NN, KK, routing, 20, 3)
         sweep["dequant_b4_K5120_N17408"] = measure_dequant(torch, mq, N, K, 50, 3)
 
     cpu = None if args.no_cpu else cpu_baseline(N, K, args.cpu_seconds)

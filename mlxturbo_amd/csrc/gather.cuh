@@ -24,6 +24,7 @@
 // Pairs with an out-of-range expert or x index produce zero rows.
 #pragma once
 #include "launch.h"
+#include "qmm_wide.cuh"
 #include "qmv.cuh"
 
 namespace mq {
@@ -293,6 +294,50 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   }
 }
 
+// Prefill gather_qmm: prep tables with segments of BM / M pairs, then the
+// expert-grouped MFMA tile kernel.  The row-tile height follows the expected
+// rows per expert (thin experts waste most of a tall tile).
+template <int DT, int BITS, int GS, int BM>
+inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, const void* b,
+                             const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
+                             int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
+                             hipStream_t st, int* nlaunch) {
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_grouped_kernel<DT, BITS, GS, BM>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds_bytes<BM>());
+  if (attr != hipSuccess) return (int)attr;
+  const int R = (int)(BM / M);
+  const size_t shmem = 4 * sizeof(int) * (size_t)(E + 1);
+  hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, lhs, (int)P, (int)E,
+                     (int)B, R, (int32_t*)ws);
+  const int64_t bound = (P + R - 1) / R + E + 1;
+  const int64_t segs = bound < P ? bound : P;
+  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)segs);
+  hipLaunchKernelGGL((qmm_grouped_kernel<DT, BITS, GS, BM>), grid, dim3(kWideNT),
+                     wide_lds_bytes<BM>(), st, (const uint16_t*)x, w, (const uint16_t*)s,
+                     (const uint16_t*)b, lhs, (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B,
+                     (int)M, (int)N, (int)K, (int)E);
+  *nlaunch += 2;
+  return 0;
+}
+
+template <int DT, int BITS, int GS>
+inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const void* b,
+                          const int32_t* lhs, const int32_t* rhs, void* out, int64_t P, int64_t B,
+                          int64_t M, int64_t N, int64_t K, int64_t E, void* ws, hipStream_t st,
+                          int* nlaunch) {
+  const int64_t active = P < E ? P : E;
+  const int64_t rows_per_expert = P * M / (active > 0 ? active : 1);
+  if (rows_per_expert >= 192)
+    return launch_grouped_bm<DT, BITS, GS, 256>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
+                                                st, nlaunch);
+  if (rows_per_expert >= 96)
+    return launch_grouped_bm<DT, BITS, GS, 128>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
+                                                st, nlaunch);
+  return launch_grouped_bm<DT, BITS, GS, 64>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
+                                             nlaunch);
+}
+
 template <int DT, int BITS, int GS>
 int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
                                     const void* b, const int32_t* lhs, const int32_t* rhs,
@@ -301,6 +346,10 @@ int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void
                                     int* nlaunch) {
   if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
   if ((N + 15) / 16 > 65535) return kStatusUnsupported;
+  if (P * M >= kGroupedMinRows && E <= kGatherPrepMaxE && K % kWideBK == 0 &&
+      B * M * K * 2 < ((int64_t)1 << 31) && 256 * K * 2 < ((int64_t)1 << 31))
+    return launch_grouped<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
+                                        nlaunch);
   using C = QmvConf<BITS, GS>;
   using Gm = QmvGeom<BITS, GS, C::GPL>;
   // Segments of up to R pairs; R * M <= 8 A rows stream x through LDS, one

@@ -50,16 +50,19 @@ inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 
 // gather_qmm: up to kGatherFusedMaxP pairs are grouped by expert inside the
 // matmul kernel; more pairs go through a counting-sort prep kernel (experts
-// up to kGatherPrepMaxE) that fills a caller-provided workspace.
+// up to kGatherPrepMaxE) that fills a caller-provided workspace.  Calls with
+// at least kGroupedMinRows output rows (P * M, prefill) run the expert-grouped
+// MFMA tile kernel on the same prep tables (the reference's prefill switch,
+// fused.py:3122-3133, is at 1024 rows as well).
 constexpr int kGatherFusedMaxP = 256;
 constexpr int kGatherPrepMaxE = 2048;
+constexpr int64_t kGroupedMinRows = 1024;
 
 // Workspace (int32): [0] nseg | perm[P] | seg_start[P] | seg_len[P] | seg_expert[P]
 __host__ __device__ inline size_t gather_ws_words(int64_t P) { return 1 + 4 * (size_t)P; }
 
 inline size_t gather_workspace_bytes(int64_t P, int64_t M) {
-  (void)M;
-  if (P <= kGatherFusedMaxP) return 0;
+  if (P <= kGatherFusedMaxP && P * M < kGroupedMinRows) return 0;
   return (gather_ws_words(P) * 4 + 255) & ~(size_t)255;
 }
 

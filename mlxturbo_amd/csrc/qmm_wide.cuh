@@ -268,6 +268,60 @@ __global__ __launch_bounds__(kWideNT) void qmm_wide_kernel(const uint16_t* __res
                               biases + n0 * G, min(kWideBN, N - n0), K, store, wide_smem);
 }
 
+// Expert-grouped rows (prefill gather_qmm, reference moe_grouped_gemm.py:
+// 913-1066): grid (ceil(N / 256), segment bound), 512 threads, dynamic LDS
+// wide_lds_bytes<BM>().  Segment s of the prep tables in ws holds up to BM / Mi
+// pairs of one expert (pairs sorted by expert); pair p contributes rows
+// p*Mi .. p*Mi+Mi-1 of the output and reads x batch lhs[p] (or p).  Segments
+// of out-of-range experts write zeros.  B * Mi * K * 2 < 2^31.
+template <int DT, int BITS, int GS, int BM>
+__global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
+    int P, int B, int Mi, int N, int K, int E) {
+  extern __shared__ __align__(16) uint16_t wide_smem[];
+  __shared__ uint32_t s_xoff[BM];
+  __shared__ int s_orow[BM];
+  const int seg = blockIdx.y, n0 = blockIdx.x * kWideBN;
+  if (seg >= ws[0]) return;
+  const int32_t* perm = ws + 1;
+  const int st0 = perm[P + seg], len = perm[2 * P + seg], e = perm[3 * P + seg];
+  const int rows = len * Mi;                      // <= BM
+  const int t = threadIdx.x;
+  for (int r = t; r < BM; r += kWideNT) {
+    if (r < rows) {
+      const int p = perm[st0 + r / Mi], mi = r % Mi;
+      const int xb = lhs ? lhs[p] : p;
+      s_xoff[r] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
+      s_orow[r] = p * Mi + mi;
+    } else {
+      s_xoff[r] = 0xffffffffu;
+      s_orow[r] = -1;
+    }
+  }
+  __syncthreads();
+  const int ncols = min(kWideBN, N - n0);
+  if (e >= E) {
+    for (int i = t; i < rows * ncols; i += kWideNT) {
+      const int r = i / ncols, c = i - r * ncols;
+      out[(int64_t)s_orow[r] * N + n0 + c] = 0;
+    }
+    return;
+  }
+  const int64_t G = K / GS;
+  const int64_t wrow = (int64_t)e * N + n0;
+  const auto xr = wide_rsrc(x, (int64_t)B * Mi * K * 2);
+  auto xrow_off = [&](int r) { return s_xoff[r]; };
+  uint16_t* ot = out + n0;
+  auto store = [&](int r, int c, uint16_t v) {
+    const int o = s_orow[r];
+    if (o >= 0) ot[(int64_t)o * N + c] = v;
+  };
+  wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + wrow * K * BITS / 32, scales + wrow * G,
+                              biases + wrow * G, ncols, K, store, wide_smem);
+}
+
 // Row-tile height by row count: 256-row tiles leave most of the 256 CUs idle
 // on short matrices.
 inline int wide_bm_for(int64_t M) { return M <= 64 ? 64 : M <= 128 ? 128 : 256; }

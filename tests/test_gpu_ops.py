@@ -386,3 +386,55 @@ def test_gather_large_batch_prep_path(M):
     assert out.shape == (T, top, M, N)
     ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, np.repeat(np.arange(T), top), idx.reshape(-1))
     _check(out.reshape(T * top, M, N), ref)
+
+
+@pytest.mark.parametrize("M,bits,gs", [(1, 4, 64), (2, 4, 64), (1, 8, 64), (3, 4, 32)])
+def test_gather_prefill_grouped(M, bits, gs):
+    """P * M >= 1024 rows: the expert-grouped MFMA tile kernel (prefill
+    gather_qmm, moe_grouped_gemm.qmm_segmented's role); ragged N, zipf
+    routing so experts get from one to hundreds of rows."""
+    rng = np.random.default_rng(21 + M + bits)
+    E, N, K, T, top = 16, 320, 1024, 300, 4
+    banks = [quantized(rng, N, K, gs=gs, bits=bits) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    idx = zipf_routing(rng, T, top, E)
+    x = act(rng, (T, 1, M, K))
+    n0 = mq.launch_count()
+    out = mq.gather_qmm(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                        to_dev(b, "bfloat16"), rhs_indices=torch.from_numpy(idx).cuda(),
+                        group_size=gs, bits=bits)
+    assert mq.launch_count() > n0
+    assert out.shape == (T, top, M, N)
+    ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, np.repeat(np.arange(T), top),
+                           idx.reshape(-1), group_size=gs, bits=bits)
+    _check(out.reshape(T * top, M, N), ref)
+
+
+def test_gather_prefill_grouped_invalid_and_sorted():
+    """Grouped path: out-of-range experts give zero rows; sorted input (mlx-lm
+    _gather_sort) gives bit-identical per-pair rows."""
+    rng = np.random.default_rng(31)
+    E, N, K, T, top = 8, 256, 512, 400, 4
+    banks = [quantized(rng, N, K) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    dev = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    idx = zipf_routing(rng, T, top, E).astype(np.int32)
+    idx[5, 1] = -1
+    idx[17, 0] = E
+    x = act(rng, (T, 1, 1, K))
+    xd = to_dev(x, "bfloat16")
+    out = mq.gather_qmm(xd, *dev, rhs_indices=torch.from_numpy(idx).cuda())
+    o = from_dev(out).reshape(T * top, N)
+    flat = idx.reshape(-1)
+    bad = (flat < 0) | (flat >= E)
+    assert np.all(o[bad] == 0)
+    ok = np.nonzero(~bad)[0]
+    ref = O.gather_qmm_ref(x.reshape(T, 1, K), w, s, b, ok // top, flat[ok])
+    _check(out.reshape(T * top, 1, N)[torch.from_numpy(ok).cuda()], ref)
+    order = np.argsort(flat, kind="stable")
+    xs = xd.reshape(T, 1, K)[torch.from_numpy(order // top).cuda()]
+    out_s = bits16(mq.gather_qmm(xs, *dev, rhs_indices=torch.from_numpy(flat[order]).cuda(),
+                                 sorted_indices=True))
+    np.testing.assert_array_equal(out_s.reshape(T * top, N), bits16(out).reshape(T * top, N)[order])
