@@ -6,10 +6,17 @@ hand-written HIP kernels behind a C ABI (``include/mlxturbo_amd.h``):
 * :func:`quantized_matmul` - decode (M=1), verify (M=2..16) and prefill widths
 * :func:`gather_qmm`       - MoE expert gather
 * :func:`dequantize`       - bit-exact MLX affine dequantization
+
+Module level (:mod:`mlxturbo_amd.nn`, :mod:`mlxturbo_amd.dispatch`): torch
+``QuantizedLinear`` / ``QuantizedSwitchLinear`` / ``SwitchGLU`` on MLX-format
+tensors, and the reference's shape-by-M route table with per-instance and
+class-level enabling.
 """
 
+from . import dispatch, nn
 from .ops import dequantize, gather_qmm, launch_count, quantized_matmul
 
 __version__ = "0.1.0"
 
-__all__ = ["dequantize", "gather_qmm", "launch_count", "quantized_matmul", "__version__"]
+__all__ = ["dequantize", "dispatch", "gather_qmm", "launch_count", "nn", "quantized_matmul",
+           "__version__"]

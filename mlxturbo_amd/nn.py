@@ -1,0 +1,155 @@
+"""Module-level drop-in: MLX-format quantized layers as torch modules.
+
+Torch counterparts of the layers the reference routes through its kernels:
+
+* :class:`QuantizedLinear` - ``mlx.nn.QuantizedLinear`` (MLX-format ``weight``
+  uint32 ``[N, K*bits/32]``, ``scales``/``biases`` ``[N, K/group_size]``,
+  optional ``bias``), whose forward is ``quantized_matmul(x, w, s, b,
+  transpose=True)`` plus ``bias``.
+* :class:`QuantizedSwitchLinear` / :class:`SwitchGLU` - mlx-lm's expert banks
+  ``[E, N, K*bits/32]`` applied per (token, expert) pair with ``gather_qmm``
+  (reference call sites: mlxturbo/fused.py:2389-2394, 3105-3116;
+  qwen4_exp.py:1795-1802), including the ``_gather_sort`` path that sorts
+  pairs by expert and passes ``sorted_indices=True`` (fused.py:2402-2418).
+
+Every forward runs the HIP kernels; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import ops
+
+
+def _check_quantized(weight: torch.Tensor, scales: torch.Tensor,
+                     biases: Optional[torch.Tensor], group_size: int, bits: int) -> int:
+    if weight.dtype != torch.uint32 and weight.dtype != torch.int32:
+        raise ValueError(f"weight must hold packed uint32 words, got {weight.dtype}")
+    k = weight.shape[-1] * 32 // bits
+    if scales.shape[-1] * group_size != k:
+        raise ValueError(
+            f"scales last dim {scales.shape[-1]} x group_size {group_size} != K={k}")
+    if biases is not None and biases.shape != scales.shape:
+        raise ValueError("biases must have the shape of scales")
+    return k
+
+
+class QuantizedLinear(torch.nn.Module):
+    """``mlx.nn.QuantizedLinear`` on MLX-format tensors (affine mode).
+
+    Parameters are registered as buffers under MLX's names (``weight``,
+    ``scales``, ``biases``, ``bias``) so weights loaded from an MLX checkpoint
+    keep their keys.
+    """
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor,
+                 biases: Optional[torch.Tensor], bias: Optional[torch.Tensor] = None,
+                 group_size: int = 64, bits: int = 4, mode: str = "affine"):
+        super().__init__()
+        self.input_dims = _check_quantized(weight, scales, biases, group_size, bits)
+        self.output_dims = weight.shape[0]
+        self.group_size = group_size
+        self.bits = bits
+        self.mode = mode
+        self.register_buffer("weight", weight)
+        self.register_buffer("scales", scales)
+        self.register_buffer("biases", biases)
+        self.register_buffer("bias", bias)
+
+    def quantized_forward(self, x: torch.Tensor) -> torch.Tensor:
+        out = ops.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
+                                   group_size=self.group_size, bits=self.bits, mode=self.mode)
+        if self.bias is not None:
+            out = out + self.bias
+        return out
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.quantized_forward(x)
+
+    def extra_repr(self) -> str:
+        return (f"input_dims={self.input_dims}, output_dims={self.output_dims}, "
+                f"group_size={self.group_size}, bits={self.bits}, mode={self.mode!r}")
+
+
+class QuantizedSwitchLinear(torch.nn.Module):
+    """mlx-lm's ``QuantizedSwitchLinear``: an expert bank applied per index.
+
+    ``forward(x, indices, sorted_indices=False)`` with ``x`` ``(..., M, K)``
+    (mlx-lm expands tokens to ``(T, 1, 1, K)``) and ``indices`` ``(T, top_k)``
+    returns ``(T, top_k, M, N)``.
+    """
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor,
+                 biases: Optional[torch.Tensor], bias: Optional[torch.Tensor] = None,
+                 group_size: int = 64, bits: int = 4, mode: str = "affine"):
+        super().__init__()
+        if weight.ndim != 3:
+            raise ValueError("an expert bank weight is [E, N, K*bits/32]")
+        self.input_dims = _check_quantized(weight, scales, biases, group_size, bits)
+        self.num_experts, self.output_dims = weight.shape[0], weight.shape[1]
+        self.group_size = group_size
+        self.bits = bits
+        self.mode = mode
+        self.register_buffer("weight", weight)
+        self.register_buffer("scales", scales)
+        self.register_buffer("biases", biases)
+        self.register_buffer("bias", bias)
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor,
+                sorted_indices: bool = False) -> torch.Tensor:
+        out = ops.gather_qmm(x, self.weight, self.scales, self.biases, rhs_indices=indices,
+                             transpose=True, group_size=self.group_size, bits=self.bits,
+                             mode=self.mode, sorted_indices=sorted_indices)
+        if self.bias is not None:
+            # bias [E, N] per expert, broadcast over the M rows of each pair
+            out = out + self.bias[indices.long()].unsqueeze(-2)
+        return out
+
+
+class SwitchGLU(torch.nn.Module):
+    """mlx-lm's ``SwitchGLU``: ``down(silu(gate(x)) * up(x))`` over the top-k
+    experts of each token, with the ``_gather_sort`` reordering for long
+    inputs (pairs sorted by expert once, then unsorted at the end, as
+    mlx-lm does at 64+ indices: fused.py:2402-2418)."""
+
+    SORT_THRESHOLD = 64
+
+    def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
+                 down_proj: QuantizedSwitchLinear):
+        super().__init__()
+        self.gate_proj = gate_proj
+        self.up_proj = up_proj
+        self.down_proj = down_proj
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        # x: (..., K), indices: (..., top_k) -> (..., top_k, K_out)
+        lead = x.shape[:-1]
+        top_k = indices.shape[-1]
+        xe = x.reshape(-1, 1, 1, x.shape[-1])                      # (T, 1, 1, K)
+        idx = indices.reshape(-1, top_k)
+        do_sort = idx.numel() >= self.SORT_THRESHOLD
+        if do_sort:
+            flat = idx.reshape(-1)
+            order = torch.argsort(flat, stable=True)
+            inv = torch.argsort(order)
+            xe = xe.reshape(-1, 1, x.shape[-1])[order // top_k].unsqueeze(-2)  # (P, 1, 1, K)
+            idx_use = flat[order].reshape(-1, 1)
+        else:
+            idx_use = idx
+        g = self.gate_proj(xe, idx_use, sorted_indices=do_sort)
+        u = self.up_proj(xe, idx_use, sorted_indices=do_sort)
+        # SwiGLU in T as MLX evaluates it: each op in float, rounded to T
+        act = torch.nn.functional.silu(g.float()).to(g.dtype)
+        h = (act.float() * u.float()).to(g.dtype)
+        y = self.down_proj(h, idx_use, sorted_indices=do_sort)  # (T or P, k, 1, N)
+        if do_sort:
+            y = y.reshape(-1, y.shape[-1])[inv].reshape(*lead, top_k, y.shape[-1])
+        else:
+            y = y.reshape(*lead, top_k, y.shape[-1])
+        return y
+
+
+__all__ = ["QuantizedLinear", "QuantizedSwitchLinear", "SwitchGLU"]

@@ -1,0 +1,168 @@
+"""Module-level drop-in: route table, per-instance class swap, dispatch scope,
+class-level patch (reference: mlxturbo/kernels/dispatch.py:59-466,
+fast_qmm.py:395-472), and the torch QuantizedLinear / SwitchGLU modules.
+
+Routing logic runs on the CPU (module tensors stay on the CPU and nothing is
+computed); the forward passes are GPU tests against the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mlxturbo_amd as mq
+from mlxturbo_amd import dispatch
+from mlxturbo_amd.nn import QuantizedLinear, QuantizedSwitchLinear, SwitchGLU
+from oracle import oracle as O
+from qmm_helpers import act, bits16, from_dev, quantized, to_dev, zipf_routing
+
+
+def _layer(N=64, K=128, device="cpu", bias=False):
+    rng = np.random.default_rng(0)
+    w, s, b = quantized(rng, N, K)
+    return QuantizedLinear(to_dev(w, device=device), to_dev(s, "bfloat16", device),
+                           to_dev(b, "bfloat16", device),
+                           bias=(torch.zeros(N, dtype=torch.bfloat16, device=device)
+                                 if bias else None))
+
+
+def test_select_route_table():
+    # measured geometries: skinny at every verify width, wide past 16 rows
+    assert dispatch.select_route(5120, 17408, 1) == dispatch.SKINNY
+    assert dispatch.select_route(5120, 17408, 16) == dispatch.SKINNY
+    assert dispatch.select_route(5120, 17408, 17) == dispatch.WIDE
+    assert dispatch.select_route(17408, 5120, 8) == dispatch.SKINNY
+    # unknown geometry, M = 0 and negative widths: stock
+    assert dispatch.select_route(1000, 1000, 4) == dispatch.STOCK
+    assert dispatch.select_route(5120, 17408, 0) == dispatch.STOCK
+    assert dispatch.select_route(5120, 17408, -1) == dispatch.STOCK
+    # caller tables override; invalid route names are rejected
+    assert dispatch.select_route(8, 8, 2, {(8, 8): ("stock", "wide", "skinny")}) == "skinny"
+    with pytest.raises(ValueError):
+        dispatch.select_route(8, 8, 1, {(8, 8): ("stock", "bogus")})
+
+
+def test_enable_swaps_class_in_place():
+    model = torch.nn.Sequential(_layer(), torch.nn.ReLU(), _layer(bias=True))
+    first = model[0]
+    w = first.weight
+    keys = sorted(model.state_dict().keys())
+    dispatch.enable(model)
+    assert model[0] is first and model[0].weight is w
+    assert type(model[0]) is dispatch.DispatchedQuantizedLinear
+    assert type(model[2]) is dispatch.DispatchedQuantizedLinear
+    assert sorted(model.state_dict().keys()) == keys
+    assert model[0]._mq_dispatch_always is True
+    dispatch.enable(model, active=False)                 # idempotent, flips the flag
+    assert type(model[0]) is dispatch.DispatchedQuantizedLinear
+    assert model[0]._mq_dispatch_always is False
+    dispatch.disable(model)
+    assert type(model[0]) is QuantizedLinear and model[0] is first
+
+
+def test_dispatch_scope_flag():
+    assert not dispatch._DISPATCH_ACTIVE.get()
+    with dispatch.dispatch_scope():
+        assert dispatch._DISPATCH_ACTIVE.get()
+        with dispatch.dispatch_scope():
+            assert dispatch._DISPATCH_ACTIVE.get()
+        assert dispatch._DISPATCH_ACTIVE.get()
+    assert not dispatch._DISPATCH_ACTIVE.get()
+
+
+def test_class_patch_is_reversible():
+    orig = QuantizedLinear.forward
+    dispatch.enable_class()
+    assert QuantizedLinear.forward is not orig
+    dispatch.enable_class()                               # idempotent
+    dispatch.disable_class()
+    assert QuantizedLinear.forward is orig
+
+
+def test_module_validation():
+    rng = np.random.default_rng(1)
+    w, s, b = quantized(rng, 32, 128)
+    with pytest.raises(ValueError):
+        QuantizedLinear(torch.from_numpy(w.view(np.int32)).float(), to_dev(s, "bfloat16", "cpu"),
+                        to_dev(b, "bfloat16", "cpu"))
+    with pytest.raises(ValueError):
+        QuantizedLinear(to_dev(w, device="cpu"), to_dev(s, "bfloat16", "cpu"),
+                        to_dev(b, "bfloat16", "cpu"), group_size=32)
+    with pytest.raises(ValueError):
+        QuantizedSwitchLinear(to_dev(w, device="cpu"), to_dev(s, "bfloat16", "cpu"),
+                              to_dev(b, "bfloat16", "cpu"))
+
+
+def test_forward_without_gpu_fails_loudly():
+    layer = _layer()
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        layer(x)
+
+
+# ------------------------------------------------------------------ GPU
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_dispatched_forward_matches_operator(M):
+    rng = np.random.default_rng(40 + M)
+    N, K = 192, 512
+    w, s, b = quantized(rng, N, K)
+    bias = act(rng, (N,))
+    layer = QuantizedLinear(to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"),
+                            bias=to_dev(bias, "bfloat16"))
+    x = to_dev(act(rng, (2, M, K)), "bfloat16")
+    want = bits16(mq.quantized_matmul(x, layer.weight, layer.scales, layer.biases) + layer.bias)
+    base = bits16(layer(x))
+    np.testing.assert_array_equal(base, want)
+    dispatch.enable(layer, active=False)
+    np.testing.assert_array_equal(bits16(layer(x)), want)          # outside the scope
+    with dispatch.dispatch_scope():
+        np.testing.assert_array_equal(bits16(layer(x)), want)
+    # a table routing wide inputs through 16-row skinny launches: each row is
+    # bit-identical to the one-row result (the skinny kernel's property)
+    table = {(K, N): tuple(["stock"] + ["skinny"] * 64)}
+    got = bits16(dispatch.quantized_matmul(x, layer.weight, layer.scales, layer.biases,
+                                           group_size=64, bits=4, table=table))
+    one = bits16(mq.quantized_matmul(x[:1, :1], layer.weight, layer.scales, layer.biases))
+    np.testing.assert_array_equal(got[0, 0], one[0, 0])
+    assert got.shape == (2, M, N)
+    dispatch.disable(layer)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [3, 40])
+def test_switch_glu_matches_composition(T):
+    """SwitchGLU = down(silu(gate(x)) * up(x)) per (token, expert), unsorted
+    below 64 pairs and through the sort/unsort path above."""
+    rng = np.random.default_rng(50 + T)
+    E, H, I, top = 8, 256, 128, 4
+    def bank(N, K):
+        parts = [quantized(rng, N, K) for _ in range(E)]
+        return [np.stack([p[i] for p in parts]) for i in range(3)]
+    g, u, d = bank(I, H), bank(I, H), bank(H, I)
+    mods = [QuantizedSwitchLinear(to_dev(t[0]), to_dev(t[1], "bfloat16"), to_dev(t[2], "bfloat16"))
+            for t in (g, u, d)]
+    glu = SwitchGLU(*mods)
+    idx = zipf_routing(rng, T, top, E)
+    x = act(rng, (T, H))
+    y = glu(to_dev(x, "bfloat16"), torch.from_numpy(idx).cuda())
+    assert y.shape == (T, top, H)
+    lhs = np.repeat(np.arange(T), top)
+    xg = x.reshape(T, 1, H)
+    gg = O.gather_qmm_ref(xg, *g, lhs, idx.reshape(-1))        # (P, 1, I) fp32
+    uu = O.gather_qmm_ref(xg, *u, lhs, idx.reshape(-1))
+    # the module rounds gate/up outputs and each SwiGLU op to bf16
+    gb = O.to_f32(O.from_f32(gg, "bfloat16"), "bfloat16")
+    ub = O.to_f32(O.from_f32(uu, "bfloat16"), "bfloat16")
+    silu = gb / (1.0 + np.exp(-gb.astype(np.float64)))
+    a = O.to_f32(O.from_f32(silu.astype(np.float32), "bfloat16"), "bfloat16")
+    h = O.from_f32((a * ub).astype(np.float32), "bfloat16")
+    ref = O.gather_qmm_ref(h.reshape(T * top, 1, I), *d, np.arange(T * top), idx.reshape(-1))
+    res = O.check_output(from_dev(y).reshape(T * top, 1, H), ref)
+    # gate/up rounding differences propagate through SiLU: allow the
+    # tolerance of a second bf16 stage
+    assert res["rel_l2"] < 1e-2, res
