@@ -54,7 +54,33 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--copy-probe", type=int, default=0,
                    help="run a plain copy of this many bytes first (counter calibration)")
+    p.add_argument("--case", default="",
+                   help="run one sweep case only and print its result (for profiling): "
+                        "wide<M> (configs[2]), gather_<proj>_<routing>_T<T> (configs[3] decode), "
+                        "gather_prefill_<proj>_<routing> (2048 tokens)")
     return p.parse_args()
+
+
+def run_case(torch, mq, case: str) -> dict:
+    """One sweep entry by name, so a profiler sees only its kernels."""
+    K, N = 5120, 17408
+    banks = {"gate_up": (1024, 2048), "down": (2048, 512)}
+    if case.startswith("wide"):
+        M = int(case[4:])
+        r = measure_qmm(torch, mq, M, N, K, 4, 20, 3, copies=2)
+        tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
+        return {"case": case, "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
+                "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    if case.startswith("gather_prefill_"):
+        proj, routing = case[len("gather_prefill_"):].rsplit("_", 1)
+        NN, KK = banks[proj]
+        return {"case": case, **measure_gather_prefill(torch, mq, 2048, NN, KK, routing, 20, 3)}
+    if case.startswith("gather_"):
+        body, t = case[len("gather_"):].rsplit("_T", 1)
+        proj, routing = body.rsplit("_", 1)
+        NN, KK = banks[proj]
+        return {"case": case, **measure_gather(torch, mq, int(t), NN, KK, routing, 100, 5)}
+    raise SystemExit(f"unknown --case {case!r}")
 
 
 def copies_for(nbytes: int, requested: int = 0) -> int:
@@ -298,6 +324,9 @@ def main():
 
     if args.copy_probe:
         copy_probe(torch, args.copy_probe)
+    if args.case:
+        print(json.dumps(run_case(torch, mq, args.case)))
+        return
     K, N = 5120, 17408
     head = measure_qmm(torch, mq, 1, N, K, 4, args.steps, args.warmup, args.copies)
     value = head["GBps"]

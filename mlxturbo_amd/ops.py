@@ -176,6 +176,27 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_LHS_CACHE: dict = {}
+
+
+def _default_lhs(dev: torch.device, bx: tuple, shape: tuple) -> Optional[torch.Tensor]:
+    """x's own batch index per pair (lhs_indices=None), flattened over the
+    broadcast shape; None when that is the identity (the C ABI's NULL lhs).
+    Cached per shape: building it costs two small kernels per call."""
+    if tuple(bx) == tuple(shape):
+        return None
+    key = (dev.type, dev.index, tuple(bx), tuple(shape))
+    t = _LHS_CACHE.get(key)
+    if t is None:
+        B = math.prod(bx)
+        t = (torch.arange(B, device=dev, dtype=torch.int32).reshape(bx).expand(shape)
+             .reshape(-1).contiguous())
+        if len(_LHS_CACHE) > 64:
+            _LHS_CACHE.clear()
+        _LHS_CACHE[key] = t
+    return t
+
+
 def _as_index(t, dev) -> torch.Tensor:
     if not isinstance(t, torch.Tensor):
         t = torch.as_tensor(t)
@@ -212,14 +233,14 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     bw = tuple(w.shape[:-2])
     B = math.prod(bx)
     E = math.prod(bw)
-    lhs = (torch.arange(B, device=dev, dtype=torch.int32).reshape(bx) if lhs_indices is None
-           else _as_index(lhs_indices, dev))
+    lhs = None if lhs_indices is None else _as_index(lhs_indices, dev)
     rhs = (torch.arange(E, device=dev, dtype=torch.int32).reshape(bw) if rhs_indices is None
            else _as_index(rhs_indices, dev))
+    lshape = bx if lhs is None else tuple(lhs.shape)
     try:
-        shape = torch.broadcast_shapes(lhs.shape, rhs.shape)
+        shape = torch.broadcast_shapes(lshape, rhs.shape)
     except RuntimeError as exc:
-        raise ValueError(f"lhs_indices {tuple(lhs.shape)} and rhs_indices "
+        raise ValueError(f"lhs_indices {lshape} and rhs_indices "
                          f"{tuple(rhs.shape)} do not broadcast") from exc
     P = math.prod(shape)
     out = torch.empty((*shape, M, N), dtype=x.dtype, device=dev)
@@ -227,7 +248,8 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         return out
     if M > 16:
         raise NotImplementedError(f"gather_qmm with M={M} rows per pair (> 16)")
-    lhs_f = lhs.expand(shape).reshape(-1).to(torch.int32).contiguous()
+    lhs_f = (_default_lhs(dev, bx, tuple(shape)) if lhs is None
+             else lhs.expand(shape).reshape(-1).to(torch.int32).contiguous())
     rhs_f = rhs.expand(shape).reshape(-1).to(torch.int32).contiguous()
     x_ = _aligned(x.reshape(B, M, K))
     w_ = _aligned(w.reshape(E, N, w.shape[-1]))
@@ -237,7 +259,8 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     nbytes = int(lib.mq_gather_qmm_workspace_size(P, M))
     ws = _workspace(dev, nbytes) if nbytes else None
     rc = lib.mq_gather_qmm(x_.data_ptr(), w_.data_ptr(), s_.data_ptr(), b_.data_ptr(),
-                           lhs_f.data_ptr(), rhs_f.data_ptr(), out.data_ptr(), P, B, M, N, K, E,
+                           lhs_f.data_ptr() if lhs_f is not None else None,
+                           rhs_f.data_ptr(), out.data_ptr(), P, B, M, N, K, E,
                            group_size, bits, code, int(bool(sorted_indices)),
                            ws.data_ptr() if ws is not None else None,
                            ws.numel() if ws is not None else 0, _stream_ptr(out))
