@@ -132,8 +132,11 @@ class _FakeLib:
                       sorted_, ws, wsb, stream):
         read = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
                                                shape=(P,)).copy()
-        self.calls.append(("gather", dict(P=P, B=B, M=M, N=N, K=K, E=E, lhs=read(lhs),
-                                          rhs=read(rhs), sorted=sorted_)))
+        # a NULL lhs means pair p reads x batch p (the C ABI requires B == P then)
+        assert lhs or B == P
+        self.calls.append(("gather", dict(P=P, B=B, M=M, N=N, K=K, E=E,
+                                          lhs=read(lhs) if lhs else np.arange(P),
+                                          lhs_null=not lhs, rhs=read(rhs), sorted=sorted_)))
         return 0
 
     def mq_dequantize(self, w, s, b, out, N, K, gs, bits, dtype, stream):
@@ -208,6 +211,7 @@ def test_gather_sorted_layout(fake):
     assert out.shape == (P, 1, N)
     _, c = fake.calls[-1]
     np.testing.assert_array_equal(c["lhs"], np.arange(P))
+    assert c["lhs_null"]                  # identity lhs travels as NULL
     assert c["sorted"] == 1
 
 
