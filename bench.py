@@ -246,6 +246,24 @@ def measure_gather_prefill(torch, mq, T, N, K, routing, steps, warmup, E=512, to
             "distinct_experts": int(len(np.unique(flat)))}
 
 
+def measure_combine(torch, mq, rows, top_k, N, steps, warmup, seed=6):
+    """MoE combine epilogue over an expert-sorted down-projection output of
+    rows*top_k x N (the reference's prefill shape: 2048 tokens x top-8 x
+    2048).  Bytes per call: y read once + out written once + inv and w."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    y = torch.randn((rows * top_k, N), device="cuda", generator=g).to(torch.bfloat16)
+    inv = torch.argsort(torch.randperm(rows * top_k, device="cuda", generator=g)).to(torch.int32)
+    w = torch.rand(rows * top_k, device="cuda", generator=g)
+
+    def fn(i):
+        mq.moe_combine(y, inv, w, rows, top_k)
+
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    nbytes = 2 * rows * top_k * N + 2 * rows * N + 8 * rows * top_k
+    return {"us": round(per_step * 1e6, 2), "GBps": round(nbytes / per_step / 1e9, 1)}
+
+
 def measure_dequant(torch, mq, N, K, steps, warmup):
     R = copies_for(N * K // 2)
     ws = make_weights(torch, N, K, R, seed=7)
@@ -362,6 +380,7 @@ def main():
             for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
                 sweep[f"gather_prefill_{name}_{routing}_T2048"] = measure_gather_prefill(
                     torch, mq, 2048, NN, KK, routing, 20, 3)
+        sweep["moe_combine_T2048_k8_N2048"] = measure_combine(torch, mq, 2048, 8, 2048, 50, 3)
         sweep["dequant_b4_K5120_N17408"] = measure_dequant(torch, mq, N, K, 50, 3)
 
     cpu = None if args.no_cpu else cpu_baseline(N, K, args.cpu_seconds)

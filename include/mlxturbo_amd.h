@@ -103,6 +103,20 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
                   int dtype, int sorted_indices, void* workspace, size_t workspace_bytes,
                   void* hip_stream);
 
+/*
+ * MoE combine epilogue: out[t, n] = sum_k w[t*top_k + k] * y[inv[t*top_k + k], n]
+ * for t < rows, accumulated in float in k order and rounded once to dtype.
+ * Replaces kernels/moe_combine.py:160-195 (`combine(y, inv, w, rows, top_k)`,
+ * the unsort + router weight + top-k sum after the down projection,
+ * fused._moe_fold_block combine mode, fused.py:3283-3316).
+ * y is [*, N] in expert order (dtype bf16 or fp16), inv int32 [rows*top_k]
+ * gives the row of y holding token t's k-th expert output (NULL: row
+ * t*top_k + k), w float32 [rows*top_k], out [rows, N].  N % 8 == 0,
+ * 1 <= top_k <= 64, y and out 16-byte aligned.
+ */
+int mq_moe_combine(const void* y, const int32_t* inv, const float* w, void* out, int64_t rows,
+                   int64_t top_k, int64_t N, int dtype, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "../../include/mlxturbo_amd.h"
+#include "combine.cuh"
 #include "dequant.cuh"
 #include "launch.h"
 
@@ -168,6 +169,26 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
   if (e != hipSuccess) return fail((int)e, "gather_qmm: launch failed: %s", hipGetErrorString(e));
   g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
   return MQ_OK;
+}
+
+int mq_moe_combine(const void* y, const int32_t* inv, const float* w, void* out, int64_t rows,
+                   int64_t top_k, int64_t N, int dtype, void* hip_stream) {
+  if (!y || !w || !out) return fail(MQ_EINVAL, "y, w and out must be non-null");
+  if (rows < 0 || N <= 0) return fail(MQ_EINVAL, "invalid sizes rows=%lld N=%lld",
+                                      (long long)rows, (long long)N);
+  if (top_k < 1 || top_k > mq::kCombineMaxTopK)
+    return fail(MQ_EINVAL, "top_k must be in 1..%d (got %lld)", mq::kCombineMaxTopK,
+                (long long)top_k);
+  if (N % 8) return fail(MQ_EUNSUPPORTED, "moe_combine needs N %% 8 == 0 (got %lld)", (long long)N);
+  if (dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16)
+    return fail(MQ_EUNSUPPORTED, "moe_combine supports bf16 and fp16 (dtype %d)", dtype);
+  if (!aligned16(y) || !aligned16(out)) return fail(MQ_EINVAL, "y and out must be 16-byte aligned");
+  if (rows > 65535) return fail(MQ_EUNSUPPORTED, "moe_combine supports up to 65535 rows per call");
+  if (rows == 0) return MQ_OK;
+  int rc = mq::launch_moe_combine(y, inv, w, out, rows, top_k, N, dtype,
+                                  reinterpret_cast<hipStream_t>(hip_stream));
+  if (rc) return fail(rc, "moe_combine: no kernel for this configuration");
+  return check_launch("moe_combine");
 }
 
 }  // extern "C"

@@ -1,0 +1,72 @@
+// MoE combine epilogue: out[t, n] = T( sum_k w[t*top_k + k] * y[inv[t*top_k + k], n] ).
+//
+// Reference: mlxturbo/kernels/moe_combine.py:160-195 (one pass over the down
+// projection's expert-ordered output: unsort, router weight and top-k sum,
+// fp32 accumulation in k order, one rounding).  inv may be NULL: then the
+// rows of y are already in (token, k) order (decode widths, no sort).
+//
+// HBM-bound: bytes per call rows*top_k*N*2 (y) + rows*N*2 (out) + rows*top_k*8
+// (inv, w).  One workgroup per token; each thread owns 8 columns (one 16-byte
+// load per expert row, one 16-byte store), so every read of y is a
+// contiguous 16-byte piece of a row and a wave reads 1 KiB per instruction.
+// The token's row numbers and weights are read once into LDS.
+#pragma once
+#include "mq_common.h"
+
+namespace mq {
+
+constexpr int kCombineMaxTopK = 64;
+
+template <int DT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y,
+                                                          const int32_t* __restrict__ inv,
+                                                          const float* __restrict__ w,
+                                                          uint16_t* __restrict__ out, int top_k,
+                                                          int N) {
+  using T = T16<DT>;
+  __shared__ int s_row[kCombineMaxTopK];
+  __shared__ float s_w[kCombineMaxTopK];
+  const int t = blockIdx.y;
+  const int64_t base = (int64_t)t * top_k;
+  for (int i = threadIdx.x; i < top_k; i += blockDim.x) {
+    s_row[i] = inv ? inv[base + i] : (int)(base + i);
+    s_w[i] = w[base + i];
+  }
+  __syncthreads();
+  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (n >= N) return;
+  float acc[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) acc[v] = 0.f;
+  for (int k = 0; k < top_k; ++k) {
+    const float wk = s_w[k];
+    const u32x4 p = *reinterpret_cast<const u32x4*>(y + (int64_t)s_row[k] * N + n);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc[2 * v] = __builtin_fmaf(wk, T::to_f32((uint16_t)p[v]), acc[2 * v]);
+      acc[2 * v + 1] = __builtin_fmaf(wk, T::to_f32((uint16_t)(p[v] >> 16)), acc[2 * v + 1]);
+    }
+  }
+  u32x4 o;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) o[v] = T::pack2(acc[2 * v], acc[2 * v + 1]);
+  *reinterpret_cast<u32x4*>(out + (int64_t)t * N + n) = o;
+}
+
+inline int launch_moe_combine(const void* y, const int32_t* inv, const float* w, void* out,
+                              int64_t rows, int64_t top_k, int64_t N, int dtype, hipStream_t st) {
+  const int64_t cols = N / 8;
+  const int tb = cols >= 256 ? 256 : cols >= 128 ? 128 : 64;
+  const dim3 grid((unsigned)((cols + tb - 1) / tb), (unsigned)rows);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(moe_combine_kernel<kBF16>, grid, dim3(tb), 0, st, (const uint16_t*)y, inv,
+                       w, (uint16_t*)out, (int)top_k, (int)N);
+  else if (dtype == kF16)
+    hipLaunchKernelGGL(moe_combine_kernel<kF16>, grid, dim3(tb), 0, st, (const uint16_t*)y, inv,
+                       w, (uint16_t*)out, (int)top_k, (int)N);
+  else
+    return kStatusUnsupported;
+  return 0;
+}
+
+}  // namespace mq

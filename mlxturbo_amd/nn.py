@@ -124,8 +124,13 @@ class SwitchGLU(torch.nn.Module):
         self.up_proj = up_proj
         self.down_proj = down_proj
 
-    def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        # x: (..., K), indices: (..., top_k) -> (..., top_k, K_out)
+    def forward(self, x: torch.Tensor, indices: torch.Tensor,
+                scores: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x: (..., K), indices: (..., top_k) -> (..., top_k, K_out); with
+        router ``scores`` (..., top_k) -> (..., K_out): the router-weighted
+        sum over the top-k experts, folded into one combine pass over the
+        down projection's (possibly expert-sorted) output (the reference's
+        combine mode, kernels/moe_combine.py; fused.py:3283-3316)."""
         lead = x.shape[:-1]
         top_k = indices.shape[-1]
         xe = x.reshape(-1, 1, 1, x.shape[-1])                      # (T, 1, 1, K)
@@ -145,6 +150,11 @@ class SwitchGLU(torch.nn.Module):
         act = torch.nn.functional.silu(g.float()).to(g.dtype)
         h = (act.float() * u.float()).to(g.dtype)
         y = self.down_proj(h, idx_use, sorted_indices=do_sort)  # (T or P, k, 1, N)
+        if scores is not None:
+            rows = idx.shape[0]
+            out = ops.moe_combine(y.reshape(-1, y.shape[-1]), inv if do_sort else None,
+                                  scores.reshape(-1), rows, top_k)
+            return out.reshape(*lead, y.shape[-1])
         if do_sort:
             y = y.reshape(-1, y.shape[-1])[inv].reshape(*lead, top_k, y.shape[-1])
         else:

@@ -268,9 +268,48 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, rows: int,
+                top_k: int) -> torch.Tensor:
+    """MoE combine epilogue (kernels/moe_combine.py:160-195): from the down
+    projection's expert-ordered output ``y`` ``(M, N)`` build ``(rows, N)``
+    with ``out[t] = sum_k w[t*top_k + k] * y[inv[t*top_k + k]]``, float
+    accumulation in k order, one rounding.  ``inv`` (int, ``(rows*top_k,)``)
+    is the sorted row of each (token, k) -- ``argsort(order)``; ``None``
+    when ``y`` is already in (token, k) order.  ``w`` is the router weight
+    per (token, k), cast to float32 as the reference does."""
+    dev = _require_gpu(y, w, inv)
+    if y.ndim != 2:
+        raise ValueError("y must be (M, N)")
+    if y.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"moe_combine supports bf16/fp16 y, got {y.dtype}")
+    M, N = y.shape
+    rows, top_k = int(rows), int(top_k)
+    if w.numel() != rows * top_k:
+        raise ValueError(f"w has {w.numel()} weights, expected rows*top_k={rows * top_k}")
+    if inv is None:
+        if M != rows * top_k:
+            raise ValueError(f"y has {M} rows, expected rows*top_k={rows * top_k} without inv")
+        inv_ = None
+    else:
+        if inv.numel() != rows * top_k:
+            raise ValueError(f"inv has {inv.numel()} entries, expected {rows * top_k}")
+        inv_ = inv.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+    w_ = w.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    y_ = _aligned(y)
+    out = torch.empty((rows, N), dtype=y.dtype, device=dev)
+    if rows == 0:
+        return out
+    rc = _lib.lib().mq_moe_combine(y_.data_ptr(), inv_.data_ptr() if inv_ is not None else None,
+                                   w_.data_ptr(), out.data_ptr(), rows, top_k, N,
+                                   _dtype_code(y.dtype, y.dtype), _stream_ptr(out))
+    _lib.check(rc, "moe_combine")
+    return out
+
+
 def launch_count() -> int:
     """Kernel launches made through the library so far (proof the HIP path ran)."""
     return _lib.launch_count()
 
 
-__all__: Sequence[str] = ("dequantize", "quantized_matmul", "gather_qmm", "launch_count")
+__all__: Sequence[str] = ("dequantize", "quantized_matmul", "gather_qmm", "moe_combine",
+                          "launch_count")

@@ -23,6 +23,9 @@ dequantize             closed form cases: q=0 -> b, s=0 -> b, exactness of
 quantized_matmul_ref   brute-force pure-Python loop on tiny shapes, linearity
                        in x, row independence, column independence
 gather_qmm_ref         dense matmul on w[idx] per pair, sort invariance
+moe_combine_ref        pure-Python loop on tiny shapes, one-hot weights copy
+                       rows, identity inv equals the unsorted layout, linearity
+                       in w
 quantize               **parity unpinned**: MLX's quantizer source is not in
                        the container; the restatement is checked only for
                        its invariants (codes in range, |deq - w| <= |s|/2
@@ -199,6 +202,29 @@ def gather_qmm_ref(x, w, scales, biases, lhs_indices, rhs_indices,
         xf = to_f32(x[int(lhs[p])], dtype).astype(np.float64)
         out.append(xf @ cache[e].T if transpose else xf @ cache[e])
     return np.stack(out).astype(np.float32)
+
+
+# ------------------------------------------------------------- moe combine
+
+def moe_combine_ref(y, inv, w, rows: int, top_k: int, dtype: str = "bfloat16") -> np.ndarray:
+    """``out[t] = sum_k w[t*top_k + k] * y[inv[t*top_k + k]]`` accumulated in
+    float32 in k order (each step rounded once, as an fma), returned
+    un-rounded float32 ``[rows, N]``.  ``inv`` ``None`` means rows of ``y``
+    are in (token, k) order.  Restates kernels/moe_combine.py:63-97 (the
+    per-thread loop ``acc += wk * (float)p[v]``) and its caller contract
+    (moe_combine.py:160-195: inv = argsort(order), w cast to float32).
+    """
+    yf = to_f32(y, dtype).astype(np.float64)
+    w = np.asarray(w, dtype=np.float32).reshape(-1).astype(np.float64)
+    idx = (np.arange(rows * top_k) if inv is None else np.asarray(inv).reshape(-1))
+    out = np.zeros((rows, yf.shape[1]), dtype=np.float32)
+    for k in range(top_k):
+        sel = idx[np.arange(rows) * top_k + k]
+        # w*y is exact in float64 (24 + 8 significant bits); the sum with the
+        # float32 accumulator rounds once to float32
+        out = (w[np.arange(rows) * top_k + k][:, None] * yf[sel] + out.astype(np.float64)
+               ).astype(np.float32)
+    return out
 
 
 # ----------------------------------------------------------------- quantize

@@ -104,6 +104,20 @@ def test_dequant_argument_validation(lib):
     assert rc == -1 and "aligned" in lib.mq_last_error().decode()
 
 
+def test_combine_argument_validation(lib):
+    rc = lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 4, 0, 64, 0, None)
+    assert rc == -1 and "top_k" in lib.mq_last_error().decode()
+    rc = lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 4, 2, 60, 0, None)
+    assert rc == -2 and "N % 8" in lib.mq_last_error().decode()
+    rc = lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 4, 2, 64, 2, None)
+    assert rc == -2
+    rc = lib.mq_moe_combine(FAKE + 2, None, FAKE, FAKE, 4, 2, 64, 0, None)
+    assert rc == -1 and "aligned" in lib.mq_last_error().decode()
+    rc = lib.mq_moe_combine(None, None, FAKE, FAKE, 4, 2, 64, 0, None)
+    assert rc == -1
+    assert lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 0, 2, 64, 0, None) == 0
+
+
 def test_ops_refuse_cpu_tensors():
     x = torch.zeros(1, 256, dtype=torch.bfloat16)
     w = torch.zeros(16, 32, dtype=torch.int32)
@@ -141,6 +155,16 @@ class _FakeLib:
 
     def mq_dequantize(self, w, s, b, out, N, K, gs, bits, dtype, stream):
         self.calls.append(("deq", dict(N=N, K=K, gs=gs, bits=bits, dtype=dtype)))
+        return 0
+
+    def mq_moe_combine(self, y, inv, w, out, rows, top_k, N, dtype, stream):
+        n = rows * top_k
+        read_i = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
+                                                 shape=(n,)).copy()
+        read_f = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)),
+                                                 shape=(n,)).copy()
+        self.calls.append(("combine", dict(rows=rows, top_k=top_k, N=N, dtype=dtype,
+                                           inv=read_i(inv) if inv else None, w=read_f(w))))
         return 0
 
 
@@ -232,3 +256,21 @@ def test_dequantize_shapes(fake):
     out = mlxturbo_amd.dequantize(w, s, b, group_size=64, bits=8)
     assert out.shape == (48, 512) and out.dtype == torch.bfloat16
     assert fake.calls[-1] == ("deq", dict(N=48, K=512, gs=64, bits=8, dtype=0))
+
+
+def test_combine_passes_indices_and_weights(fake):
+    rows, top_k, N = 3, 2, 64
+    y = torch.zeros(rows * top_k, N, dtype=torch.bfloat16)
+    inv = torch.tensor([5, 0, 3, 1, 4, 2], dtype=torch.int64)
+    w = torch.tensor([0.5, 0.25, 1.0, 2.0, 0.125, 4.0], dtype=torch.float64)
+    out = mlxturbo_amd.moe_combine(y, inv, w, rows, top_k)
+    assert out.shape == (rows, N)
+    _, c = fake.calls[-1]
+    np.testing.assert_array_equal(c["inv"], inv.numpy())
+    np.testing.assert_array_equal(c["w"], w.numpy().astype(np.float32))
+    mlxturbo_amd.moe_combine(y, None, w, rows, top_k)
+    assert fake.calls[-1][1]["inv"] is None
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_combine(y[:5], None, w, rows, top_k)
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_combine(y, inv[:4], w, rows, top_k)

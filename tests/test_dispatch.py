@@ -166,3 +166,27 @@ def test_switch_glu_matches_composition(T):
     # gate/up rounding differences propagate through SiLU: allow the
     # tolerance of a second bf16 stage
     assert res["rel_l2"] < 1e-2, res
+
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [3, 40])
+def test_switch_glu_router_combine(T):
+    """scores fold into one combine pass (sorted path above 64 pairs)."""
+    rng = np.random.default_rng(60 + T)
+    E, H, I, top = 8, 256, 128, 4
+    def bank(N, K):
+        parts = [quantized(rng, N, K) for _ in range(E)]
+        return [np.stack([p[i] for p in parts]) for i in range(3)]
+    mods = [QuantizedSwitchLinear(to_dev(t[0]), to_dev(t[1], "bfloat16"), to_dev(t[2], "bfloat16"))
+            for t in (bank(I, H), bank(I, H), bank(H, I))]
+    glu = SwitchGLU(*mods)
+    idx = torch.from_numpy(zipf_routing(rng, T, top, E)).cuda()
+    x = to_dev(act(rng, (T, H)), "bfloat16")
+    scores = torch.from_numpy(rng.random((T, top)).astype(np.float32)).cuda()
+    per = glu(x, idx).float()                           # (T, top, H) bf16 outputs
+    want = (per * scores[..., None]).sum(-2)            # fp32 sum of the same rows
+    got = glu(x, idx, scores)
+    assert got.shape == (T, H)
+    res = O.check_output(from_dev(got), want.cpu().numpy())
+    assert res["ok"], res

@@ -438,3 +438,24 @@ def test_gather_prefill_grouped_invalid_and_sorted():
     out_s = bits16(mq.gather_qmm(xs, *dev, rhs_indices=torch.from_numpy(flat[order]).cuda(),
                                  sorted_indices=True))
     np.testing.assert_array_equal(out_s.reshape(T * top, N), bits16(out).reshape(T * top, N)[order])
+
+
+
+@pytest.mark.parametrize("rows,top_k,N,sorted_", [(1, 8, 2048, False), (7, 8, 2048, True),
+                                                 (2048, 8, 2048, True), (33, 2, 64, True),
+                                                 (5, 3, 264, False)])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_moe_combine(rows, top_k, N, sorted_, dtype):
+    """kernels/moe_combine.py's contract: unsort + router weight + top-k sum,
+    float accumulation, one rounding."""
+    rng = np.random.default_rng(rows + top_k + N)
+    y = O.from_f32(rng.standard_normal((rows * top_k, N)).astype(np.float32), dtype)
+    w = rng.random(rows * top_k).astype(np.float32)
+    inv = np.argsort(rng.permutation(rows * top_k)).astype(np.int32) if sorted_ else None
+    out = mq.moe_combine(to_dev(y, dtype), torch.from_numpy(inv).cuda() if sorted_ else None,
+                         torch.from_numpy(w).cuda(), rows, top_k)
+    ref = O.moe_combine_ref(y, inv, w, rows, top_k, dtype)
+    res = O.check_output(from_dev(out), ref, dtype)
+    assert res["ok"], res
+    # the same fma order as the restatement: at most a last-bit difference
+    assert res["max_ulp"] <= 1.0, res

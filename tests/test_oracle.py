@@ -338,3 +338,61 @@ def test_tolerance_rejects_planted_mistakes():
     x_drop[:, 256:512] = 0
     lost = O.quantized_matmul_ref(O.from_f32(x_drop, "bfloat16"), wq, s, b, gs, 4)
     assert not O.check_output(as_out(lost), ref)["ok"]
+
+
+# --------------------------------------------------------------- moe combine
+
+def _combine_loop(y_f32, inv, w, rows, top_k):
+    """Pure-Python restatement, element by element, with struct-rounded
+    float32 accumulation (independent of numpy's vector casts)."""
+    def f32(v):
+        return struct.unpack("f", struct.pack("f", v))[0]
+    N = y_f32.shape[1]
+    out = np.zeros((rows, N), np.float32)
+    for t in range(rows):
+        for n in range(N):
+            acc = 0.0
+            for k in range(top_k):
+                r = t * top_k + k if inv is None else int(inv[t * top_k + k])
+                acc = f32(float(np.float32(w[t * top_k + k])) * float(y_f32[r, n]) + acc)
+            out[t, n] = acc
+    return out
+
+
+def test_moe_combine_matches_loop():
+    rng = np.random.default_rng(3)
+    rows, top_k, N = 5, 3, 16
+    y = O.from_f32(rng.standard_normal((rows * top_k, N)).astype(np.float32), "bfloat16")
+    inv = rng.permutation(rows * top_k)
+    w = rng.random(rows * top_k).astype(np.float32)
+    got = O.moe_combine_ref(y, inv, w, rows, top_k)
+    want = _combine_loop(O.to_f32(y, "bfloat16"), inv, w, rows, top_k)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_moe_combine_invariants():
+    rng = np.random.default_rng(4)
+    rows, top_k, N = 7, 4, 24
+    y = O.from_f32(rng.standard_normal((rows * top_k, N)).astype(np.float32), "bfloat16")
+    yf = O.to_f32(y, "bfloat16")
+    order = rng.permutation(rows * top_k)
+    inv = np.argsort(order)
+    # one-hot weights copy exactly the selected rows
+    w = np.zeros(rows * top_k, np.float32)
+    w[np.arange(rows) * top_k + 2] = 1.0
+    got = O.moe_combine_ref(y, inv, w, rows, top_k)
+    np.testing.assert_array_equal(got, yf[inv[np.arange(rows) * top_k + 2]])
+    # identity inv == the unsorted layout; a sorted copy with inv == the original
+    w = rng.random(rows * top_k).astype(np.float32)
+    plain = O.moe_combine_ref(y, None, w, rows, top_k)
+    np.testing.assert_array_equal(O.moe_combine_ref(y, np.arange(rows * top_k), w, rows, top_k),
+                                  plain)
+    y_sorted = y[order]                     # row j of y_sorted = row order[j] of y
+    np.testing.assert_array_equal(O.moe_combine_ref(y_sorted, inv, w, rows, top_k), plain)
+    # linear in w (up to float32 rounding)
+    np.testing.assert_allclose(O.moe_combine_ref(y, None, 2 * w, rows, top_k), 2 * plain,
+                               rtol=1e-6, atol=1e-6)
+    # a planted mistake (dropping the last expert) is caught by the loop check
+    bad = O.moe_combine_ref(y, None, np.where(np.arange(rows * top_k) % top_k == top_k - 1, 0, w)
+                            .astype(np.float32), rows, top_k)
+    assert not np.array_equal(bad, _combine_loop(yf, None, w, rows, top_k))
