@@ -11,14 +11,15 @@ hand-written HIP kernels behind a C ABI (``include/mlxturbo_amd.h``):
 Module level (:mod:`mlxturbo_amd.nn`, :mod:`mlxturbo_amd.dispatch`): torch
 ``QuantizedLinear`` / ``QuantizedSwitchLinear`` / ``SwitchGLU`` on MLX-format
 tensors, and the reference's shape-by-M route table with per-instance and
-class-level enabling.
+class-level enabling.  :mod:`mlxturbo_amd.checkpoint` builds those modules
+from MLX safetensors checkpoints.
 """
 
-from . import dispatch, nn
+from . import checkpoint, dispatch, nn
 from .ops import dequantize, gather_qmm, launch_count, moe_combine, quantized_matmul
 
 __version__ = "0.1.0"
 
-__all__ = ["dequantize", "dispatch", "gather_qmm", "launch_count", "moe_combine", "nn",
-           "quantized_matmul",
+__all__ = ["checkpoint", "dequantize", "dispatch", "gather_qmm", "launch_count", "moe_combine",
+           "nn", "quantized_matmul",
            "__version__"]
