@@ -57,6 +57,7 @@ def parse():
     p.add_argument("--case", default="",
                    help="run one sweep case only and print its result (for profiling): "
                         "wide<M> (configs[2]), gather_<proj>_<routing>_T<T> (configs[3] decode), "
+                        "gather_glu_<routing>_T<T> (fused gate+up+SiLU), "
                         "gather_prefill_<proj>_<routing> (2048 tokens)")
     return p.parse_args()
 
@@ -78,8 +79,9 @@ def run_case(torch, mq, case: str) -> dict:
     if case.startswith("gather_"):
         body, t = case[len("gather_"):].rsplit("_T", 1)
         proj, routing = body.rsplit("_", 1)
-        NN, KK = banks[proj]
-        return {"case": case, **measure_gather(torch, mq, int(t), NN, KK, routing, 100, 5)}
+        NN, KK = banks["gate_up" if proj == "glu" else proj]
+        return {"case": case, **measure_gather(torch, mq, int(t), NN, KK, routing, 100, 5,
+                                               glu=proj == "glu")}
     raise SystemExit(f"unknown --case {case!r}")
 
 
@@ -186,30 +188,38 @@ def zipf_routing(rng, T, top_k, E, s=1.1):
                      for _ in range(T)]).astype(np.int32)
 
 
-def measure_gather(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, nroute=64, seed=4):
+def measure_gather(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, nroute=64, seed=4,
+                   glu=False):
     """gather_qmm over an E-expert 4-bit bank for T tokens x top_k
     experts; `nroute` seeded routings rotate so weights stream from HBM.
-    Algorithmic bytes count each distinct expert's weights once per call."""
+    Algorithmic bytes count each distinct expert's weights once per call.
+    glu: the N rows per expert are a gate and an up bank of N/2 rows each,
+    through the fused gate+up+SiLU (gather_glu, N/2 outputs per pair)."""
     rng = np.random.default_rng(seed + T)
     routes = [(zipf_routing(rng, T, top_k, E) if routing == "zipf" else
                np.stack([rng.choice(E, size=top_k, replace=False) for _ in range(T)]).astype(np.int32))
               for _ in range(nroute)]
-    (w, s, b), = make_weights(torch, E * N, K, 1, seed=seed)
-    w, s, b = w.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
+    nb = 2 if glu else 1
+    banks = [tuple(t.view(E, N // nb, -1) for t in make_weights(torch, E * N // nb, K, 1,
+                                                                 seed=seed + i)[0])
+             for i in range(nb)]
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     x = torch.randn((T, 1, 1, K), device="cuda", generator=g).to(torch.bfloat16)
     idx = [torch.from_numpy(r).cuda() for r in routes]
     per_expert = N * K // 2 + 4 * N * (K // 64)
-    nbytes = [len(np.unique(r)) * per_expert + 2 * T * K + 2 * T * top_k * N for r in routes]
+    nbytes = [len(np.unique(r)) * per_expert + 2 * T * K + 2 * T * top_k * N // nb for r in routes]
 
     def fn(i):
-        mq.gather_qmm(x, w, s, b, rhs_indices=idx[i % nroute])
+        if glu:
+            mq.gather_glu(x, *banks[0], *banks[1], rhs_indices=idx[i % nroute])
+        else:
+            mq.gather_qmm(x, *banks[0], rhs_indices=idx[i % nroute])
 
     elapsed, per_step = time_graph(torch, fn, steps, warmup)
     avg_bytes = sum(nbytes[i % nroute] for i in range(steps)) / steps
     uniq = sum(len(np.unique(r)) for r in routes) / nroute
-    del w, s, b
+    del banks
     torch.cuda.empty_cache()
     return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
             "distinct_experts": round(uniq, 1)}
@@ -375,6 +385,9 @@ def main():
                 for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
                     sweep[f"gather_{name}_{routing}_T{T}"] = measure_gather(
                         torch, mq, T, NN, KK, routing, 100, 5)
+                # the same gate/up bytes through the fused gate+up+SiLU kernel
+                sweep[f"gather_glu_{routing}_T{T}"] = measure_gather(
+                    torch, mq, T, 1024, 2048, routing, 100, 5, glu=True)
         # config 4 banks at prefill width (2048 tokens): expert-grouped MFMA tiles
         for routing in ("zipf", "uniform"):
             for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):

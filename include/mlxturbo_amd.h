@@ -104,6 +104,27 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
                   void* hip_stream);
 
 /*
+ * Fused MoE gate+up+SiLU at decode / verify widths:
+ *   out[p, M, N] = silu(x[lhs[p]] . dequantize(w_gate[rhs[p]])^T)
+ *                * (x[lhs[p]] . dequantize(w_up[rhs[p]])^T)
+ * with both products summed in float, silu(g) = g / (1 + exp(-g)) and the
+ * product rounded once to dtype.  Replaces kernels/moe_glu.py:145-168
+ * (`fused_glu(x_pairs, idx_flat, gate_proj, up_proj)`) and
+ * kernels/moe_decode_fused.py:331-350 (`gate_up(x, idx_flat, gate, up,
+ * topk)`).  Arguments as mq_gather_qmm, with two banks of one shape
+ * ([E, N, K*bits/32], scales/biases [E, N, K/group_size]); the workspace is
+ * mq_gather_qmm_workspace_size(P, M) bytes.  P * M >= 1024 output rows
+ * (prefill) returns MQ_EUNSUPPORTED: the caller composes two mq_gather_qmm
+ * calls there, as the reference keeps its stock path outside decode.
+ */
+int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate,
+                  const void* biases_gate, const uint32_t* w_up, const void* scales_up,
+                  const void* biases_up, const int32_t* lhs_indices,
+                  const int32_t* rhs_indices, void* out, int64_t P, int64_t B, int64_t M,
+                  int64_t N, int64_t K, int64_t E, int group_size, int bits, int dtype,
+                  void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/*
  * MoE combine epilogue: out[t, n] = sum_k w[t*top_k + k] * y[inv[t*top_k + k], n]
  * for t < rows, accumulated in float in k order and rounded once to dtype.
  * Replaces kernels/moe_combine.py:160-195 (`combine(y, inv, w, rows, top_k)`,

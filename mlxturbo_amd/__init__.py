@@ -6,6 +6,7 @@ hand-written HIP kernels behind a C ABI (``include/mlxturbo_amd.h``):
 * :func:`quantized_matmul` - decode (M=1), verify (M=2..16) and prefill widths
 * :func:`gather_qmm`       - MoE expert gather
 * :func:`dequantize`       - bit-exact MLX affine dequantization
+* :func:`gather_glu`       - fused MoE gate+up+SiLU at decode widths
 * :func:`moe_combine`      - MoE unsort + router weight + top-k sum epilogue
 
 Module level (:mod:`mlxturbo_amd.nn`, :mod:`mlxturbo_amd.dispatch`): torch
@@ -16,10 +17,12 @@ from MLX safetensors checkpoints.
 """
 
 from . import checkpoint, dispatch, nn
-from .ops import dequantize, gather_qmm, launch_count, moe_combine, quantized_matmul
+from .ops import (dequantize, gather_glu, gather_qmm, launch_count, moe_combine,
+                  quantized_matmul)
 
 __version__ = "0.1.0"
 
-__all__ = ["checkpoint", "dequantize", "dispatch", "gather_qmm", "launch_count", "moe_combine",
+__all__ = ["checkpoint", "dequantize", "dispatch", "gather_glu", "gather_qmm", "launch_count",
+           "moe_combine",
            "nn", "quantized_matmul",
            "__version__"]

@@ -30,6 +30,7 @@ EXPORTED = (
     "mq_quantized_matmul",
     "mq_gather_qmm_workspace_size",
     "mq_gather_qmm",
+    "mq_gather_glu",
     "mq_moe_combine",
 )
 
@@ -62,6 +63,10 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_gather_qmm.restype = _int
     lib.mq_gather_qmm.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]
+    lib.mq_gather_glu.restype = _int
+    lib.mq_gather_glu.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                  _i64, _i64, _i64, _i64, _int, _int, _int, _vp, ctypes.c_size_t,
+                                  _vp]
     lib.mq_moe_combine.restype = _int
     lib.mq_moe_combine.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]
 

@@ -42,8 +42,8 @@ def hipcc() -> str:
 
 # (source, extra defines) of each translation unit
 UNITS = [("abi.hip", [])] + [
-    ("inst.hip", [f"-DMQ_INST_DT={dt}", f"-DMQ_INST_BITS={bits}"])
-    for dt in (0, 1) for bits in (4, 8)
+    ("inst.hip", [f"-DMQ_INST_DT={dt}", f"-DMQ_INST_BITS={bits}"] + glu)
+    for glu in ([], ["-DMQ_INST_GLU"]) for dt in (0, 1) for bits in (4, 8)
 ]
 
 _NOISE = ("packed-fp32-ops", "warning generated", "warnings generated")

@@ -171,6 +171,47 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
   return MQ_OK;
 }
 
+int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate,
+                  const void* biases_gate, const uint32_t* w_up, const void* scales_up,
+                  const void* biases_up, const int32_t* lhs_indices,
+                  const int32_t* rhs_indices, void* out, int64_t P, int64_t B, int64_t M,
+                  int64_t N, int64_t K, int64_t E, int group_size, int bits, int dtype,
+                  void* workspace, size_t workspace_bytes, void* hip_stream) {
+  int rc = check_common(w_gate, scales_gate, biases_gate, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  rc = check_common(w_up, scales_up, biases_up, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !out || !rhs_indices) return fail(MQ_EINVAL, "x, out and rhs_indices must be non-null");
+  if (P < 0 || M < 0 || E <= 0 || B < 0)
+    return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
+                (long long)M, (long long)E, (long long)B);
+  if (!lhs_indices && B != P)
+    return fail(MQ_EINVAL, "lhs_indices=NULL requires B == P (B=%lld P=%lld)", (long long)B,
+                (long long)P);
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (N > INT32_MAX || K > INT32_MAX || P > INT32_MAX || E > INT32_MAX || M > 16)
+    return fail(MQ_EUNSUPPORTED, "gather_glu supports M <= 16 rows per pair");
+  if (P * M >= mq::kGroupedMinRows)
+    return fail(MQ_EUNSUPPORTED, "gather_glu is fused below %lld output rows (got %lld)",
+                (long long)mq::kGroupedMinRows, (long long)(P * M));
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (P == 0 || M == 0 || N == 0) return MQ_OK;
+  const size_t ws_need = mq::gather_workspace_bytes(P, M);
+  if (ws_need && (workspace_bytes < ws_need || !workspace))
+    return fail(MQ_EINVAL, "workspace too small: need %zu bytes", ws_need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  int nl = 0;
+  rc = dispatch_16<mq::GluLaunch>(dtype, bits, group_size, x, w_gate, scales_gate, biases_gate,
+                                  w_up, scales_up, biases_up, lhs_indices, rhs_indices, out, P, B,
+                                  M, N, K, E, workspace, st, &nl);
+  if (rc) return fail(rc, "gather_glu: no kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail((int)e, "gather_glu: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
 int mq_moe_combine(const void* y, const int32_t* inv, const float* w, void* out, int64_t rows,
                    int64_t top_k, int64_t N, int dtype, void* hip_stream) {
   if (!y || !w || !out) return fail(MQ_EINVAL, "y, w and out must be non-null");

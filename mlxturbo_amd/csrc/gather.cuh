@@ -111,6 +111,7 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
 
 // A rows of a gather segment: pair members[j] contributes rows j*Mi .. j*Mi+Mi-1.
 struct GatherRows {
+  static constexpr bool kCombine = false;
   const uint16_t* x;
   uint32_t x_nrec;
   uint16_t* out;
@@ -127,10 +128,23 @@ struct GatherRows {
   }
 };
 
+// Fused gate+up+SiLU (the reference's moe_glu.py:30-105 and
+// moe_decode_fused.py:135-223): the call's two tiles are the same rows of
+// the gate and the up bank; the epilogue stores silu(g) * u =
+// g / (1 + exp(-g)) * u from the float sums, rounded once.
+template <int DT>
+struct GluRows : GatherRows {
+  static constexpr bool kCombine = true;
+  __device__ __forceinline__ void store_combined(int m, int nn, const float (&v)[2]) const {
+    const float g = v[0], u = v[1];
+    store(m, nn, T16<DT>::round1(g / (1.0f + __expf(-g)) * u));
+  }
+};
+
 // Dynamic LDS of one wave group of the gather kernel (see below).
 template <int BITS, int GS, int GPL>
-__host__ __device__ inline size_t gather_group_lds(int NWT, int XM, bool sbl, int G) {
-  return qmv_x_lds<BITS, GS, GPL>(NWT, XM) + (sbl ? qmv_sb_lds(G) : 0);
+__host__ __device__ inline size_t gather_group_lds(int NWT, int XM, bool sbl, int G, int TJ) {
+  return qmv_x_lds<BITS, GS, GPL>(NWT, XM) + (sbl ? TJ * qmv_sb_lds(G) : 0);
 }
 
 // grid = (segments upper bound, ceil(N / (16 * NW / NWT * tpw))); block 64 * NW.
@@ -143,14 +157,20 @@ __host__ __device__ inline size_t gather_group_lds(int NWT, int XM, bool sbl, in
 // XM > 0: x streams through LDS, R * Mi <= XM and B * Mi * K * 2 < 2^31; a
 // segment of one pair with Mi == 1 runs the one-row variant of the tile.
 // SBL: tile scales/biases are copied to LDS (qmv_sb_fits holds).
-template <int DT, int BITS, int GS, int GPL, int NW, int NWT, int PF, int XM, bool SBL>
+// GLU: (w, scales, biases) is the gate bank and (w2, scales2, biases2) the up
+// bank of the same shape; out = silu(gate) * up (GluRows: the gate and up
+// tiles of a row block run as the two tiles of one qmv_tile call).
+template <int DT, int BITS, int GS, int GPL, int NW, int NWT, int PF, int XM, bool SBL, bool GLU>
 __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ ws, int P, int B, int Mi, int N, int K, int E, int R, int tpw) {
+    const uint32_t* __restrict__ w2, const uint16_t* __restrict__ scales2,
+    const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
+    const int32_t* __restrict__ rhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
+    int P, int B, int Mi, int N, int K, int E, int R, int tpw) {
   extern __shared__ __align__(16) unsigned char qmv_smem[];
-  __shared__ f32x4 red[NW][64];
+  constexpr int TJ = GLU ? 2 : 1;
+  __shared__ f32x4 red[NW * TJ][64];
   __shared__ int s_key[kGatherFusedMaxP];
   __shared__ int s_cb[kGatherFusedMaxP];
   __shared__ int s_members[16];
@@ -253,7 +273,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     __syncthreads();
   }
   constexpr int NG = NW / NWT;                 // tile groups per workgroup
-  const int e = s_expert;
+  const int e = __builtin_amdgcn_readfirstlane(s_expert);
   const int M = nmem * Mi;
   const int nb = blockIdx.y * 16 * NG * tpw;
   if (e >= E) {
@@ -271,7 +291,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   const uint32_t x_nrec = XM > 0 ? (uint32_t)((int64_t)B * Mi * K * 2) : 0u;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int g = wave / NWT, kw = wave - g * NWT;
-  unsigned char* gsm = qmv_smem + g * gather_group_lds<BITS, GS, GPL>(NWT, XM, SBL, K / GS);
+  unsigned char* gsm = qmv_smem + g * gather_group_lds<BITS, GS, GPL>(NWT, XM, SBL, K / GS, TJ);
   for (int tt = 0; tt < tpw; ++tt) {
     const int n00 = nb + 16 * NG * tt;
     if (n00 >= N) break;                       // uniform in the workgroup
@@ -280,17 +300,29 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const int rows = min(16, N - n0);
     const int64_t row0 = (int64_t)e * N + (rows > 0 ? n0 : 0);
     const GatherRows src{x, x_nrec, out, s_members, s_xbase, Mi, K, N, n0};
-    const char* wt = reinterpret_cast<const char*>(w) + row0 * rowB;
-    const char* st = reinterpret_cast<const char*>(scales) + row0 * sRowB;
-    const char* bt = reinterpret_cast<const char*>(biases) + row0 * sRowB;
+    QmvTiles<TJ> tl;
+    tl.w[0] = reinterpret_cast<const char*>(w) + row0 * rowB;
+    tl.s[0] = reinterpret_cast<const char*>(scales) + row0 * sRowB;
+    tl.b[0] = reinterpret_cast<const char*>(biases) + row0 * sRowB;
+    tl.rows[0] = rows;
+    if constexpr (GLU) {
+      tl.w[1] = reinterpret_cast<const char*>(w2) + row0 * rowB;
+      tl.s[1] = reinterpret_cast<const char*>(scales2) + row0 * sRowB;
+      tl.b[1] = reinterpret_cast<const char*>(biases2) + row0 * sRowB;
+      tl.rows[1] = rows;
+    }
     // the one-row variant uses a prefix of the group's x region; its scale
     // copy lands inside the group's region too
-    if (XM > 1 && M == 1)
-      qmv_tile<DT, BITS, GS, GPL, NWT, PF, (XM > 1 ? 1 : XM), SBL>(
-          wt, st, bt, rows, M, K, src, gsm, red + g * NWT, kw, t - 64 * NWT * g);
-    else
-      qmv_tile<DT, BITS, GS, GPL, NWT, PF, XM, SBL>(wt, st, bt, rows, M, K, src, gsm,
-                                                    red + g * NWT, kw, t - 64 * NWT * g);
+    auto tile = [&](const auto& rs) {
+      if (XM > 1 && M == 1)
+        qmv_tile<DT, BITS, GS, GPL, NWT, PF, (XM > 1 ? 1 : XM), SBL, TJ>(
+            tl, M, K, rs, gsm, red + g * NWT * TJ, kw, t - 64 * NWT * g);
+      else
+        qmv_tile<DT, BITS, GS, GPL, NWT, PF, XM, SBL, TJ>(tl, M, K, rs, gsm, red + g * NWT * TJ,
+                                                          kw, t - 64 * NWT * g);
+    };
+    if constexpr (GLU) tile(GluRows<DT>{src});
+    else tile(src);
   }
 }
 
@@ -338,18 +370,14 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
                                              nlaunch);
 }
 
-template <int DT, int BITS, int GS>
-int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
-                                    const void* b, const int32_t* lhs, const int32_t* rhs,
-                                    void* out, int64_t P, int64_t B, int64_t M, int64_t N,
-                                    int64_t K, int64_t E, void* ws, hipStream_t st,
-                                    int* nlaunch) {
-  if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
-  if ((N + 15) / 16 > 65535) return kStatusUnsupported;
-  if (P * M >= kGroupedMinRows && E <= kGatherPrepMaxE && K % kWideBK == 0 &&
-      B * M * K * 2 < ((int64_t)1 << 31) && 256 * K * 2 < ((int64_t)1 << 31))
-    return launch_grouped<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
-                                        nlaunch);
+// The streaming gather kernel over segments (GLU: fused gate+up+SiLU with the
+// up bank in w2 / s2 / b2).
+template <int DT, int BITS, int GS, bool GLU>
+inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, const void* b,
+                             const uint32_t* w2, const void* s2, const void* b2,
+                             const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
+                             int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
+                             hipStream_t st, int* nlaunch) {
   using C = QmvConf<BITS, GS>;
   using Gm = QmvGeom<BITS, GS, C::GPL>;
   // Segments of up to R pairs; R * M <= 8 A rows stream x through LDS, one
@@ -364,12 +392,14 @@ int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void
   const int64_t nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
   const int nwt = nsteps >= 4 ? 4 : nsteps >= 2 ? 2 : 1;
   const int ng = C::NW / nwt;
-  const bool sbl = qmv_sb_fits(K / GS, nwt, s, b);
+  constexpr int TJ = GLU ? 2 : 1;
+  const bool sbl =
+      qmv_sb_fits(K / GS, nwt, TJ, s, b) && (!GLU || qmv_sb_fits(K / GS, nwt, TJ, s2, b2));
   // without the scale copy only the 8-row streamed-x variant is built
   const int xml = (sbl || XM == 0) ? XM : kQmvMaxXM;
   auto lds_for = [&](int xmax, int wpt, bool with_sb) {
     return (size_t)(C::NW / wpt) *
-           gather_group_lds<BITS, GS, C::GPL>(wpt, xmax, with_sb, (int)(K / GS));
+           gather_group_lds<BITS, GS, C::GPL>(wpt, xmax, with_sb, (int)(K / GS), TJ);
   };
   int64_t max_seg = P;
   const int32_t* wsp = nullptr;
@@ -390,10 +420,11 @@ int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void
   const dim3 grid((unsigned)max_seg, (unsigned)((slots + tpw - 1) / tpw));
 #define MQ_GX(WPT, X, SB)                                                                    \
   if (nwt == WPT && xml == X && sbl == SB) {                                                  \
-    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, WPT, C::PF, X, SB>),    \
+    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, WPT, C::PF, X, SB, GLU>), \
                        grid, dim3(64 * C::NW), lds_for(X, WPT, SB), st, (const uint16_t*)x, w, \
-                       (const uint16_t*)s, (const uint16_t*)b, lhs, rhs, (uint16_t*)out, wsp,  \
-                       (int)P, (int)B, (int)M, (int)N, (int)K, (int)E, R, tpw);              \
+                       (const uint16_t*)s, (const uint16_t*)b, w2, (const uint16_t*)s2,       \
+                       (const uint16_t*)b2, lhs, rhs, (uint16_t*)out, wsp, (int)P, (int)B,    \
+                       (int)M, (int)N, (int)K, (int)E, R, tpw);                              \
   }
 #define MQ_GXW(WPT)                                                                          \
   MQ_GX(WPT, 0, true) MQ_GX(WPT, 1, true) MQ_GX(WPT, 2, true) MQ_GX(WPT, 4, true)            \
@@ -403,6 +434,34 @@ int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void
 #undef MQ_GX
   *nlaunch += 1;
   return 0;
+}
+
+template <int DT, int BITS, int GS>
+int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
+                                    const void* b, const int32_t* lhs, const int32_t* rhs,
+                                    void* out, int64_t P, int64_t B, int64_t M, int64_t N,
+                                    int64_t K, int64_t E, void* ws, hipStream_t st,
+                                    int* nlaunch) {
+  if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
+  if ((N + 15) / 16 > 65535) return kStatusUnsupported;
+  if (P * M >= kGroupedMinRows && E <= kGatherPrepMaxE && K % kWideBK == 0 &&
+      B * M * K * 2 < ((int64_t)1 << 31) && 256 * K * 2 < ((int64_t)1 << 31))
+    return launch_grouped<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
+                                        nlaunch);
+  return gather_qmv_launch<DT, BITS, GS, false>(x, w, s, b, nullptr, nullptr, nullptr, lhs, rhs,
+                                                out, P, B, M, N, K, E, ws, st, nlaunch);
+}
+
+template <int DT, int BITS, int GS>
+int GluLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const void* sg,
+                                 const void* bg, const uint32_t* wu, const void* su,
+                                 const void* bu, const int32_t* lhs, const int32_t* rhs,
+                                 void* out, int64_t P, int64_t B, int64_t M, int64_t N,
+                                 int64_t K, int64_t E, void* ws, hipStream_t st, int* nlaunch) {
+  if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
+  if ((N + 15) / 16 > 65535 || P * M >= kGroupedMinRows) return kStatusUnsupported;
+  return gather_qmv_launch<DT, BITS, GS, true>(x, wg, sg, bg, wu, su, bu, lhs, rhs, out, P, B, M,
+                                               N, K, E, ws, st, nlaunch);
 }
 
 }  // namespace mq

@@ -1,6 +1,7 @@
 // Kernel instantiations of one (dtype, bits) pair for every group size.  The
 // build compiles this file once per pair with -DMQ_INST_DT=<0|1> and
-// -DMQ_INST_BITS=<4|8>; abi.hip calls the launchers through launch.h.
+// -DMQ_INST_BITS=<4|8>, and once more per pair with -DMQ_INST_GLU for the
+// fused gate+up kernels; abi.hip calls the launchers through launch.h.
 #include "launch.h"
 #include "dequant.cuh"
 #include "gather.cuh"
@@ -13,11 +14,15 @@
 
 namespace mq {
 
+#ifdef MQ_INST_GLU
+#define MQ_INST(GS) template struct GluLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
+#else
 #define MQ_INST(GS)                                                  \
   template struct DequantLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;       \
   template struct SkinnyLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;        \
   template struct WideLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;          \
   template struct GatherLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
+#endif
 
 MQ_INST(32)
 MQ_INST(64)

@@ -39,6 +39,17 @@ struct GatherLaunch {
                  int* nlaunch);
 };
 
+// Fused gate+up+SiLU over P pairs: out = silu(x . Wg^T) * (x . Wu^T) with
+// float sums and one rounding (gather.cuh); decode / verify widths only
+// (P * M < kGroupedMinRows, else kStatusUnsupported).
+template <int DT, int BITS, int GS>
+struct GluLaunch {
+  static int run(const void* x, const uint32_t* wg, const void* sg, const void* bg,
+                 const uint32_t* wu, const void* su, const void* bu, const int32_t* lhs,
+                 const int32_t* rhs, void* out, int64_t P, int64_t B, int64_t M, int64_t N,
+                 int64_t K, int64_t E, void* ws, hipStream_t st, int* nlaunch);
+};
+
 // ---- host-side routing and sizing ------------------------------------------
 
 // The wide kernel takes M > 16 rows, K in whole 64-code steps, 4/8-bit codes

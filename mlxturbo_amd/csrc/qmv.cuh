@@ -28,14 +28,18 @@
 //    from memory (16 scattered 16-byte pieces per instruction) took ~2 us of
 //    a 15 us launch at the headline shape.  Shapes whose scale rows are not
 //    16-byte multiples, or too long for the copy, read them per step.
-//  * x (M <= 8 rows) streams with the weights: each step's x slice is loaded
-//    in the same batch as the step's weights and staged through a per-wave
-//    LDS region from which the MFMA A fragments are read (ds_read_b128).  An
-//    up-front copy of all of x stalled every wave for microseconds behind the
-//    weight prologue in the memory queues.  Lanes whose A row is >= M read
-//    row M-1: it only fills output rows that are never stored, since the
-//    rows of an MFMA product are independent.  For M > 8 A fragments come
-//    from global memory in the same order.
+//  * x (M <= 16 rows) streams with the weights: each step's x slice is
+//    loaded in the same batch as the step's weights and staged through a
+//    per-wave LDS region from which the MFMA A fragments are read
+//    (ds_read_b128).  An up-front copy of all of x stalled every wave for
+//    microseconds behind the weight prologue in the memory queues.  Lanes
+//    whose A row is >= M read row M-1: it only fills output rows that are
+//    never stored, since the rows of an MFMA product are independent.
+//    Rows beyond the streamed capacity read A fragments from global memory
+//    in the same order.
+//  * From 8 rows on, a workgroup runs two 16-row tiles (TJ = 2) over each x
+//    slice, halving the x traffic per weight byte; each tile keeps its own
+//    accumulator, so results do not depend on TJ.
 //  * Dequantization is the exact fma_mix trick of mq_common.h, rounded to T
 //    per weight (bit-exact MLX dequantization); the packed T pairs are the
 //    B operand of v_mfma_f32_16x16x32 (32 k x 16 rows).  A and B use the same
@@ -112,14 +116,30 @@ struct QmvConf {
 // 4), 4 otherwise.
 inline int qmv_nw_for(int64_t N) { return (N + 15) / 16 < 640 ? 8 : 4; }
 
-// Most A rows whose x slices stream through LDS; more rows read A fragments
-// straight from global memory (same arithmetic order).
+// Streamed-x capacities: 1, 2, 4 and 8 rows everywhere, 16 rows in the
+// skinny kernel for steps of at most 256 codes (longer steps would hold 64
+// x registers per stage).  Rows beyond the capacity read A fragments straight
+// from global memory (same arithmetic order).
 constexpr int kQmvMaxXM = 8;
 
 // Smallest streamed-x capacity (1, 2, 4, 8) holding M rows, or 0.
 inline int qmv_xm_for(int64_t M) {
   return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= kQmvMaxXM ? 8 : 0;
 }
+
+template <int BITS, int GS, int GPL>
+inline int qmv_skinny_xm_for(int64_t M) {
+  if (M > kQmvMaxXM && M <= 16 && QmvGeom<BITS, GS, GPL>::STEPK <= 256) return 16;
+  return qmv_xm_for(M);
+}
+
+// Tiles per workgroup of the skinny kernel: two 16-row tiles share each x
+// slice once x outweighs the tile's weights per step (8+ streamed rows:
+// M=8 18.4 against 18.7 us, M=16 21.9 against 24.8 at K=5120 N=17408; 19.4
+// against 22.4 and 23.3 against 31.9 at K=17408 N=5120); fewer rows run one
+// tile per workgroup (M=1..4 lose 1.5-2.5 us with two: fewer, longer
+// workgroups).
+inline int qmv_tj_for(int xm) { return xm >= 8 ? 2 : 1; }
 
 // Dynamic LDS of a workgroup streaming x for up to XM rows: one region of
 // XM rows x one step (rows padded by 16 bytes) per wave.
@@ -134,11 +154,19 @@ constexpr int kQmvSbChunks = 3;
 __host__ __device__ inline int qmv_sb_stride(int G) { return 2 * G + 16; }
 __host__ __device__ inline size_t qmv_sb_lds(int G) { return 2 * 16 * (size_t)qmv_sb_stride(G); }
 
-// Whether a tile's scales/biases can be copied to LDS: rows of whole 16-byte
-// chunks (so the copy never splits a chunk across rows), 16-byte aligned
-// bases, and at most kQmvSbChunks chunks of each array per thread.
-inline bool qmv_sb_fits(int64_t G, int NW, const void* scales, const void* biases) {
-  return G % 8 == 0 && 16 * (G / 8) <= (int64_t)kQmvSbChunks * 64 * NW &&
+// Upper bound of the dynamic LDS of one skinny launch over every K the
+// scale copy accepts (TJ * 16 * G / 8 <= kQmvSbChunks * 64 * NW).
+template <int BITS, int GS, int GPL>
+__host__ __device__ inline size_t qmv_lds_bound(int NW, int XM, bool sbl, int TJ) {
+  const int gmax = 8 * (kQmvSbChunks * 64 * NW / (16 * TJ));
+  return qmv_x_lds<BITS, GS, GPL>(NW, XM) + (sbl ? TJ * qmv_sb_lds(gmax) : 0);
+}
+
+// Whether the scales/biases of TJ tiles can be copied to LDS: rows of whole
+// 16-byte chunks (so the copy never splits a chunk across rows), 16-byte
+// aligned bases, and at most kQmvSbChunks chunks of each array per thread.
+inline bool qmv_sb_fits(int64_t G, int NW, int TJ, const void* scales, const void* biases) {
+  return G % 8 == 0 && TJ * 16 * (G / 8) <= (int64_t)kQmvSbChunks * 64 * NW &&
          (reinterpret_cast<uintptr_t>(scales) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(biases) & 15) == 0;
 }
@@ -146,9 +174,12 @@ inline bool qmv_sb_fits(int64_t G, int NW, const void* scales, const void* biase
 // Row sources of a tile: where the A rows (x) come from and where outputs go.
 // Every Rows type gives x (base of all A rows), x_nrec (bytes of x readable
 // from x, < 2^31 when x streams through LDS), xoff(m) (element offset of A
-// row m from x) and store(m, nn, v).
+// row m from x) and either store(m, nn, v) of a rounded 16-bit output
+// (kCombine false) or store_combined(m, nn, v[TJ]) of the float sums of all
+// tiles of the call (kCombine true).
 // Dense: A row m is x row m; output (m, column n0 + nn).
 struct DenseRows {
+  static constexpr bool kCombine = false;
   const uint16_t* x;
   uint32_t x_nrec;
   uint16_t* out;
@@ -160,19 +191,48 @@ struct DenseRows {
   }
 };
 
-// One 16-row weight tile (rows n0 .. n0+rows-1 of a [*, K] quantized matrix
-// whose row n0 starts at wt / st / bt; rows <= 0 is an empty tile that only
-// joins the barriers) times M <= 16 A rows, computed by a group of NW waves:
-// kw is the (wave-uniform) wave index in the group, gt = 64 kw + lane.  The
-// group owns qmv_x_lds(NW, XM) (+ qmv_sb_lds(G) when SBL) bytes of LDS at
-// qmv_smem and red[0 .. NW-1].  Every wave of the workgroup calls it the same
-// number of times (it holds workgroup barriers); requires M <= XM when XM >
-// 0, and qmv_sb_fits when SBL.
-template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, class Rows>
-__device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char* __restrict__ st,
-                                         const char* __restrict__ bt, int rows, int M, int K,
-                                         const Rows& src, unsigned char* qmv_smem,
-                                         f32x4 (*red)[64], int kw, int gt) {
+// The tiles of one qmv_tile call: tile j is rows[j] (<= 16; <= 0 is an empty
+// tile) rows of a [*, K] quantized matrix whose first row starts at w[j] /
+// s[j] / b[j].  rows[] must be wave-uniform.
+template <int TJ>
+struct QmvTiles {
+  const char* w[TJ];
+  const char* s[TJ];
+  const char* b[TJ];
+  int rows[TJ];
+};
+
+template <class T, class Rows>
+__device__ __forceinline__ void rows_put(const Rows& src, int m, int nn, float v) {
+  src.store(m, nn, T::round1(v));
+}
+
+// Output (m, nn) of every tile: tile j's value goes to column 16 j + nn, or
+// a combining Rows (kCombine) turns the TJ values into one output.
+template <class T, int TJ, class Rows>
+__device__ __forceinline__ void rows_put_tiles(const Rows& src, int m, int nn,
+                                               const float (&v)[TJ], const int (&rows)[TJ]) {
+  if constexpr (Rows::kCombine) {
+    if (nn < rows[0]) src.store_combined(m, nn, v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      if (nn < rows[j]) rows_put<T>(src, m, 16 * j + nn, v[j]);
+  }
+}
+
+// TJ 16-row weight tiles times M <= 16 A rows, computed by a group of NW
+// waves: kw is the (wave-uniform) wave index in the group, gt = 64 kw + lane.
+// The TJ tiles share every x slice (x is read once per call, not per tile)
+// and each has its own accumulator, so a tile's sum does not depend on TJ.
+// The group owns qmv_x_lds(NW, XM) (+ TJ qmv_sb_lds(G) when SBL) bytes of
+// LDS at qmv_smem and red[0 .. NW*TJ-1].  Every wave of the workgroup calls
+// it the same number of times (it holds workgroup barriers); requires M <=
+// XM when XM > 0, and qmv_sb_fits(G, NW, TJ) when SBL.
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, class Rows>
+__device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, const Rows& src,
+                                         unsigned char* qmv_smem, f32x4 (*red)[64], int kw,
+                                         int gt) {
   using Gm = QmvGeom<BITS, GS, GPL>;
   constexpr int STEPG = Gm::STEPG, STEPB = Gm::STEPB, STEPK = Gm::STEPK, NSV = Gm::NSV;
   constexpr int NL = Gm::NL, CPL = Gm::CPL, MPL = Gm::MPL, SH = Gm::SH;
@@ -183,8 +243,8 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   constexpr int XSR = 2 * STEPK + 16;                     // LDS bytes per x row (padded)
   using T = T16<DT>;
   struct Stage {
-    u32x4 w[NL];
-    uint32_t s[SBL ? 1 : NSV], b[SBL ? 1 : NSV];
+    u32x4 w[TJ][NL];
+    uint32_t s[TJ][SBL ? 1 : NSV], b[TJ][SBL ? 1 : NSV];
     u32x4 xq[XPL];
   };
   const int lane = threadIdx.x & 63;
@@ -193,8 +253,13 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const int G = K / GS;
   const uint32_t sRowB = (uint32_t)G * 2;
-  const uint32_t w_nrec = rows > 0 ? (uint32_t)(rows - 1) * rowB + STEPB : 0u;
-  const uint32_t s_nrec = rows > 0 ? (uint32_t)(rows - 1) * sRowB + STEPG * 2 : 0u;
+  uint32_t w_nrec[TJ], s_nrec[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int rj = tl.rows[j];
+    w_nrec[j] = rj > 0 ? (uint32_t)(rj - 1) * rowB + STEPB : 0u;
+    s_nrec[j] = rj > 0 ? (uint32_t)(rj - 1) * sRowB + STEPG * 2 : 0u;
+  }
   const uint32_t wofs = (uint32_t)r * rowB + (uint32_t)c * 16;
   const uint32_t sofs = (uint32_t)r * sRowB;
   // scale of load L: half ((4 L + c) >> SH) & 3 of dword pair ((4 L) >> SH) >> 2
@@ -213,8 +278,8 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   const lds_u8* xl = xreg + xr * XSR;
   const uint16_t* xg = src.x + src.xoff(xr);
   const int SBS = qmv_sb_stride(G);
-  lds_u8* sbl_s = (lds_u8*)qmv_smem + NW * (XM ? XM : 1) * XSR;
-  lds_u8* sbl_b = sbl_s + 16 * SBS;
+  // tile j's scale rows at sbl + j * 32 SBS, its bias rows 16 SBS further
+  lds_u8* sbl = (lds_u8*)qmv_smem + NW * (XM ? XM : 1) * XSR;
   // XM > 0: byte offset of this lane's x pieces from the step's x slice;
   // pieces of rows >= M are out of the buffer range (no memory access, zeros)
   uint32_t xvo[XPL];
@@ -236,30 +301,38 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
       for (int q = 0; q < XPL; ++q)
         s.xq[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, xvo[q], 0, 0);
     }
-    const auto rw = make_rsrc(wt + (int64_t)t * STEPB, live ? w_nrec : 0u);
 #pragma unroll
-    for (int L = 0; L < NL; ++L)
-      s.w[L] = __builtin_amdgcn_raw_buffer_load_b128(rw, wofs + L * 64, 0, 0);
+    for (int j = 0; j < TJ; ++j) {
+      const auto rw = make_rsrc(tl.w[j] + (int64_t)t * STEPB, live ? w_nrec[j] : 0u);
+#pragma unroll
+      for (int L = 0; L < NL; ++L)
+        s.w[j][L] = __builtin_amdgcn_raw_buffer_load_b128(rw, wofs + L * 64, 0, 0);
+    }
     if constexpr (!SBL) {
-      const auto rs = make_rsrc(st + (int64_t)t * STEPG * 2, live ? s_nrec : 0u);
-      const auto rb = make_rsrc(bt + (int64_t)t * STEPG * 2, live ? s_nrec : 0u);
-      if constexpr (NSV == 2) {
-        const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rs, sofs, 0, 0);
-        const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(rb, sofs, 0, 0);
-        s.s[0] = a[0]; s.s[1] = a[1]; s.b[0] = q[0]; s.b[1] = q[1];
-      } else {
 #pragma unroll
-        for (int v = 0; v < NSV / 4; ++v) {
-          const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, sofs + 16 * v, 0, 0);
-          const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rb, sofs + 16 * v, 0, 0);
+      for (int j = 0; j < TJ; ++j) {
+        const auto rs = make_rsrc(tl.s[j] + (int64_t)t * STEPG * 2, live ? s_nrec[j] : 0u);
+        const auto rb = make_rsrc(tl.b[j] + (int64_t)t * STEPG * 2, live ? s_nrec[j] : 0u);
+        if constexpr (NSV == 2) {
+          const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rs, sofs, 0, 0);
+          const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(rb, sofs, 0, 0);
+          s.s[j][0] = a[0]; s.s[j][1] = a[1]; s.b[j][0] = q[0]; s.b[j][1] = q[1];
+        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) { s.s[4 * v + e] = a[e]; s.b[4 * v + e] = q[e]; }
+          for (int v = 0; v < NSV / 4; ++v) {
+            const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, sofs + 16 * v, 0, 0);
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rb, sofs + 16 * v, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { s.s[j][4 * v + e] = a[e]; s.b[j][4 * v + e] = q[e]; }
+          }
         }
       }
     }
   };
 
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // A fragment covering codes [k, k+8): k relative to the step (LDS slice) or
   // absolute (global).  Codes past K read zeros (LDS slices are zeroed there).
@@ -289,90 +362,114 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    uint32_t sv[NSV], bv[NSV];
-    if constexpr (SBL) {
-      const lds_u8* ps = sbl_s + r * SBS + t * STEPG * 2;
-      const lds_u8* pb = sbl_b + r * SBS + t * STEPG * 2;
-      if constexpr (NSV == 2) {
-        const u32x2 a = *(const lds_u32x2*)ps, q = *(const lds_u32x2*)pb;
-        sv[0] = a[0]; sv[1] = a[1]; bv[0] = q[0]; bv[1] = q[1];
-      } else {
-#pragma unroll
-        for (int v = 0; v < NSV / 4; ++v) {
-          const u32x4 a = *(const lds_u32x4*)(ps + 16 * v);
-          const u32x4 q = *(const lds_u32x4*)(pb + 16 * v);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { sv[4 * v + e] = a[e]; bv[4 * v + e] = q[e]; }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int v = 0; v < NSV; ++v) { sv[v] = s.s[v]; bv[v] = s.b[v]; }
-    }
-    float sf[NL], bf[NL];
+    float sf[TJ][NL], bf[TJ][NL];
     bool big = false;
 #pragma unroll
-    for (int L = 0; L < NL; ++L) {
-      const int q = ((4 * L) >> SH) >> 2;     // same for the 4 lanes of a row
-      sf[L] = selected_to_f32<DT>(__builtin_amdgcn_perm(sv[2 * q + 1], sv[2 * q], selL[L]));
-      bf[L] = selected_to_f32<DT>(__builtin_amdgcn_perm(bv[2 * q + 1], bv[2 * q], selL[L]));
-      if (checked && t * STEPG + ((4 * L + c) >> SH) >= G) { sf[L] = 0.f; bf[L] = 0.f; }
-      big |= needs_plain(sf[L]);
+    for (int j = 0; j < TJ; ++j) {
+      uint32_t sv[NSV], bv[NSV];
+      if constexpr (SBL) {
+        const lds_u8* ps = sbl + j * 32 * SBS + r * SBS + t * STEPG * 2;
+        const lds_u8* pb = ps + 16 * SBS;
+        if constexpr (NSV == 2) {
+          const u32x2 a = *(const lds_u32x2*)ps, q = *(const lds_u32x2*)pb;
+          sv[0] = a[0]; sv[1] = a[1]; bv[0] = q[0]; bv[1] = q[1];
+        } else {
+#pragma unroll
+          for (int v = 0; v < NSV / 4; ++v) {
+            const u32x4 a = *(const lds_u32x4*)(ps + 16 * v);
+            const u32x4 q = *(const lds_u32x4*)(pb + 16 * v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { sv[4 * v + e] = a[e]; bv[4 * v + e] = q[e]; }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < NSV; ++v) { sv[v] = s.s[j][v]; bv[v] = s.b[j][v]; }
+      }
+#pragma unroll
+      for (int L = 0; L < NL; ++L) {
+        const int q = ((4 * L) >> SH) >> 2;     // same for the 4 lanes of a row
+        sf[j][L] = selected_to_f32<DT>(__builtin_amdgcn_perm(sv[2 * q + 1], sv[2 * q], selL[L]));
+        bf[j][L] = selected_to_f32<DT>(__builtin_amdgcn_perm(bv[2 * q + 1], bv[2 * q], selL[L]));
+        if (checked && t * STEPG + ((4 * L + c) >> SH) >= G) { sf[j][L] = 0.f; bf[j][L] = 0.f; }
+        big |= needs_plain(sf[j][L]);
+      }
     }
     const int kr = c * CPL;                   // lane's first code, relative to the step
     const int kt = t * STEPK + kr;            // same, absolute
     if (__builtin_amdgcn_ballot_w64(big) == 0) {
 #pragma unroll
       for (int L = 0; L < NL; ++L) {
-        const GroupScale g = make_group(sf[L], bf[L]);
+        GroupScale g[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) g[j] = make_group(sf[j][L], bf[j][L]);
 #pragma unroll
         for (int p = 0; p < MPL; ++p) {
-          uint32_t bo[4];
-          if constexpr (BITS == 4) {
-            deq4_word<DT>(s.w[L][p], g, bo);
-          } else {
-            deq8_word<DT>(s.w[L][2 * p], g, bo);
-            deq8_word<DT>(s.w[L][2 * p + 1], g, bo + 2);
-          }
           const int ko = 4 * L * CPL + 8 * p;
           const u32x4 a = afrag(kr + ko, kt + ko, checked);
-          acc = T::mfma(a, (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc);
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            uint32_t bo[4];
+            if constexpr (BITS == 4) {
+              deq4_word<DT>(s.w[j][L][p], g[j], bo);
+            } else {
+              deq8_word<DT>(s.w[j][L][2 * p], g[j], bo);
+              deq8_word<DT>(s.w[j][L][2 * p + 1], g[j], bo + 2);
+            }
+            acc[j] = T::mfma(a, (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc[j]);
+          }
         }
       }
     } else {
 #pragma unroll
       for (int L = 0; L < NL; ++L) {
-        const GroupScale g = make_group(sf[L], bf[L]);
+        GroupScale g[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) g[j] = make_group(sf[j][L], bf[j][L]);
 #pragma unroll
         for (int p = 0; p < MPL; ++p) {
-          uint32_t bo[4];
-          if constexpr (BITS == 4) {
-            deq_word_plain<DT, 4>(s.w[L][p], g, bo);
-          } else {
-            deq_word_plain<DT, 8>(s.w[L][2 * p], g, bo);
-            deq_word_plain<DT, 8>(s.w[L][2 * p + 1], g, bo + 2);
-          }
           const int ko = 4 * L * CPL + 8 * p;
           const u32x4 a = afrag(kr + ko, kt + ko, checked);
-          acc = T::mfma(a, (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc);
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            uint32_t bo[4];
+            if constexpr (BITS == 4) {
+              deq_word_plain<DT, 4>(s.w[j][L][p], g[j], bo);
+            } else {
+              deq_word_plain<DT, 8>(s.w[j][L][2 * p], g[j], bo);
+              deq_word_plain<DT, 8>(s.w[j][L][2 * p + 1], g[j], bo + 2);
+            }
+            acc[j] = T::mfma(a, (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc[j]);
+          }
         }
       }
     }
   };
 
   // ---- scale/bias copy: loads issued ahead of the weight prologue ---------
+  // Chunk i (16 bytes of scales and of biases) of the TJ tiles: tile
+  // i / (16 cpr), 16-byte chunk i % (16 cpr) of that tile's contiguous rows.
+  // Each tile's buffer range ends at its last row, so a lane's chunk loads
+  // from exactly one tile and reads zeros from the others.
   Stage S[PF];
   u32x4 sbq[2][SBL ? kQmvSbChunks : 1];
   const int cpr = G / 8;                      // 16-byte chunks per scale row (SBL)
-  const int nch = max(rows, 0) * cpr;         // chunks of each of s and b
+  const int tch = 16 * cpr;                   // chunks per tile
   if constexpr (SBL) {
-    const auto rs0 = make_rsrc(st, (uint32_t)nch * 16u);
-    const auto rb0 = make_rsrc(bt, (uint32_t)nch * 16u);
 #pragma unroll
     for (int u = 0; u < kQmvSbChunks; ++u) {
       const uint32_t i = gt + u * 64 * NW;
-      sbq[0][u] = __builtin_amdgcn_raw_buffer_load_b128(rs0, i * 16u, 0, 0);
-      sbq[1][u] = __builtin_amdgcn_raw_buffer_load_b128(rb0, i * 16u, 0, 0);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const uint32_t nb = (uint32_t)(max(tl.rows[j], 0) * cpr) * 16u;
+        const auto rs0 = make_rsrc(tl.s[j], nb);
+        const auto rb0 = make_rsrc(tl.b[j], nb);
+        const uint32_t o = (i - (uint32_t)(j * tch)) * 16u;   // wraps past the range below
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs0, o, 0, 0);
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rb0, o, 0, 0);
+        sbq[0][u] = j ? (sbq[0][u] | a) : a;
+        sbq[1][u] = j ? (sbq[1][u] | q) : q;
+      }
     }
   }
   // ---- main loop: PF-stage pipeline over the unchecked steps --------------
@@ -382,10 +479,13 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
 #pragma unroll
     for (int u = 0; u < kQmvSbChunks; ++u) {
       const int i = gt + u * 64 * NW;
-      if (i < nch) {
-        const int rr = i / cpr, cc = i - rr * cpr;
-        *(lds_u32x4*)(sbl_s + rr * SBS + cc * 16) = sbq[0][u];
-        *(lds_u32x4*)(sbl_b + rr * SBS + cc * 16) = sbq[1][u];
+      if (i < TJ * tch) {
+        const int j = TJ == 1 ? 0 : i / tch;
+        const int ii = i - j * tch;
+        const int rr = ii / cpr, cc = ii - rr * cpr;
+        lds_u8* d = sbl + j * 32 * SBS + rr * SBS + cc * 16;
+        *(lds_u32x4*)d = sbq[0][u];
+        *(lds_u32x4*)(d + 16 * SBS) = sbq[1][u];
       }
     }
     __syncthreads();
@@ -393,8 +493,8 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
   for (int t = sb; t < fe; t += PF) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int tl = t + i + PF - 1;
-      load(S[(i + PF - 1) % PF], tl, tl < fe);
+      const int tl2 = t + i + PF - 1;
+      load(S[(i + PF - 1) % PF], tl2, tl2 < fe);
       if (t + i < fe) compute(S[i], t + i, false);
     }
   }
@@ -403,8 +503,10 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
     Stage s;
     load(s, fe, true);
 #pragma unroll
-    for (int L = 0; L < NL; ++L)
-      if (fe * STEPG + ((4 * L + c) >> SH) >= G) s.w[L] = (u32x4){0u, 0u, 0u, 0u};
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int L = 0; L < NL; ++L)
+        if (fe * STEPG + ((4 * L + c) >> SH) >= G) s.w[j][L] = (u32x4){0u, 0u, 0u, 0u};
     compute(s, fe, true);
   }
 
@@ -414,28 +516,36 @@ __device__ __forceinline__ void qmv_tile(const char* __restrict__ wt, const char
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = 4 * c + v;
-      if (m < M && r < rows) src.store(m, r, T::round1(acc[v]));
+      float val[TJ];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) val[j] = acc[j][v];
+      if (m < M) rows_put_tiles<T, TJ>(src, m, r, val, tl.rows);
     }
   } else {
-    red[wave][lane] = acc;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) red[wave * TJ + j][lane] = acc[j];
     __syncthreads();
     for (int tt = gt; tt < 256; tt += 64 * NW) {
       const int mm = tt >> 4, nn = tt & 15;
       const int sl = ((mm >> 2) << 4) | nn, v = mm & 3;
-      float sum = red[0][sl][v];
+      float sum[TJ];
 #pragma unroll
-      for (int q = 1; q < NW; ++q) sum += red[q][sl][v];
-      if (mm < M && nn < rows) src.store(mm, nn, T::round1(sum));
+      for (int j = 0; j < TJ; ++j) {
+        sum[j] = red[j][sl][v];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) sum[j] += red[q * TJ + j][sl][v];
+      }
+      if (mm < M) rows_put_tiles<T, TJ>(src, mm, nn, sum, tl.rows);
     }
     // the next tile of this workgroup reuses red and the LDS copies
     __syncthreads();
   }
 }
 
-// grid.x = ceil(N / 16) tiles, block = 64 * NW threads, dynamic LDS
-// qmv_x_lds<BITS, GS, GPL>(NW, XM) (+ qmv_sb_lds(K / GS) when SBL) bytes;
-// M <= XM unless XM == 0, and then ((M - 1) * ldx + K) * 2 < 2^31.
-template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL>
+// grid.x = ceil(N / (16 TJ)) workgroups of TJ tiles, block = 64 * NW threads,
+// dynamic LDS qmv_x_lds<BITS, GS, GPL>(NW, XM) (+ TJ qmv_sb_lds(K / GS) when
+// SBL) bytes; M <= XM unless XM == 0, and then ((M - 1) * ldx + K) * 2 < 2^31.
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ>
 __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict__ x,
                                                       const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ scales,
@@ -443,54 +553,86 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
                                                       uint16_t* __restrict__ out, int M, int N,
                                                       int K, int64_t ldx, int64_t ldo) {
   extern __shared__ __align__(16) unsigned char qmv_smem[];
-  __shared__ f32x4 red[NW][64];
-  const int n0 = blockIdx.x * 16;
+  __shared__ f32x4 red[NW * TJ][64];
+  const int n0 = blockIdx.x * 16 * TJ;
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  QmvTiles<TJ> tl;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int nj = n0 + 16 * j;
+    const int rj = min(16, N - nj);
+    const int64_t base = rj > 0 ? nj : 0;
+    tl.w[j] = reinterpret_cast<const char*>(w) + base * rowB;
+    tl.s[j] = reinterpret_cast<const char*>(scales) + base * sRowB;
+    tl.b[j] = reinterpret_cast<const char*>(biases) + base * sRowB;
+    tl.rows[j] = rj;
+  }
   const DenseRows src{x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2), out, ldx, ldo, n0};
-  qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL>(
-      reinterpret_cast<const char*>(w) + (int64_t)n0 * rowB,
-      reinterpret_cast<const char*>(scales) + (int64_t)n0 * sRowB,
-      reinterpret_cast<const char*>(biases) + (int64_t)n0 * sRowB, min(16, N - n0), M, K, src,
-      qmv_smem, red, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x);
+  qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL, TJ>(
+      tl, M, K, src, qmv_smem, red, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+      threadIdx.x);
+}
+
+// One skinny launch of M <= 16 rows.  Launches above 64 KiB of dynamic LDS
+// (16 streamed rows with 8 waves) need the kernel's limit raised once.
+template <int DT, int BITS, int GS, int NW, int XM, bool SBL, int TJ>
+inline int skinny_launch_one(const uint16_t* x, const uint32_t* w, const void* s, const void* b,
+                             uint16_t* out, int M, int64_t N, int64_t K, size_t lds,
+                             hipStream_t st) {
+  using C = QmvConf<BITS, GS>;
+  auto kern = &qmv_kernel<DT, BITS, GS, C::GPL, NW, C::PF, XM, SBL, TJ>;
+  if (lds > 65536) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)qmv_lds_bound<BITS, GS, C::GPL>(NW, XM, SBL, TJ));
+    if (attr != hipSuccess) return (int)attr;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TJ - 1) / (16 * TJ))), dim3(64 * NW), lds, st,
+                     x, w, (const uint16_t*)s, (const uint16_t*)b, out, M, (int)N, (int)K,
+                     (int64_t)K, (int64_t)N);
+  return 0;
 }
 
 template <int DT, int BITS, int GS, int NW>
-inline void skinny_launch_nw(const void* x, const uint32_t* w, const void* s, const void* b,
-                             void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, const void* b,
+                            void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
   using C = QmvConf<BITS, GS>;
-  const unsigned grid = (unsigned)((N + 15) / 16);
-  const bool sbl = qmv_sb_fits(K / GS, NW, s, b);
-  const size_t sb_lds = qmv_sb_lds((int)(K / GS));
-  auto lds_for = [&](int xmax, bool with_sb) {
-    return qmv_x_lds<BITS, GS, C::GPL>(NW, xmax) + (with_sb ? sb_lds : 0);
-  };
+  const int G = (int)(K / GS);
   for (int64_t m0 = 0; m0 < M; m0 += 16) {
     const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
     const uint16_t* xp = (const uint16_t*)x + m0 * K;
     uint16_t* op = (uint16_t*)out + m0 * N;
-    // x streams through LDS for up to 8 rows whose bytes a buffer range covers;
-    // without the scale copy only the 8-row streamed-x variant is built
-    int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? qmv_xm_for(mt) : 0;
-    if (!sbl && xm) xm = kQmvMaxXM;
-#define MQ_SX(X, SB)                                                                        \
-    if (xm == X && sbl == SB)                                                               \
-      hipLaunchKernelGGL((qmv_kernel<DT, BITS, GS, C::GPL, NW, C::PF, X, SB>), dim3(grid),    \
-                         dim3(64 * NW), lds_for(X, SB), st, xp, w, (const uint16_t*)s,      \
-                         (const uint16_t*)b, op, mt, (int)N, (int)K, (int64_t)K, (int64_t)N);
-    MQ_SX(0, true) MQ_SX(1, true) MQ_SX(2, true) MQ_SX(4, true) MQ_SX(8, true)
-    MQ_SX(0, false) MQ_SX(8, false)
+    // x streams through LDS when a buffer range covers its bytes
+    int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? qmv_skinny_xm_for<BITS, GS, C::GPL>(mt)
+                                                        : 0;
+    int tj = qmv_tj_for(xm);
+    if (tj == 2 && !qmv_sb_fits(G, NW, 2, s, b)) tj = 1;
+    const bool sbl = qmv_sb_fits(G, NW, tj, s, b);
+    // without the scale copy: one tile per workgroup, 8 or 16 streamed rows
+    if (!sbl && xm) xm = xm > kQmvMaxXM ? 16 : kQmvMaxXM;
+    const size_t lds = qmv_x_lds<BITS, GS, C::GPL>(NW, xm) + (sbl ? tj * qmv_sb_lds(G) : 0);
+    int rc = kStatusUnsupported;
+#define MQ_SX(X, SB, J)                                                                   \
+    if (xm == X && sbl == SB && tj == J)                                                  \
+      rc = skinny_launch_one<DT, BITS, GS, NW, X, SB, J>(xp, w, s, b, op, mt, N, K, lds, st);
+    MQ_SX(0, true, 1) MQ_SX(1, true, 1) MQ_SX(2, true, 1) MQ_SX(4, true, 1)
+    MQ_SX(8, true, 1) MQ_SX(8, true, 2) MQ_SX(0, false, 1) MQ_SX(8, false, 1)
+    if constexpr (QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
+      MQ_SX(16, true, 1) MQ_SX(16, true, 2) MQ_SX(16, false, 1)
+    }
 #undef MQ_SX
+    if (rc) return rc;
   }
+  return 0;
 }
 
 template <int DT, int BITS, int GS>
 int SkinnyLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
                                     const void* b, void* out, int64_t M, int64_t N, int64_t K,
                                     hipStream_t st) {
-  if (qmv_nw_for(N) == 8) skinny_launch_nw<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, st);
-  else skinny_launch_nw<DT, BITS, GS, 4>(x, w, s, b, out, M, N, K, st);
-  return 0;
+  if (qmv_nw_for(N) == 8) return skinny_launch_nw<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, st);
+  return skinny_launch_nw<DT, BITS, GS, 4>(x, w, s, b, out, M, N, K, st);
 }
 
 }  // namespace mq

@@ -118,11 +118,23 @@ class SwitchGLU(torch.nn.Module):
     SORT_THRESHOLD = 64
 
     def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
-                 down_proj: QuantizedSwitchLinear):
+                 down_proj: QuantizedSwitchLinear, fuse_gate_up: bool = False):
+        """``fuse_gate_up``: at decode widths (fewer than 1024 pairs) compute
+        ``silu(gate) * up`` in one fused kernel (:func:`ops.gather_glu`, float
+        sums, one rounding) with no expert sort -- the reference's opt-in
+        ``moe_dec_fused`` route (fused.py:2456-2492).  Off by default, as in
+        the reference, because it rounds differently from mlx-lm's SwiGLU."""
         super().__init__()
         self.gate_proj = gate_proj
         self.up_proj = up_proj
         self.down_proj = down_proj
+        self.fuse_gate_up = fuse_gate_up
+
+    def _fused(self, pairs: int) -> bool:
+        g, u = self.gate_proj, self.up_proj
+        return (self.fuse_gate_up and pairs < ops._GLU_FUSED_MAX_ROWS and g.bias is None
+                and u.bias is None and g.weight.shape == u.weight.shape
+                and (g.group_size, g.bits, g.mode) == (u.group_size, u.bits, u.mode))
 
     def forward(self, x: torch.Tensor, indices: torch.Tensor,
                 scores: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -135,6 +147,17 @@ class SwitchGLU(torch.nn.Module):
         top_k = indices.shape[-1]
         xe = x.reshape(-1, 1, 1, x.shape[-1])                      # (T, 1, 1, K)
         idx = indices.reshape(-1, top_k)
+        if self._fused(idx.numel()):
+            g, u = self.gate_proj, self.up_proj
+            h = ops.gather_glu(xe, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases,
+                               rhs_indices=idx, group_size=g.group_size, bits=g.bits,
+                               mode=g.mode)                        # (T, k, 1, I)
+            y = self.down_proj(h, idx)                             # (T, k, 1, N)
+            if scores is not None:
+                out = ops.moe_combine(y.reshape(-1, y.shape[-1]), None, scores.reshape(-1),
+                                      idx.shape[0], top_k)
+                return out.reshape(*lead, y.shape[-1])
+            return y.reshape(*lead, top_k, y.shape[-1])
         do_sort = idx.numel() >= self.SORT_THRESHOLD
         if do_sort:
             flat = idx.reshape(-1)

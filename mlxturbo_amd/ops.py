@@ -10,6 +10,9 @@ MLX 0.32's operators as the reference calls them:
   QuantizedSwitchLinear (mlxturbo/fused.py:2389-2394, 3105-3116)
 * ``dequantize(w, scales, biases, group_size, bits, mode)`` - mx.dequantize
   (bench/test_qmm_wide_shapes.py:35-42)
+* ``gather_glu`` - fused MoE gate+up+SiLU (kernels/moe_glu.py:145-168)
+* ``moe_combine`` - MoE unsort + router weight + top-k sum
+  (kernels/moe_combine.py:160-195)
 
 Errors: genuinely invalid arguments raise ``ValueError`` as MLX does;
 configurations the reference never accelerates and this build does not
@@ -205,32 +208,29 @@ def _as_index(t, dev) -> torch.Tensor:
     return t.to(device=dev)
 
 
-def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
-               biases: Optional[torch.Tensor] = None, lhs_indices=None, rhs_indices=None,
-               transpose: bool = True, group_size: int = 64, bits: int = 4,
-               mode: str = "affine", sorted_indices: bool = False) -> torch.Tensor:
-    """``mx.gather_qmm``: per index pair, ``x[lhs] @ dequantize(w[rhs]).T``.
-
-    ``x`` is ``(..., M, K)`` and ``w`` ``(..., N, K*bits/32)``; ``lhs_indices``
-    index x's batch dims (default: all of them), ``rhs_indices`` index w's
-    batch dims (default: all of them); the two broadcast together and the
-    output is ``broadcast_shape + (M, N)``.
-    """
-    _check_mode(mode, biases)
-    dev = _require_gpu(x, w, scales, biases)
+def _gather_prep(x, banks, lhs_indices, rhs_indices, transpose, group_size, bits, mode):
+    """Validation and flattening shared by gather_qmm and gather_glu; ``banks``
+    is a list of (w, scales, biases) of one shape."""
+    for _, _, b in banks:
+        _check_mode(mode, b)
+    dev = _require_gpu(x, *[t for bank in banks for t in bank])
     if not transpose:
         raise NotImplementedError("transpose=False is not on this path")
-    if x.ndim < 2 or w.ndim < 3:
+    w0 = banks[0][0]
+    if x.ndim < 2 or w0.ndim < 3:
         raise ValueError("gather_qmm needs x (..., M, K) and w (..., N, K*bits/32) with a batch dim")
-    K = _check_quant(w, scales, biases, group_size, bits)
+    for w, s, b in banks:
+        if w.shape != w0.shape:
+            raise ValueError(f"expert banks differ in shape: {tuple(w.shape)} and {tuple(w0.shape)}")
+        K = _check_quant(w, s, b, group_size, bits)
     if x.shape[-1] != K:
         raise ValueError(
             f"x last dimension {x.shape[-1]} does not match the quantized weight K={K}")
-    code = _dtype_code(x.dtype, scales.dtype)
+    code = _dtype_code(x.dtype, banks[0][1].dtype)
     M = x.shape[-2]
-    N = w.shape[-2]
+    N = w0.shape[-2]
     bx = tuple(x.shape[:-2])
-    bw = tuple(w.shape[:-2])
+    bw = tuple(w0.shape[:-2])
     B = math.prod(bx)
     E = math.prod(bw)
     lhs = None if lhs_indices is None else _as_index(lhs_indices, dev)
@@ -245,27 +245,93 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     P = math.prod(shape)
     out = torch.empty((*shape, M, N), dtype=x.dtype, device=dev)
     if P == 0 or M == 0 or N == 0:
-        return out
+        return out, None
     if M > 16:
         raise NotImplementedError(f"gather_qmm with M={M} rows per pair (> 16)")
     lhs_f = (_default_lhs(dev, bx, tuple(shape)) if lhs is None
              else lhs.expand(shape).reshape(-1).to(torch.int32).contiguous())
     rhs_f = rhs.expand(shape).reshape(-1).to(torch.int32).contiguous()
     x_ = _aligned(x.reshape(B, M, K))
-    w_ = _aligned(w.reshape(E, N, w.shape[-1]))
-    s_ = _aligned(scales.reshape(E, N, scales.shape[-1]))
-    b_ = _aligned(biases.reshape(E, N, biases.shape[-1]))
+    flat = []
+    for w, s, b in banks:
+        flat += [_aligned(w.reshape(E, N, w.shape[-1])),
+                 _aligned(s.reshape(E, N, s.shape[-1])),
+                 _aligned(b.reshape(E, N, b.shape[-1]))]
     lib = _lib.lib()
     nbytes = int(lib.mq_gather_qmm_workspace_size(P, M))
     ws = _workspace(dev, nbytes) if nbytes else None
-    rc = lib.mq_gather_qmm(x_.data_ptr(), w_.data_ptr(), s_.data_ptr(), b_.data_ptr(),
-                           lhs_f.data_ptr() if lhs_f is not None else None,
-                           rhs_f.data_ptr(), out.data_ptr(), P, B, M, N, K, E,
-                           group_size, bits, code, int(bool(sorted_indices)),
-                           ws.data_ptr() if ws is not None else None,
-                           ws.numel() if ws is not None else 0, _stream_ptr(out))
+    args = dict(x=x_, flat=flat, lhs=lhs_f, rhs=rhs_f, P=P, B=B, M=M, N=N, K=K, E=E, code=code,
+                ws=ws, lib=lib)
+    return out, args
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return t.data_ptr() if t is not None else None
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+               biases: Optional[torch.Tensor] = None, lhs_indices=None, rhs_indices=None,
+               transpose: bool = True, group_size: int = 64, bits: int = 4,
+               mode: str = "affine", sorted_indices: bool = False) -> torch.Tensor:
+    """``mx.gather_qmm``: per index pair, ``x[lhs] @ dequantize(w[rhs]).T``.
+
+    ``x`` is ``(..., M, K)`` and ``w`` ``(..., N, K*bits/32)``; ``lhs_indices``
+    index x's batch dims (default: all of them), ``rhs_indices`` index w's
+    batch dims (default: all of them); the two broadcast together and the
+    output is ``broadcast_shape + (M, N)``.
+    """
+    out, a = _gather_prep(x, [(w, scales, biases)], lhs_indices, rhs_indices, transpose,
+                          group_size, bits, mode)
+    if a is None:
+        return out
+    ws = a["ws"]
+    rc = a["lib"].mq_gather_qmm(a["x"].data_ptr(), *[t.data_ptr() for t in a["flat"]],
+                                _ptr(a["lhs"]), a["rhs"].data_ptr(), out.data_ptr(), a["P"],
+                                a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
+                                a["code"], int(bool(sorted_indices)), _ptr(ws),
+                                ws.numel() if ws is not None else 0, _stream_ptr(out))
     _lib.check(rc, "gather_qmm")
     return out
+
+
+def gather_glu(x: torch.Tensor, gate_w: torch.Tensor, gate_scales: torch.Tensor,
+               gate_biases: Optional[torch.Tensor], up_w: torch.Tensor,
+               up_scales: torch.Tensor, up_biases: Optional[torch.Tensor],
+               lhs_indices=None, rhs_indices=None, transpose: bool = True,
+               group_size: int = 64, bits: int = 4, mode: str = "affine",
+               sorted_indices: bool = False) -> torch.Tensor:
+    """Fused MoE gate+up+SiLU: ``silu(g) * u`` with ``g``, ``u`` the
+    :func:`gather_qmm` products of the gate and up banks (same indices and
+    broadcasting), summed in float and rounded once -- the reference's
+    ``moe_glu.fused_glu`` (kernels/moe_glu.py:145-168) and
+    ``moe_decode_fused.gate_up`` (kernels/moe_decode_fused.py:331-350).
+
+    Fused in one kernel below 1024 output rows (decode / verify).  Above it
+    (prefill) the result is composed from two :func:`gather_qmm` calls and
+    a float SiLU-multiply of their rounded outputs, as the reference keeps
+    its stock path outside decode widths (fused.py:2476-2479)."""
+    out, a = _gather_prep(x, [(gate_w, gate_scales, gate_biases), (up_w, up_scales, up_biases)],
+                          lhs_indices, rhs_indices, transpose, group_size, bits, mode)
+    if a is None:
+        return out
+    if a["P"] * a["M"] >= _GLU_FUSED_MAX_ROWS:
+        kw = dict(lhs_indices=lhs_indices, rhs_indices=rhs_indices, group_size=group_size,
+                  bits=bits, mode=mode, sorted_indices=sorted_indices)
+        g = gather_qmm(x, gate_w, gate_scales, gate_biases, **kw)
+        u = gather_qmm(x, up_w, up_scales, up_biases, **kw)
+        return (torch.nn.functional.silu(g.float()) * u.float()).to(x.dtype)
+    ws = a["ws"]
+    rc = a["lib"].mq_gather_glu(a["x"].data_ptr(), *[t.data_ptr() for t in a["flat"]],
+                                _ptr(a["lhs"]), a["rhs"].data_ptr(), out.data_ptr(), a["P"],
+                                a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
+                                a["code"], _ptr(ws), ws.numel() if ws is not None else 0,
+                                _stream_ptr(out))
+    _lib.check(rc, "gather_glu")
+    return out
+
+
+# mq_gather_glu fuses below this many output rows (P * M)
+_GLU_FUSED_MAX_ROWS = 1024
 
 
 def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, rows: int,
@@ -311,5 +377,5 @@ def launch_count() -> int:
     return _lib.launch_count()
 
 
-__all__: Sequence[str] = ("dequantize", "quantized_matmul", "gather_qmm", "moe_combine",
-                          "launch_count")
+__all__: Sequence[str] = ("dequantize", "quantized_matmul", "gather_qmm", "gather_glu",
+                          "moe_combine", "launch_count")

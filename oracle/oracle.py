@@ -23,6 +23,10 @@ dequantize             closed form cases: q=0 -> b, s=0 -> b, exactness of
 quantized_matmul_ref   brute-force pure-Python loop on tiny shapes, linearity
                        in x, row independence, column independence
 gather_qmm_ref         dense matmul on w[idx] per pair, sort invariance
+gather_glu_ref         closed-form SiLU values (silu(0) = 0, silu(1) =
+                       1/(1+e^-1), silu(x) -> x / 0 at +-20), a zero gate
+                       bank zeroes the output whatever the up bank, swapping
+                       gate and up changes it, linearity in the up bank
 moe_combine_ref        pure-Python loop on tiny shapes, one-hot weights copy
                        rows, identity inv equals the unsorted layout, linearity
                        in w
@@ -202,6 +206,23 @@ def gather_qmm_ref(x, w, scales, biases, lhs_indices, rhs_indices,
         xf = to_f32(x[int(lhs[p])], dtype).astype(np.float64)
         out.append(xf @ cache[e].T if transpose else xf @ cache[e])
     return np.stack(out).astype(np.float32)
+
+
+def gather_glu_ref(x, gate, up, lhs_indices, rhs_indices, group_size: int = 64,
+                   bits: int = 4, dtype: str = "bfloat16") -> np.ndarray:
+    """Fused MoE gate+up+SiLU: ``silu(g) * u`` with ``g`` / ``u`` the
+    :func:`gather_qmm_ref` products of the gate and up banks (``gate`` and
+    ``up`` are ``(w, scales, biases)``), ``silu(g) = g / (1 + exp(-g))``,
+    evaluated in float64 and returned un-rounded float32 ``[P, M, N]``.
+    Restates the epilogue of kernels/moe_glu.py:94-101 (float sums, float
+    sigmoid, product rounded once to T) and kernels/moe_decode_fused.py:
+    135-223 (same epilogue with per-token x rows)."""
+    g = gather_qmm_ref(x, *gate, lhs_indices, rhs_indices, group_size, bits, dtype)
+    u = gather_qmm_ref(x, *up, lhs_indices, rhs_indices, group_size, bits, dtype)
+    g = g.astype(np.float64)
+    with np.errstate(over="ignore"):
+        act = g / (1.0 + np.exp(-g))
+    return (act * u.astype(np.float64)).astype(np.float32)
 
 
 # ------------------------------------------------------------- moe combine

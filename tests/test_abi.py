@@ -153,6 +153,15 @@ class _FakeLib:
                                           lhs_null=not lhs, rhs=read(rhs), sorted=sorted_)))
         return 0
 
+    def mq_gather_glu(self, x, wg, sg, bg, wu, su, bu, lhs, rhs, out, P, B, M, N, K, E, gs,
+                      bits, dtype, ws, wsb, stream):
+        read = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
+                                               shape=(P,)).copy()
+        self.calls.append(("glu", dict(P=P, B=B, M=M, N=N, K=K, E=E, gate=(wg, sg, bg),
+                                       up=(wu, su, bu), rhs=read(rhs),
+                                       lhs=read(lhs) if lhs else np.arange(P))))
+        return 0
+
     def mq_dequantize(self, w, s, b, out, N, K, gs, bits, dtype, stream):
         self.calls.append(("deq", dict(N=N, K=K, gs=gs, bits=bits, dtype=dtype)))
         return 0
@@ -274,3 +283,31 @@ def test_combine_passes_indices_and_weights(fake):
         mlxturbo_amd.moe_combine(y[:5], None, w, rows, top_k)
     with pytest.raises(ValueError):
         mlxturbo_amd.moe_combine(y, inv[:4], w, rows, top_k)
+
+
+def test_glu_passes_both_banks(fake):
+    T, top, E, N, K = 3, 4, 8, 32, 256
+    gate, up = _qweights(N, K, E=E), _qweights(N, K, E=E)
+    x = torch.zeros(T, 1, 1, K, dtype=torch.bfloat16)
+    idx = torch.tensor([[0, 3, 5, 1], [3, 0, 2, 4], [3, 5, 0, 7]], dtype=torch.int32)
+    out = mlxturbo_amd.gather_glu(x, *gate, *up, rhs_indices=idx)
+    assert out.shape == (T, top, 1, N)
+    kind, c = fake.calls[-1]
+    assert kind == "glu" and (c["P"], c["B"], c["M"], c["E"]) == (T * top, T, 1, E)
+    assert c["gate"] == tuple(t.data_ptr() for t in gate)
+    assert c["up"] == tuple(t.data_ptr() for t in up)
+    np.testing.assert_array_equal(c["rhs"], idx.reshape(-1).numpy())
+    np.testing.assert_array_equal(c["lhs"], np.repeat(np.arange(T), top))
+    with pytest.raises(ValueError, match="differ in shape"):
+        mlxturbo_amd.gather_glu(x, *gate, *_qweights(N + 16, K, E=E), rhs_indices=idx)
+
+
+def test_glu_prefill_composes_two_gathers(fake):
+    # 1024+ output rows: two gather_qmm calls (the fused kernel is decode-only)
+    T, top, E, N, K = 128, 8, 8, 32, 256
+    gate, up = _qweights(N, K, E=E), _qweights(N, K, E=E)
+    x = torch.zeros(T, 1, 1, K, dtype=torch.bfloat16)
+    idx = torch.randint(0, E, (T, top), dtype=torch.int32)
+    out = mlxturbo_amd.gather_glu(x, *gate, *up, rhs_indices=idx)
+    assert out.shape == (T, top, 1, N) and out.dtype == torch.bfloat16
+    assert [k for k, _ in fake.calls] == ["gather", "gather"]

@@ -190,3 +190,34 @@ def test_switch_glu_router_combine(T):
     assert got.shape == (T, H)
     res = O.check_output(from_dev(got), want.cpu().numpy())
     assert res["ok"], res
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 6])
+def test_switch_glu_fused_gate_up(T):
+    """fuse_gate_up: one gate+up+SiLU kernel (float sums, one rounding), no
+    sort, then the down gather; with scores the combine epilogue."""
+    rng = np.random.default_rng(80 + T)
+    E, H, I, top = 8, 256, 128, 4
+    def bank(N, K):
+        parts = [quantized(rng, N, K) for _ in range(E)]
+        return [np.stack([p[i] for p in parts]) for i in range(3)]
+    g, u, d = bank(I, H), bank(I, H), bank(H, I)
+    mods = [QuantizedSwitchLinear(to_dev(t[0]), to_dev(t[1], "bfloat16"), to_dev(t[2], "bfloat16"))
+            for t in (g, u, d)]
+    glu = SwitchGLU(*mods, fuse_gate_up=True)
+    idx = zipf_routing(rng, T, top, E)
+    x = act(rng, (T, H))
+    n0 = mq.launch_count()
+    y = glu(to_dev(x, "bfloat16"), torch.from_numpy(idx).cuda())
+    assert mq.launch_count() - n0 == 2                      # gate+up, down
+    assert y.shape == (T, top, H)
+    lhs, rhs = np.repeat(np.arange(T), top), idx.reshape(-1)
+    h = O.from_f32(O.gather_glu_ref(x.reshape(T, 1, H), g, u, lhs, rhs), "bfloat16")
+    ref = O.gather_qmm_ref(h.reshape(T * top, 1, I), *d, np.arange(T * top), rhs)
+    res = O.check_output(from_dev(y).reshape(T * top, 1, H), ref)
+    assert res["ok"], res
+    scores = torch.from_numpy(rng.random((T, top)).astype(np.float32)).cuda()
+    got = glu(to_dev(x, "bfloat16"), torch.from_numpy(idx).cuda(), scores)
+    want = (y.float() * scores[..., None]).sum(-2)
+    assert O.check_output(from_dev(got), want.cpu().numpy())["ok"]

@@ -116,11 +116,14 @@ def test_qmm_vs_oracle_ragged(M, bits):
     _check(out, O.quantized_matmul_ref(x, w, s, b, gs, bits))
 
 
+@pytest.mark.parametrize("M", [6, 12])
 @pytest.mark.parametrize("gs", [32, 128])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-def test_qmm_group_sizes_and_dtypes(gs, dtype):
-    rng = np.random.default_rng(gs)
-    M, N, K = 6, 300, 2048
+def test_qmm_group_sizes_and_dtypes(M, gs, dtype):
+    # M=12: 16 streamed x rows with two tiles per workgroup (gs 32), global
+    # x fragments (4-bit gs 128, whose steps are 512 codes long)
+    rng = np.random.default_rng(gs + M)
+    N, K = 300, 2048
     for bits in (4, 8):
         w, s, b = quantized(rng, N, K, gs, bits, dtype)
         x = act(rng, (M, K), dtype)
@@ -219,6 +222,25 @@ def test_config2_skinny(cfg2_weights, shape, M):
     out = mq.quantized_matmul(to_dev(x, "bfloat16"), *dev)
     ref = (O.bf16_to_f32(x).astype(np.float64) @ deq.T).astype(np.float32)
     _check(out, ref)
+
+
+@pytest.mark.parametrize("M", [8, 13])
+def test_skinny_long_k_many_rows(M):
+    """K=17408 with N >= 10240 (four waves per tile): the two-tile scale copy
+    would not fit, so these widths run one tile per workgroup; checked on a
+    column sample and against the one-row results."""
+    rng = np.random.default_rng(300 + M)
+    N, K = 10256, 17408
+    w, s, b = random_packed(rng, N, K)
+    x = act(rng, (M, K), scale=0.1)
+    args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    xd = to_dev(x, "bfloat16")
+    out = mq.quantized_matmul(xd, *args)
+    cols = np.concatenate([np.arange(0, 48), np.arange(N - 40, N), rng.choice(N, 64, False)])
+    ref = O.quantized_matmul_ref(x, w[cols], s[cols], b[cols])
+    _check(out[:, torch.from_numpy(cols).cuda()], ref)
+    one = bits16(mq.quantized_matmul(xd[M - 1:], *args))
+    np.testing.assert_array_equal(bits16(out)[M - 1], one[0])
 
 
 # ------------------------------------------------- BASELINE config 3 (wide)
@@ -439,6 +461,84 @@ def test_gather_prefill_grouped_invalid_and_sorted():
                                  sorted_indices=True))
     np.testing.assert_array_equal(out_s.reshape(T * top, N), bits16(out).reshape(T * top, N)[order])
 
+
+
+@pytest.mark.parametrize("routing", ["zipf", "uniform"])
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_config4_gather_glu(moe_banks, T, routing):
+    """Fused gate+up+SiLU (moe_glu.fused_glu / moe_decode_fused.gate_up) on
+    config 4's gate/up bank split into its gate and up halves."""
+    w, s, b, dev = moe_banks["gate_up"]
+    E, N2, Kw = w.shape
+    N, K = N2 // 2, Kw * 8
+    gate = [t[:, :N] for t in (w, s, b)]
+    up = [t[:, N:] for t in (w, s, b)]
+    gate_d = [t[:, :N].contiguous() for t in dev]
+    up_d = [t[:, N:].contiguous() for t in dev]
+    rng = np.random.default_rng(60 + T)
+    idx = (zipf_routing if routing == "zipf" else uniform_routing)(rng, T, 8, E)
+    x = act(rng, (T, 1, 1, K))
+    out = mq.gather_glu(to_dev(x, "bfloat16"), *gate_d, *up_d,
+                        rhs_indices=torch.from_numpy(idx).cuda())
+    assert out.shape == (T, 8, 1, N)
+    lhs = np.repeat(np.arange(T), 8)
+    ref = O.gather_glu_ref(x.reshape(T, 1, K), gate, up, lhs, idx.reshape(-1))
+    _check(out.reshape(T * 8, 1, N), ref)
+
+
+@pytest.mark.parametrize("M,bits,gs,dtype,T", [(1, 4, 64, "bfloat16", 5), (3, 4, 32, "bfloat16", 7),
+                                              (2, 8, 64, "float16", 6), (1, 4, 128, "bfloat16", 200),
+                                              (5, 8, 32, "float16", 40)])
+def test_gather_glu_formats_and_paths(M, bits, gs, dtype, T):
+    """Ragged N, every format, M rows per pair, invalid experts (zero rows),
+    and P > 256 pairs (counting-sort prep tables)."""
+    rng = np.random.default_rng(70 + M + bits + T)
+    E, N, K, top = 12, 88, 512, 4
+    def bank():
+        parts = [quantized(rng, N, K, gs=gs, bits=bits, dtype=dtype) for _ in range(E)]
+        return [np.stack([p[i] for p in parts]) for i in range(3)]
+    gate, up = bank(), bank()
+    dev = lambda bk: (to_dev(bk[0]), to_dev(bk[1], dtype), to_dev(bk[2], dtype))  # noqa: E731
+    idx = zipf_routing(rng, T, top, E).astype(np.int32)
+    idx[0, 1] = -1
+    idx[T - 1, 0] = E
+    x = act(rng, (T, 1, M, K))
+    out = mq.gather_glu(to_dev(x, dtype), *dev(gate), *dev(up),
+                        rhs_indices=torch.from_numpy(idx).cuda(), group_size=gs, bits=bits)
+    assert out.shape == (T, top, M, N)
+    o = from_dev(out).reshape(T * top, M, N)
+    flat = idx.reshape(-1)
+    bad = (flat < 0) | (flat >= E)
+    assert np.all(o[bad] == 0)
+    ok = np.nonzero(~bad)[0]
+    ref = O.gather_glu_ref(x.reshape(T, M, K), gate, up, ok // top, flat[ok], gs, bits, dtype)
+    res = O.check_output(o[ok], ref, dtype)
+    assert res["ok"], res
+
+
+def test_gather_glu_prefill_composition():
+    """1024+ output rows: two grouped gather_qmm calls, then SiLU-multiply in
+    float of their rounded outputs."""
+    rng = np.random.default_rng(91)
+    E, N, K, T, top = 8, 96, 512, 300, 4
+    def bank():
+        parts = [quantized(rng, N, K) for _ in range(E)]
+        return [np.stack([p[i] for p in parts]) for i in range(3)]
+    gate, up = bank(), bank()
+    dev = lambda bk: (to_dev(bk[0]), to_dev(bk[1], "bfloat16"), to_dev(bk[2], "bfloat16"))  # noqa: E731
+    idx = zipf_routing(rng, T, top, E)
+    x = act(rng, (T, 1, 1, K))
+    out = mq.gather_glu(to_dev(x, "bfloat16"), *dev(gate), *dev(up),
+                        rhs_indices=torch.from_numpy(idx).cuda())
+    lhs, rhs = np.repeat(np.arange(T), top), idx.reshape(-1)
+    rb = lambda v: O.to_f32(O.from_f32(v, "bfloat16"), "bfloat16").astype(np.float64)  # noqa: E731
+    g = rb(O.gather_qmm_ref(x.reshape(T, 1, K), *gate, lhs, rhs))
+    u = rb(O.gather_qmm_ref(x.reshape(T, 1, K), *up, lhs, rhs))
+    ref = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+    # g and u each carry one bf16 rounding that the fused kernel avoids; the
+    # reference models them, the sums' order remains
+    res = O.check_output(from_dev(out).reshape(T * top, 1, N), ref)
+    assert res["rel_l2"] < 2e-3, res
 
 
 @pytest.mark.parametrize("rows,top_k,N,sorted_", [(1, 8, 2048, False), (7, 8, 2048, True),

@@ -267,6 +267,63 @@ def test_gather_equals_dense_per_pair():
     np.testing.assert_array_equal(ref_sorted, ref[order])
 
 
+# --------------------------------------------------------------- gather glu
+
+def _const_bank(E, N, row_vals, bits=4, gs=64, K=64):
+    """Bank whose dequantized row n of expert e is the constant row_vals[e][n]
+    (codes 0, scale 1, bias = the value), exact in bf16 for the values used."""
+    w = np.zeros((E, N, K * bits // 32), dtype=np.uint32)
+    s = np.full((E, N, K // gs), O.bf16_bits(np.float32(1.0)), dtype=np.uint16)
+    b = O.bf16_bits(np.asarray(row_vals, dtype=np.float32).reshape(E, N, 1)
+                    .repeat(K // gs, axis=2))
+    return w, s, b
+
+
+def test_gather_glu_closed_forms():
+    K = 64
+    x = np.full((2, 1, K), O.bf16_bits(np.float32(1.0)), dtype=np.uint16)   # sum(x) = 64
+    # gate / up rows give g = 64 * value: g in {0, 1, 2, 20, -20}
+    gv = np.array([[0, 1, 2, 20, -20], [1, 2, 0, 1, 1]], dtype=np.float64) / 64
+    uv = np.array([[5, 2, 1, 1, 1], [2, 1, 7, -3, 0]], dtype=np.float64) / 64
+    gate, up = _const_bank(2, 5, gv), _const_bank(2, 5, uv)
+    lhs, rhs = np.array([0, 1, 1]), np.array([0, 1, 0])
+    out = O.gather_glu_ref(x, gate, up, lhs, rhs)
+    e0 = [0.0, 2 * 0.7310585786300049, 2 * 0.8807970779778823,
+          20 * 0.9999999979388463, -20 * 2.0611536181902037e-09]
+    e1 = [2 * 0.7310585786300049, 2 * 0.8807970779778823, 0.0,
+          -3 * 0.7310585786300049, 0.0]
+    np.testing.assert_allclose(out[0, 0], e0, rtol=1e-7, atol=1e-12)
+    np.testing.assert_allclose(out[1, 0], e1, rtol=1e-7, atol=1e-12)
+    np.testing.assert_allclose(out[2, 0], e0, rtol=1e-7, atol=1e-12)
+    # swapping the banks applies SiLU to the other product: pair 0, row 1
+    # becomes g = 2, u = 1 -> 2 * sigmoid(2) instead of 2 * sigmoid(1)
+    swapped = O.gather_glu_ref(x, up, gate, lhs, rhs)
+    np.testing.assert_allclose(swapped[0, 0, 1], 2 * 0.8807970779778823, rtol=1e-7)
+    assert not np.allclose(swapped, out)
+
+
+def test_gather_glu_zero_gate_and_up_linearity():
+    rng = np.random.default_rng(21)
+    E, N, K = 3, 32, 128
+    def bank():
+        parts = [O.quantize((rng.standard_normal((N, K)) * 0.05).astype(np.float32), 64, 4)
+                 for _ in range(E)]
+        return [np.stack([p[i] for p in parts]) for i in range(3)]
+    gate, up = bank(), bank()
+    x = O.from_f32(rng.standard_normal((4, 2, K)).astype(np.float32), "bfloat16")
+    lhs, rhs = np.array([0, 1, 2, 3, 0]), np.array([2, 0, 1, 2, 1])
+    out = O.gather_glu_ref(x, gate, up, lhs, rhs)
+    # a zero gate bank (scale 0, bias 0) zeroes every output
+    zero = [gate[0], np.zeros_like(gate[1]), np.zeros_like(gate[2])]
+    np.testing.assert_array_equal(O.gather_glu_ref(x, zero, up, lhs, rhs), 0.0)
+    # doubling the up bank's scales and biases doubles the output exactly
+    up2 = [up[0], O.bf16_bits(O.bf16_to_f32(up[1]) * 2), O.bf16_bits(O.bf16_to_f32(up[2]) * 2)]
+    np.testing.assert_array_equal(O.gather_glu_ref(x, gate, up2, lhs, rhs), 2 * out)
+    # and the gate product alone is gather_qmm's
+    g = O.gather_qmm_ref(x, *gate, lhs, rhs)
+    assert np.all(np.sign(out) == np.sign(g * O.gather_qmm_ref(x, *up, lhs, rhs)))
+
+
 # ----------------------------------------------------------------- quantize
 
 def test_quantize_invariants():
