@@ -24,6 +24,7 @@
 // Pairs with an out-of-range expert or x index produce zero rows.
 #pragma once
 #include "launch.h"
+#include "grouped.cuh"
 #include "qmm_wide.cuh"
 #include "qmv.cuh"
 
@@ -353,6 +354,28 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
   return 0;
 }
 
+// Prefill gather_qmm with thin experts: prep tables with segments of 64 / M
+// pairs, then the register-B grouped kernel (grouped.cuh).
+template <int DT, int BITS, int GS>
+inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, const void* b,
+                               const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
+                               int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
+                               hipStream_t st, int* nlaunch) {
+  const int R = (int)(kThinBM / M);
+  const size_t shmem = 4 * sizeof(int) * (size_t)(E + 1);
+  hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, lhs, (int)P, (int)E,
+                     (int)B, R, (int32_t*)ws);
+  const int64_t bound = (P + R - 1) / R + E + 1;
+  const int64_t segs = bound < P ? bound : P;
+  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)segs);
+  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2>), grid, dim3(kThinNT), 0, st,
+                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,
+                     (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K,
+                     (int)E);
+  *nlaunch += 2;
+  return 0;
+}
+
 template <int DT, int BITS, int GS>
 inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const void* b,
                           const int32_t* lhs, const int32_t* rhs, void* out, int64_t P, int64_t B,
@@ -366,6 +389,12 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
   if (rows_per_expert >= 96)
     return launch_grouped_bm<DT, BITS, GS, 128>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
                                                 st, nlaunch);
+  // thin experts: the register-B kernel wins on short K (config-4 down bank,
+  // K=512: 201-209 against 265-270 us); at K=2048 the LDS-shared wide tile
+  // stays ahead with uniform routing (341-352 against 427 us)
+  if (K <= 1024)
+    return launch_grouped_thin<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
+                                             nlaunch);
   return launch_grouped_bm<DT, BITS, GS, 64>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
                                              nlaunch);
 }

@@ -1,0 +1,221 @@
+// Prefill gather_qmm for thin experts: expert-grouped rows with the weights
+// dequantized straight into MFMA B registers.
+//
+// Reference behaviour: moe_grouped_gemm.qmm_segmented (moe_grouped_gemm.py:
+// 913-1066): pairs sorted by expert, each tile belongs to one expert; the
+// reference notes that thin segments waste tile rows (moe_grouped_gemm.py:
+// 61-67).  At prefill MoE widths most experts get tens of rows (config 4:
+// 16384 pairs over 512 experts, 32 on average), so a tile is mostly weights:
+// the shared-LDS wide tile (qmm_wide.cuh) writes 32 KB of dequantized
+// weights to LDS per k-step and reads them back from every wave row for only
+// 64 x rows, needs 92 KB of LDS (one workgroup per CU) and measured 1.4 TB/s.
+//
+// CDNA4 design: a workgroup of 4 waves owns (segment of <= 64 rows, 256
+// weight columns); wave w owns columns 64 w .. 64 w + 63 as two 32-column
+// blocks.  Per 64-code k-step, lane l (h = l >> 5) loads 32 codes of column
+// (l & 31) of each block, k = 32 h .. 32 h + 31 of the step (one 16-byte load
+// per block for 4-bit), dequantizes them exactly (mq_common.h) into the B
+// operands of four v_mfma_f32_32x32x16 (MFMA ks takes codes 8 ks .. 8 ks + 7
+// of the lane's 32; A rows use the same k order), so weights never touch
+// LDS.  Only the x tile (64 rows x 64 codes, 9 KB) is staged in LDS, double
+// buffered; 18 KB of LDS per workgroup leaves room for several workgroups
+// per CU.  Global loads run PS k-steps ahead in registers (two measured
+// best: deeper prefetch lowered occupancy and lost 10-15% on the down bank).
+// 32-row blocks past the segment's rows skip their MFMAs.  Measured on the
+// config-4 banks at 2048 tokens x top-8 (prep included): down (K=512) 201-212
+// us against 265-270 for the wide tile; gate/up (K=2048) 427-475 against
+// 341-462 (its loads alone take ~200 us and the dequant + MFMA work does not
+// overlap them), so only short K is routed here.
+#pragma once
+#include "qmm_wide.cuh"
+
+namespace mq {
+
+constexpr int kThinBM = 64, kThinNT = 256;
+
+// grid (ceil(N / 256), segment bound), 256 threads; segments of the prep
+// tables in ws hold up to 64 / Mi pairs of one expert; pair p contributes
+// rows p*Mi .. p*Mi+Mi-1 and reads x batch lhs[p] (or p).  Segments of
+// out-of-range experts write zeros.  K % 64 == 0, B * Mi * K * 2 < 2^31.
+template <int DT, int BITS, int GS, int PS>
+__global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
+    int P, int B, int Mi, int N, int K, int E) {
+  constexpr int BM = kThinBM, BN = kWideBN, BK = kWideBK, LD = kWideLD, NT = kThinNT;
+  constexpr int WB = BITS / 4;                  // 16-byte loads per lane per block per step
+  static_assert(GS >= 32, "a lane's 32 codes lie in one group");
+  using T = T16<DT>;
+  __shared__ __align__(16) uint16_t As[2][BM * LD];
+  __shared__ uint32_t s_xoff[BM];
+  __shared__ int s_orow[BM];
+  const int seg = blockIdx.y, n0 = blockIdx.x * BN;
+  if (seg >= ws[0]) return;
+  const int32_t* perm = ws + 1;
+  const int st0 = perm[P + seg], len = perm[2 * P + seg];
+  const int e = __builtin_amdgcn_readfirstlane(perm[3 * P + seg]);
+  const int rows = len * Mi;                    // <= BM
+  const int t = threadIdx.x;
+  if (t < BM) {
+    if (t < rows) {
+      const int p = perm[st0 + t / Mi], mi = t % Mi;
+      const int xb = lhs ? lhs[p] : p;
+      s_xoff[t] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
+      s_orow[t] = p * Mi + mi;
+    } else {
+      s_xoff[t] = 0xffffffffu;
+      s_orow[t] = -1;
+    }
+  }
+  __syncthreads();
+  const int ncols = min(BN, N - n0);
+  if (e >= E) {
+    for (int i = t; i < rows * ncols; i += NT) {
+      const int r = i / ncols, c = i - r * ncols;
+      out[(int64_t)s_orow[r] * N + n0 + c] = 0;
+    }
+    return;
+  }
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int h = lane >> 5, lr = lane & 31;
+  const int G = K / GS, nk = K / BK;
+  const int64_t Kw = (int64_t)K * BITS / 32;    // words per weight row
+  const int64_t wrow = (int64_t)e * N + n0;
+  // columns past ncols are past these ranges and read zeros (never stored)
+  const auto rw = wide_rsrc(w + wrow * Kw, (int64_t)ncols * Kw * 4);
+  const auto rs = wide_rsrc(scales + wrow * G, (int64_t)ncols * G * 2);
+  const auto rb = wide_rsrc(biases + wrow * G, (int64_t)ncols * G * 2);
+  const auto xr = wide_rsrc(x, (int64_t)B * Mi * K * 2);
+  uint32_t wo[2], so[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = 64 * wave + 32 * j + lr;
+    wo[j] = (uint32_t)(c * Kw * 4) + (uint32_t)h * 16u * WB;
+    so[j] = (uint32_t)c * (uint32_t)G * 2u;
+  }
+  // x: thread t stages rows (t >> 3) + 32 i, codes 8 (t & 7) .. +8 of the step
+  uint32_t xo[2];
+  int xl[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (t >> 3) + 32 * i;
+    const uint32_t ro = s_xoff[r];
+    xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
+    xl[i] = r * LD + 8 * (t & 7);
+  }
+  struct Stage {
+    u32x4 xa[2];
+    u32x4 wv[2][WB];
+    uint16_t s[2], b[2];
+  };
+  auto gload = [&](Stage& st, int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], k0 * 2, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int q = 0; q < WB; ++q)
+        st.wv[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[j] + 16u * q, k0 * BITS / 8, 0);
+      const uint32_t go = so[j] + 2u * (uint32_t)((k0 + 32 * h) / GS);
+      st.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
+      st.b[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+    }
+  };
+  auto store_x = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&As[buf][xl[i]]) = st.xa[i];
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+  const int live = rows > 32 ? 2 : 1;           // 32-row blocks holding rows
+
+  // One k-step: dequantize codes 8 ks .. 8 ks + 7 of the lane's 32 (B of MFMA
+  // ks, per 32-column block) and multiply with the x rows in LDS buffer buf.
+  auto step = [&](const Stage& st, int buf) {
+    GroupScale g[2];
+    bool big = false;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      g[j] = make_group(T::to_f32(st.s[j]), T::to_f32(st.b[j]));
+      big |= needs_plain(g[j].s);
+    }
+    const bool plain = __builtin_amdgcn_ballot_w64(big) != 0;
+    const uint16_t* A = &As[buf][lr * LD + 32 * h];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 bq[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        uint32_t o[4];
+        if constexpr (BITS == 4) {
+          if (plain) deq_word_plain<DT, 4>(st.wv[j][0][ks], g[j], o);
+          else deq4_word<DT>(st.wv[j][0][ks], g[j], o);
+        } else {
+          const u32x4 v = st.wv[j][ks / 2];
+          if (plain) {
+            deq_word_plain<DT, 8>(v[2 * (ks % 2)], g[j], o);
+            deq_word_plain<DT, 8>(v[2 * (ks % 2) + 1], g[j], o + 2);
+          } else {
+            deq8_word<DT>(v[2 * (ks % 2)], g[j], o);
+            deq8_word<DT>(v[2 * (ks % 2) + 1], g[j], o + 2);
+          }
+        }
+        bq[j] = (u32x4){o[0], o[1], o[2], o[3]};
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (i == 0 || i < live) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(A + 32 * i * LD + 8 * ks);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<DT>(a, bq[j], acc[i][j]);
+        }
+    }
+  };
+
+  Stage S[PS];
+#pragma unroll
+  for (int i = 0; i < PS; ++i) gload(S[i], min(i, nk - 1));
+  store_x(S[0], 0);
+  __syncthreads();
+  // At step k: LDS buffer k & 1 holds x of step k; S[k % PS] holds step k's
+  // weights and is reloaded with step k + PS once they are multiplied;
+  // S[(k + i) % PS] holds step k + i.  The body is unrolled over lcm(PS, 2)
+  // steps so stage and buffer indices are constants; the last steps reload
+  // step nk - 1 (valid memory, unused), so the loads need no conditions.
+  constexpr int U = PS % 2 ? 2 * PS : PS;
+  for (int kt = 0; kt < nk; kt += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u > 0 && kt + u >= nk) break;         // uniform
+      step(S[u % PS], u & 1);
+      gload(S[u % PS], min(kt + u + PS, nk - 1));
+      store_x(S[(u + 1) % PS], (u + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // D[row][col] of a 32x32 tile: col = lane & 31, row = 8*(e/4) + 4*(lane>>5) + e%4
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = 64 * wave + 32 * j + lr;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int r = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
+        if (r < rows && c < ncols) out[(int64_t)s_orow[r] * N + n0 + c] = T::round1(acc[i][j][q]);
+      }
+    }
+}
+
+}  // namespace mq

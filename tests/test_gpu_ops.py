@@ -433,6 +433,36 @@ def test_gather_prefill_grouped(M, bits, gs):
     _check(out.reshape(T * top, M, N), ref)
 
 
+@pytest.mark.parametrize("M,bits,gs,dtype", [(1, 4, 64, "bfloat16"), (2, 4, 32, "float16"),
+                                              (3, 8, 64, "bfloat16"), (1, 8, 128, "float16"),
+                                              (5, 4, 128, "bfloat16")])
+def test_gather_prefill_thin_experts(M, bits, gs, dtype):
+    """Prefill widths with few rows per expert (< 96): the register-B grouped
+    kernel.  Zipf routing gives experts from 1 row to several 64-row
+    segments; ragged N; two invalid pairs write zero rows."""
+    rng = np.random.default_rng(40 + M + bits + gs)
+    E, N, K, T, top = 64, 200, 768, 256, 4
+    banks = [quantized(rng, N, K, gs=gs, bits=bits, dtype=dtype) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    idx = zipf_routing(rng, T, top, E).astype(np.int32)
+    idx[3, 2] = -1
+    idx[T - 1, 0] = E + 5
+    x = act(rng, (T, 1, M, K), dtype)
+    n0 = mq.launch_count()
+    out = mq.gather_qmm(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
+                        rhs_indices=torch.from_numpy(idx).cuda(), group_size=gs, bits=bits)
+    assert mq.launch_count() - n0 == 2                 # prep + grouped kernel
+    o = from_dev(out).reshape(T * top, M, N)
+    flat = idx.reshape(-1)
+    bad = (flat < 0) | (flat >= E)
+    assert np.all(o[bad] == 0)
+    ok = np.nonzero(~bad)[0]
+    ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, ok // top, flat[ok], gs, bits, dtype)
+    res = O.check_output(o[ok], ref, dtype)
+    assert res["ok"], res
+
+
 def test_gather_prefill_grouped_invalid_and_sorted():
     """Grouped path: out-of-range experts give zero rows; sorted input (mlx-lm
     _gather_sort) gives bit-identical per-pair rows."""
