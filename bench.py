@@ -57,7 +57,8 @@ def parse():
     p.add_argument("--case", default="",
                    help="run one sweep case only and print its result (for profiling): "
                         "wide<M> (configs[2]), gather_<proj>_<routing>_T<T> (configs[3] decode), "
-                        "gather_glu_<routing>_T<T> (fused gate+up+SiLU), "
+                        "gather_glu_<routing>_T<T> (fused gate+up+SiLU), qmv<M> / qmvdown<M> "
+                        "(configs[1] skinny), combine (MoE combine, 2048 x top-8 x 2048), "
                         "gather_prefill_<proj>_<routing> (2048 tokens)")
     return p.parse_args()
 
@@ -66,6 +67,15 @@ def run_case(torch, mq, case: str) -> dict:
     """One sweep entry by name, so a profiler sees only its kernels."""
     K, N = 5120, 17408
     banks = {"gate_up": (1024, 2048), "down": (2048, 512)}
+    if case.startswith("qmv"):
+        # qmv<M> (K=5120 N=17408) or qmvdown<M> (K=17408 N=5120), 4-bit g64
+        down = case.startswith("qmvdown")
+        M = int(case[7:] if down else case[3:])
+        KK, NN = (N, K) if down else (K, N)
+        r = measure_qmm(torch, mq, M, NN, KK, 4, 200, 20)
+        return {"case": case, "us": round(r["us"], 2), "GBps": round(r["GBps"], 1)}
+    if case == "combine":
+        return {"case": case, **measure_combine(torch, mq, 2048, 8, 2048, 50, 3)}
     if case.startswith("wide"):
         M = int(case[4:])
         r = measure_qmm(torch, mq, M, N, K, 4, 20, 3, copies=2)
