@@ -30,74 +30,159 @@
 
 namespace mq {
 
-// Counting sort of the pairs by key (expert, or E for invalid pairs) into
-// segments of up to R pairs; one workgroup.  Internal linkage: every
-// translation unit that launches it has its own copy.
+// Pairs whose keys the prep kernel stages in LDS (larger P reads them from
+// memory on each pass).
+constexpr int kPrepLdsKeys = 24576;
+
+// Dynamic LDS of the prep kernel: counting-sort tables (4 (E + 1) ints) and
+// the staged keys.
+inline size_t gather_prep_lds(int64_t P, int64_t E) {
+  return sizeof(int) * (size_t)(4 * (E + 1) + (P <= kPrepLdsKeys ? P : 0));
+}
+
+// Segment tables for the pairs: sorted by key (expert, or E for invalid
+// pairs) into segments of up to R pairs of one key; one workgroup of 1024
+// threads.  Keys are staged in LDS with coalesced loads, 16 per thread in
+// flight.  Every pass walks the pairs with consecutive threads on consecutive
+// pairs (no per-thread chains: a sequential walk over contiguous chunks of 16
+// took ~2.5 us per pass).  Pairs already in
+// key order (mlx-lm's _gather_sort, the reference's prefill path) keep their
+// order (perm = identity): each key's run is read off its boundaries, with
+// no atomics; other orders are counting-sorted.  Internal linkage: every translation
+// unit that launches it has its own copy.
 static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __restrict__ rhs,
                                                            const int32_t* __restrict__ lhs, int P,
                                                            int E, int B, int R,
                                                            int32_t* __restrict__ ws) {
   extern __shared__ int sh[];
   const int NE = E + 1;  // bucket E collects out-of-range experts
+  __shared__ int wtot[16];
+  const int t = threadIdx.x;
+  const int nt = blockDim.x;
+  const int lane = t & 63, wv = t >> 6, nw = nt >> 6;
   int* cnt = sh;
   int* base = sh + NE;
   int* segb = sh + 2 * NE;
   int* cur = sh + 3 * NE;
-  __shared__ int part[1024][2];
-  const int t = threadIdx.x;
-  const int nt = blockDim.x;
-  for (int e = t; e < NE; e += nt) {
-    cnt[e] = 0;
-    cur[e] = 0;
-  }
-  __syncthreads();
+  int* skey = sh + 4 * NE;
+  const bool staged = P <= kPrepLdsKeys;
   auto key_of = [&](int p) {
     const int e = rhs[p];
     const int xb = lhs ? lhs[p] : p;
     return (e >= 0 && e < E && xb >= 0 && xb < B) ? e : E;
   };
-  for (int p = t; p < P; p += nt) atomicAdd(&cnt[key_of(p)], 1);
+  if (staged) {
+    for (int p0 = t; p0 < P; p0 += 16 * nt) {
+      int k[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) k[i] = p0 + i * nt < P ? key_of(p0 + i * nt) : 0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int q = p0 + i * nt;
+        if (q < P) skey[q] = k[i];
+      }
+    }
+    __syncthreads();
+  }
+  auto key_at = [&](int p) { return staged ? skey[p] : key_of(p); };
+  int32_t* perm = ws + 1;
+  int32_t* seg_start = perm + P;
+  int32_t* seg_len = seg_start + P;
+  int32_t* seg_exp = seg_len + P;
+  // exclusive workgroup scan (sum, or max with identity -1) of one int per
+  // thread: wave scans with cross-lane reads, then one wave over the totals
+  auto wg_scan = [&](int v, bool is_max) {
+    const int id = is_max ? -1 : 0;
+    auto op = [&](int a, int b) { return is_max ? max(a, b) : a + b; };
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d, 64);
+      if (lane >= d) x = op(x, y);
+    }
+    const int below = __shfl_up(x, 1, 64);
+    if (lane == 63) wtot[wv] = x;
+    __syncthreads();
+    if (wv == 0) {
+      int z = lane < nw ? wtot[lane] : id;
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) {
+        const int y = __shfl_up(z, d, 64);
+        if (lane >= d) z = op(z, y);
+      }
+      if (lane < nw) wtot[lane] = z;
+    }
+    __syncthreads();
+    const int off = wv ? wtot[wv - 1] : id;
+    const int excl = op(off, lane ? below : id);
+    __syncthreads();                          // wtot is reused by the next scan
+    return excl;
+  };
+
+  // ---- keys already in order: runs from their boundaries, no atomics --------
+  bool ordered = true;
+  for (int p = t + 1; p < P; p += nt) ordered &= key_at(p) >= key_at(p - 1);
+  if (__syncthreads_and(ordered)) {
+    // base[e] / cur[e]: first / last pair of key e's run (base -1: absent)
+    for (int e = t; e < NE; e += nt) base[e] = -1;
+    __syncthreads();
+    for (int p = t; p < P; p += nt) {
+      const int k = key_at(p);
+      if (p == 0 || key_at(p - 1) != k) base[k] = p;
+      if (p == P - 1 || key_at(p + 1) != k) cur[k] = p;
+      perm[p] = p;
+    }
+    __syncthreads();
+    const int per = (NE + nt - 1) / nt;
+    const int e0 = min(NE, t * per), e1 = min(NE, e0 + per);
+    int ss = 0;
+    for (int e = e0; e < e1; ++e) {
+      const int c = base[e] >= 0 ? cur[e] - base[e] + 1 : 0;
+      ss += (c + R - 1) / R;
+    }
+    int sid = wg_scan(ss, false);
+    for (int e = e0; e < e1; ++e) {
+      const int c = base[e] >= 0 ? cur[e] - base[e] + 1 : 0;
+      for (int j = 0; j * R < c; ++j, ++sid) {
+        seg_start[sid] = base[e] + j * R;
+        seg_len[sid] = min(R, c - j * R);
+        seg_exp[sid] = e;
+      }
+    }
+    if (t == nt - 1) ws[0] = sid;
+    return;
+  }
+
+  // ---- any order: counting sort by key ------------------------------------
+  for (int e = t; e < NE; e += nt) {
+    cnt[e] = 0;
+    cur[e] = 0;
+  }
   __syncthreads();
-  // exclusive scans of cnt and ceil(cnt/R): chunk per thread, then Hillis-Steele.
+  for (int p = t; p < P; p += nt) atomicAdd(&cnt[key_at(p)], 1);
+  __syncthreads();
+  // exclusive scans of cnt and ceil(cnt/R) over contiguous key chunks
   const int per = (NE + nt - 1) / nt;
-  const int e0 = t * per;
+  const int e0 = min(NE, t * per);
   const int e1 = min(NE, e0 + per);
   int sc = 0, ss = 0;
   for (int e = e0; e < e1; ++e) {
     sc += cnt[e];
     ss += (cnt[e] + R - 1) / R;
   }
-  part[t][0] = sc;
-  part[t][1] = ss;
-  __syncthreads();
-  for (int off = 1; off < nt; off <<= 1) {
-    int a = 0, b = 0;
-    if (t >= off) {
-      a = part[t - off][0];
-      b = part[t - off][1];
-    }
-    __syncthreads();
-    part[t][0] += a;
-    part[t][1] += b;
-    __syncthreads();
-  }
-  int rc = part[t][0] - sc;
-  int rs = part[t][1] - ss;
+  int rc = wg_scan(sc, false);
+  int rs = wg_scan(ss, false);
   for (int e = e0; e < e1; ++e) {
     base[e] = rc;
     segb[e] = rs;
     rc += cnt[e];
     rs += (cnt[e] + R - 1) / R;
   }
-  if (t == nt - 1) ws[0] = part[t][1];
+  if (t == nt - 1) ws[0] = rs;
   __syncthreads();
-  int32_t* perm = ws + 1;
-  int32_t* seg_start = perm + P;
-  int32_t* seg_len = seg_start + P;
-  int32_t* seg_exp = seg_len + P;
   for (int p = t; p < P; p += nt) {
-    const int e = key_of(p);
-    perm[base[e] + atomicAdd(&cur[e], 1)] = p;
+    const int k = key_at(p);
+    perm[base[k] + atomicAdd(&cur[k], 1)] = p;
   }
   for (int e = t; e < NE; e += nt) {
     const int c = cnt[e];
@@ -108,6 +193,18 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
       seg_exp[s] = e;
     }
   }
+}
+
+// One prep launch; its LDS can pass 64 KiB, so the limit is raised once.
+inline int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, int64_t B,
+                       int R, void* ws, hipStream_t st) {
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&gather_prep_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+      (int)gather_prep_lds(kPrepLdsKeys, kGatherPrepMaxE));
+  if (attr != hipSuccess) return (int)attr;
+  hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), gather_prep_lds(P, E), st, rhs, lhs,
+                     (int)P, (int)E, (int)B, R, (int32_t*)ws);
+  return 0;
 }
 
 // A rows of a gather segment: pair members[j] contributes rows j*Mi .. j*Mi+Mi-1.
@@ -340,9 +437,7 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds_bytes<BM>());
   if (attr != hipSuccess) return (int)attr;
   const int R = (int)(BM / M);
-  const size_t shmem = 4 * sizeof(int) * (size_t)(E + 1);
-  hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, lhs, (int)P, (int)E,
-                     (int)B, R, (int32_t*)ws);
+  if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
   const int64_t bound = (P + R - 1) / R + E + 1;
   const int64_t segs = bound < P ? bound : P;
   const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)segs);
@@ -362,9 +457,7 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
                                int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
                                hipStream_t st, int* nlaunch) {
   const int R = (int)(kThinBM / M);
-  const size_t shmem = 4 * sizeof(int) * (size_t)(E + 1);
-  hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, lhs, (int)P, (int)E,
-                     (int)B, R, (int32_t*)ws);
+  if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
   const int64_t bound = (P + R - 1) / R + E + 1;
   const int64_t segs = bound < P ? bound : P;
   const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)segs);
@@ -435,9 +528,7 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
   if (P > kGatherFusedMaxP) {
     const int64_t bound = (P + R - 1) / R + E + 1;
     if (bound < max_seg) max_seg = bound;
-    const size_t shmem = 4 * sizeof(int) * (size_t)(E + 1);
-    hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), shmem, st, rhs, lhs, (int)P,
-                       (int)E, (int)B, R, (int32_t*)ws);
+    if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
     wsp = (const int32_t*)ws;
     *nlaunch += 1;
   }

@@ -463,6 +463,36 @@ def test_gather_prefill_thin_experts(M, bits, gs, dtype):
     assert res["ok"], res
 
 
+@pytest.mark.parametrize("T,top,M,K", [(150, 4, 1, 512), (300, 4, 1, 1024), (300, 4, 1, 2048),
+                                        (200, 4, 2, 512)])
+def test_gather_sorted_prep_matches_counting_sort(T, top, M, K):
+    """Pairs already in expert order (mlx-lm's _gather_sort) take the prep
+    kernel's scan path (identity order); the same pairs shuffled take the
+    counting sort.  Per-pair rows must be bit-identical, and match the
+    oracle.  Covers the streaming kernel with prep tables (P*M < 1024), the
+    thin and the wide grouped kernels, runs longer than a segment."""
+    rng = np.random.default_rng(T + top + M + K)
+    E, N = 24, 160
+    banks = [quantized(rng, N, K) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    dev = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    flat = np.sort(zipf_routing(rng, T, top, E).reshape(-1)).astype(np.int32)
+    P = flat.size
+    x = act(rng, (P, M, K))
+    xd = to_dev(x, "bfloat16")
+    out_sorted = bits16(mq.gather_qmm(xd, *dev, rhs_indices=torch.from_numpy(flat).cuda(),
+                                      sorted_indices=True))
+    shuf = rng.permutation(P)
+    out_shuf = bits16(mq.gather_qmm(xd[torch.from_numpy(shuf).cuda()], *dev,
+                                    rhs_indices=torch.from_numpy(flat[shuf]).cuda()))
+    np.testing.assert_array_equal(out_shuf, out_sorted[shuf])
+    rows = rng.choice(P, 64, replace=False)
+    ref = O.gather_qmm_ref(x, w, s, b, rows, flat[rows])
+    res = O.check_output(O.to_f32(out_sorted[rows].view(np.uint16), "bfloat16"), ref)
+    assert res["ok"], res
+
+
 def test_gather_prefill_grouped_invalid_and_sorted():
     """Grouped path: out-of-range experts give zero rows; sorted input (mlx-lm
     _gather_sort) gives bit-identical per-pair rows."""
