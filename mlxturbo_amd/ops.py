@@ -167,11 +167,18 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def _stream_of(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
 _WS_CACHE: dict = {}
 
 
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    key = (dev.type, dev.index)
+    """The gather workspace of the current stream (kernels on one stream run
+    in order, so consecutive calls can share it; calls on other streams get
+    their own, as concurrent calls must not share one)."""
+    key = (dev.type, dev.index, _stream_of(dev))
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
@@ -185,10 +192,11 @@ _LHS_CACHE: dict = {}
 def _default_lhs(dev: torch.device, bx: tuple, shape: tuple) -> Optional[torch.Tensor]:
     """x's own batch index per pair (lhs_indices=None), flattened over the
     broadcast shape; None when that is the identity (the C ABI's NULL lhs).
-    Cached per shape: building it costs two small kernels per call."""
+    Cached per shape and stream (the table is written by kernels on the
+    stream that built it): building it costs two small kernels per call."""
     if tuple(bx) == tuple(shape):
         return None
-    key = (dev.type, dev.index, tuple(bx), tuple(shape))
+    key = (dev.type, dev.index, _stream_of(dev), tuple(bx), tuple(shape))
     t = _LHS_CACHE.get(key)
     if t is None:
         B = math.prod(bx)

@@ -183,6 +183,7 @@ def fake(monkeypatch):
     monkeypatch.setattr(_lib, "lib", lambda: f)
     monkeypatch.setattr(ops, "_require_gpu", lambda *ts: torch.device("cpu"))
     monkeypatch.setattr(ops, "_stream_ptr", lambda t: 0)
+    monkeypatch.setattr(ops, "_stream_of", lambda dev: 0)
     return f
 
 

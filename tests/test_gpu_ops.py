@@ -619,3 +619,35 @@ def test_moe_combine(rows, top_k, N, sorted_, dtype):
     assert res["ok"], res
     # the same fma order as the restatement: at most a last-bit difference
     assert res["max_ulp"] <= 1.0, res
+
+
+def test_gather_two_streams_own_workspaces():
+    """Calls on different streams do not share the prep workspace: both
+    streams run the prep path at once and match their single-stream
+    results bit for bit."""
+    from mlxturbo_amd import ops
+    rng = np.random.default_rng(99)
+    E, N, K, T, top = 16, 64, 256, 100, 4
+    banks = [quantized(rng, N, K) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    dev = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    cases = []
+    for _ in range(2):
+        idx = torch.from_numpy(zipf_routing(rng, T, top, E)).cuda()
+        x = to_dev(act(rng, (T, 1, 1, K)), "bfloat16")
+        cases.append((x, idx, bits16(mq.gather_qmm(x, *dev, rhs_indices=idx))))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    outs = []
+    for st, (x, idx, _) in zip(streams, cases):
+        with torch.cuda.stream(st):
+            outs.append(mq.gather_qmm(x, *dev, rhs_indices=idx))
+    torch.cuda.synchronize()
+    for o, (_, _, want) in zip(outs, cases):
+        np.testing.assert_array_equal(bits16(o), want)
+    with torch.cuda.stream(streams[0]):
+        w0 = ops._workspace(torch.device("cuda"), 1024)
+    with torch.cuda.stream(streams[1]):
+        w1 = ops._workspace(torch.device("cuda"), 1024)
+    assert w0.data_ptr() != w1.data_ptr()
