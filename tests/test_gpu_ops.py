@@ -393,6 +393,26 @@ def test_gather_adversarial_and_invalid():
     assert O.check_output(out2[ok], ref)["ok"]
 
 
+@pytest.mark.parametrize("M,bits,gs", [(9, 4, 64), (12, 4, 32), (16, 8, 64), (16, 4, 128)])
+def test_gather_many_rows_per_pair(M, bits, gs):
+    """9..16 rows per pair: one pair per segment, A fragments read from
+    global memory (more rows than the streamed-x capacity of a segment)."""
+    rng = np.random.default_rng(50 + M + bits + gs)
+    E, N, K, T, top = 8, 72, 512, 5, 3
+    banks = [quantized(rng, N, K, gs=gs, bits=bits) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    idx = zipf_routing(rng, T, top, E)
+    x = act(rng, (T, 1, M, K))
+    out = mq.gather_qmm(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                        to_dev(b, "bfloat16"), rhs_indices=torch.from_numpy(idx).cuda(),
+                        group_size=gs, bits=bits)
+    assert out.shape == (T, top, M, N)
+    ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, np.repeat(np.arange(T), top),
+                           idx.reshape(-1), gs, bits)
+    _check(out.reshape(T * top, M, N), ref)
+
+
 @pytest.mark.parametrize("M", [1, 3])
 def test_gather_large_batch_prep_path(M):
     """P > 256 pairs: segment tables built by the counting-sort prep kernel."""
@@ -548,7 +568,8 @@ def test_config4_gather_glu(moe_banks, T, routing):
 
 @pytest.mark.parametrize("M,bits,gs,dtype,T", [(1, 4, 64, "bfloat16", 5), (3, 4, 32, "bfloat16", 7),
                                               (2, 8, 64, "float16", 6), (1, 4, 128, "bfloat16", 200),
-                                              (5, 8, 32, "float16", 40)])
+                                              (5, 8, 32, "float16", 40), (12, 4, 64, "bfloat16", 9),
+                                              (16, 8, 128, "float16", 3)])
 def test_gather_glu_formats_and_paths(M, bits, gs, dtype, T):
     """Ragged N, every format, M rows per pair, invalid experts (zero rows),
     and P > 256 pairs (counting-sort prep tables)."""
