@@ -672,3 +672,48 @@ def test_gather_two_streams_own_workspaces():
     with torch.cuda.stream(streams[1]):
         w1 = ops._workspace(torch.device("cuda"), 1024)
     assert w0.data_ptr() != w1.data_ptr()
+
+
+def test_randomized_shapes_against_oracle():
+    """Seeded random small problems across every route: M from 1 to 70
+    (skinny, two-tile, wide, 16-row chunks when K is not whole 64-code
+    steps), N from 1, K from one group, every format; gather with random
+    M rows per pair and expert counts."""
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        bits = int(rng.choice([4, 8]))
+        gs = int(rng.choice([32, 64, 128]))
+        dtype = str(rng.choice(["bfloat16", "float16"]))
+        K = gs * int(rng.integers(1, 12))
+        N = int(rng.integers(1, 300))
+        M = int(rng.choice([1, 2, 3, 5, 8, 9, 13, 16, 17, 40, 70]))
+        w, s, b = quantized(rng, N, K, gs, bits, dtype)
+        x = act(rng, (M, K), dtype)
+        print(f"case {case}: M={M} N={N} K={K} bits={bits} gs={gs} {dtype}", flush=True)
+        out = mq.quantized_matmul(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
+                                  group_size=gs, bits=bits)
+        res = O.check_output(from_dev(out), O.quantized_matmul_ref(x, w, s, b, gs, bits, dtype), dtype)
+        assert res["ok"], (case, res)
+    for case in range(12):
+        bits = int(rng.choice([4, 8]))
+        gs = int(rng.choice([32, 64, 128]))
+        K = gs * int(rng.integers(1, 8))
+        N = int(rng.integers(1, 200))
+        E = int(rng.integers(1, 20))
+        T = int(rng.integers(1, 40))
+        top = int(rng.integers(1, min(E, 6) + 1))
+        M = int(rng.choice([1, 2, 4, 7, 16]))
+        banks = [quantized(rng, N, K, gs, bits) for _ in range(E)]
+        w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+        b = np.stack([t[2] for t in banks])
+        idx = np.stack([rng.choice(E, size=top, replace=False) for _ in range(T)]).astype(np.int32)
+        x = act(rng, (T, 1, M, K))
+        print(f"gather {case}: T={T} top={top} E={E} M={M} N={N} K={K} bits={bits} gs={gs}",
+              flush=True)
+        out = mq.gather_qmm(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                            to_dev(b, "bfloat16"), rhs_indices=torch.from_numpy(idx).cuda(),
+                            group_size=gs, bits=bits)
+        ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, np.repeat(np.arange(T), top),
+                               idx.reshape(-1), gs, bits)
+        res = O.check_output(from_dev(out).reshape(T * top, M, N), ref)
+        assert res["ok"], (case, res)
