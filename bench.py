@@ -382,12 +382,15 @@ def main():
                     "pct_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}
 
         # config 3: prefill widths on the MFMA tile kernel (compute-bound)
-        for M in (512, 2048, 8192):
-            r = measure_qmm(torch, mq, M, N, K, 4, 20, 3, copies=2)
+        # configs[2] (512/2048/8192) plus points across the bandwidth/compute
+        # crossover (M ~ 95 at the MFMA ridge): HBM GB/s and TFLOP/s for each
+        for M in (32, 96, 256, 512, 2048, 8192):
+            r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 512 else 100, 3, copies=2)
             tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
             sweep[f"b4_K{K}_N{N}_M{M}"] = {
                 "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
-                "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+                "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "GBps": round(r["GBps"], 1)}
 
         # config 4: MoE gather at decode/verify widths (gate/up and down banks)
         for routing in ("zipf", "uniform"):

@@ -118,7 +118,7 @@ int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
   if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
   if (M == 0 || N == 0) return MQ_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
-  if (mq::wide_eligible(M, N, K, bits, group_size)) {
+  if (mq::wide_route(M, N, K, bits, group_size, mq::device_cu_count())) {
     rc = dispatch_16<mq::WideLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
                                      st);
     if (rc) return fail(rc, "quantized_matmul: no wide kernel for this configuration");

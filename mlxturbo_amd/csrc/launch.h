@@ -4,6 +4,8 @@
 // next to its kernels and explicitly instantiated in inst.hip; it enqueues on
 // the given stream and returns 0 or a HIP error / kStatusUnsupported.
 #pragma once
+#include <atomic>
+
 #include "mq_common.h"
 
 namespace mq {
@@ -52,11 +54,71 @@ struct GluLaunch {
 
 // ---- host-side routing and sizing ------------------------------------------
 
+// Compute units of the current device, cached per device.
+inline int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Row-tile height of the wide kernel: the one with the fewest (rounds of one
+// workgroup per CU; every height needs 92-147 KB of LDS) x (time of one tile),
+// tile times relative to BM = 256 measured at K=5120: 0.62 (64 rows), 0.71
+// (128), 1.0 (256).  A last round that fills few CUs costs as much as a full
+// one (K=5120 N=17408, 68 column tiles on 256 CUs: M=256 81 us with BM 128
+// against 112 with 256; M=512 119 with 256 against 172 with 128).
+inline int wide_bm_for(int64_t M, int64_t N, int cus, double* cost_us = nullptr,
+                       int64_t K = 5120) {
+  const int64_t cols = (N + 255) / 256;
+  const int bms[3] = {64, 128, 256};
+  const double tile_us[3] = {71.0, 81.0, 119.0};   // one tile at K=5120, measured
+  int best = 256;
+  double best_cost = 0.0;
+  for (int i = 2; i >= 0; --i) {
+    const int64_t wgs = cols * ((M + bms[i] - 1) / bms[i]);
+    const double cost = (double)((wgs + cus - 1) / cus) * tile_us[i] * (double)K / 5120.0;
+    if (i == 2 || cost < best_cost) {
+      best = bms[i];
+      best_cost = cost;
+    }
+  }
+  if (cost_us) *cost_us = best_cost;
+  return best;
+}
+
 // The wide kernel takes M > 16 rows, K in whole 64-code steps, 4/8-bit codes
 // and groups of 32/64/128.
 inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   (void)N;
   return M > 16 && K % 64 == 0 && (bits == 4 || bits == 8) && gs >= 32 && gs % 32 == 0;
+}
+
+// Wide tile or 16-row skinny launches for M > 16 rows: the cheaper by a
+// model fitted to measurements.  Few column tiles starve the wide grid
+// (K=17408 N=5120: 20 tiles; M=17..64 took 229-249 us wide against 40-87
+// in 16-row launches; K=4096 N=4096: 48 against 12-29), while at K=5120
+// N=17408 the wide tile wins from M ~ 56.  Skinny launch time: about 3 us
+// plus the weight bytes at 3.6 TB/s for one row, x1.15 for 2-4 rows, x1.4
+// for 5-8, x1.65 for 9-16.
+inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus) {
+  if (!wide_eligible(M, N, K, bits, gs)) return false;
+  double wide_us = 0.0;
+  wide_bm_for(M, N, cus, &wide_us, K);
+  const double one = 3.0 + (double)N * (double)K * bits / 8.0 / 3.6e6;
+  double skinny_us = 0.0;
+  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    const int64_t m = M - m0 < 16 ? M - m0 : 16;
+    skinny_us += one * (m > 8 ? 1.65 : m > 4 ? 1.4 : m > 1 ? 1.15 : 1.0);
+  }
+  return wide_us < skinny_us;
 }
 
 // gather_qmm: up to kGatherFusedMaxP pairs are grouped by expert inside the

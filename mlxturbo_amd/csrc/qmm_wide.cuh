@@ -322,10 +322,6 @@ __global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
                               biases + wrow * G, ncols, K, store, wide_smem);
 }
 
-// Row-tile height by row count: 256-row tiles leave most of the 256 CUs idle
-// on short matrices.
-inline int wide_bm_for(int64_t M) { return M <= 64 ? 64 : M <= 128 ? 128 : 256; }
-
 template <int DT, int BITS, int GS, int BM>
 inline int wide_launch_bm(const void* x, const uint32_t* w, const void* s, const void* b,
                           void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
@@ -346,7 +342,7 @@ int WideLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* 
   // one tile's x rows and weight rows must fit a 31-bit buffer range
   if (K * 2 * 256 >= ((int64_t)1 << 31) || M > ((int64_t)1 << 31) / 256 * 256)
     return kStatusUnsupported;
-  switch (wide_bm_for(M)) {
+  switch (wide_bm_for(M, N, device_cu_count(), nullptr, K)) {
     case 64: return wide_launch_bm<DT, BITS, GS, 64>(x, w, s, b, out, M, N, K, st);
     case 128: return wide_launch_bm<DT, BITS, GS, 128>(x, w, s, b, out, M, N, K, st);
     default: return wide_launch_bm<DT, BITS, GS, 256>(x, w, s, b, out, M, N, K, st);

@@ -245,17 +245,19 @@ def test_skinny_long_k_many_rows(M):
 
 # ------------------------------------------------- BASELINE config 3 (wide)
 
-@pytest.mark.parametrize("M", [512, 2048, 8192])
+@pytest.mark.parametrize("M", [40, 100, 300, 600, 512, 2048, 8192])
 def test_config3_wide(cfg2_weights, M):
     """Prefill widths through the MFMA tile kernel, full size; the oracle checks
-    64 sampled rows x 512 sampled columns."""
+    64 sampled rows x 512 sampled columns.  M=40 runs as 16-row skinny
+    launches, 100 / 300 / 600 pick tile heights 64 / 128 / 256 with a ragged
+    last row tile."""
     K, N = 5120, 17408
     w, s, b, deq, dev = cfg2_weights[(K, N)]
     rng = np.random.default_rng(300 + M)
     x = act(rng, (M, K))
     out = mq.quantized_matmul(to_dev(x, "bfloat16"), *dev)
     assert out.shape == (M, N) and torch.isfinite(out).all()
-    rows = np.sort(rng.choice(M, size=64, replace=False))
+    rows = np.sort(rng.choice(M, size=min(M, 64), replace=False))
     cols = np.sort(rng.choice(N, size=512, replace=False))
     ref = (O.bf16_to_f32(x[rows]).astype(np.float64) @ deq[cols].T).astype(np.float32)
     got = out[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()]
