@@ -392,6 +392,16 @@ def main():
                 "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                 "GBps": round(r["GBps"], 1)}
 
+        # the transposed (down-proj) shape at prefill widths: few column
+        # tiles, K split over workgroups
+        for M in (64, 512, 2048):
+            r = measure_qmm(torch, mq, M, K, N, 4, 20 if M >= 512 else 100, 3, copies=2)
+            tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
+            sweep[f"b4_K{N}_N{K}_M{M}"] = {
+                "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
+                "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "GBps": round(r["GBps"], 1)}
+
         # config 4: MoE gather at decode/verify widths (gate/up and down banks)
         for routing in ("zipf", "uniform"):
             for T in (1, 4, 8):

@@ -78,6 +78,30 @@ int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
                         int group_size, int bits, int dtype, int transpose, void* hip_stream);
 
 /*
+ * Bytes of device workspace mq_quantized_matmul_ws can use for an M x N x K
+ * problem (float partial sums when the K range is split over workgroups:
+ * narrow matrices at prefill widths), 0 when the chosen plan needs none.
+ * No counterpart in the reference (MLX allocates its own temporaries); it
+ * is the sizing call of the entry point below.
+ */
+size_t mq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size,
+                                          int bits);
+
+/*
+ * mq_quantized_matmul with a caller-provided device workspace of
+ * workspace_bytes bytes (16-byte aligned, may be NULL): when it holds
+ * mq_quantized_matmul_workspace_size(M, N, K, group_size, bits) bytes, wide
+ * problems may split K over workgroups and reduce the partials in a second
+ * kernel (same results up to the order of the float sums).  Replaces the
+ * same mx.quantized_matmul call as mq_quantized_matmul; calls sharing a
+ * workspace must be ordered (one stream).
+ */
+int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                           int group_size, int bits, int dtype, int transpose, void* workspace,
+                           size_t workspace_bytes, void* hip_stream);
+
+/*
  * Bytes of device workspace mq_gather_qmm needs for P index pairs.
  */
 size_t mq_gather_qmm_workspace_size(int64_t P, int64_t M);

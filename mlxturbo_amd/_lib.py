@@ -28,6 +28,8 @@ EXPORTED = (
     "mq_launch_count",
     "mq_dequantize",
     "mq_quantized_matmul",
+    "mq_quantized_matmul_workspace_size",
+    "mq_quantized_matmul_ws",
     "mq_gather_qmm_workspace_size",
     "mq_gather_qmm",
     "mq_gather_glu",
@@ -58,6 +60,11 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_quantized_matmul.restype = _int
     lib.mq_quantized_matmul.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
                                         _int, _int, _vp]
+    lib.mq_quantized_matmul_workspace_size.restype = ctypes.c_size_t
+    lib.mq_quantized_matmul_workspace_size.argtypes = [_i64, _i64, _i64, _int, _int]
+    lib.mq_quantized_matmul_ws.restype = _int
+    lib.mq_quantized_matmul_ws.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
+                                           _int, _int, _vp, ctypes.c_size_t, _vp]
     lib.mq_gather_qmm_workspace_size.restype = ctypes.c_size_t
     lib.mq_gather_qmm_workspace_size.argtypes = [_i64, _i64]
     lib.mq_gather_qmm.restype = _int

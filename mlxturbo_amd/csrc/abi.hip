@@ -102,9 +102,16 @@ int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, voi
   return check_launch("dequantize");
 }
 
-int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
-                        const void* biases, void* out, int64_t M, int64_t N, int64_t K,
-                        int group_size, int bits, int dtype, int transpose, void* hip_stream) {
+size_t mq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size,
+                                          int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size) return 0;
+  return mq::qmm_workspace_bytes(M, N, K, bits, group_size, mq::device_cu_count());
+}
+
+int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                           int group_size, int bits, int dtype, int transpose, void* workspace,
+                           size_t workspace_bytes, void* hip_stream) {
   int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
   if (rc) return rc;
   if (!x || !out) return fail(MQ_EINVAL, "x and out must be non-null");
@@ -116,19 +123,37 @@ int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
   if (N > INT32_MAX || K > INT32_MAX || M > INT32_MAX)
     return fail(MQ_EINVAL, "dimension exceeds int32 range");
   if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (workspace && !aligned16(workspace)) return fail(MQ_EINVAL, "workspace must be 16-byte aligned");
   if (M == 0 || N == 0) return MQ_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
-  if (mq::wide_route(M, N, K, bits, group_size, mq::device_cu_count())) {
+  const int cus = mq::device_cu_count();
+  // K splits only when the caller's workspace holds the planned partials
+  const size_t need = mq::qmm_workspace_bytes(M, N, K, bits, group_size, cus);
+  const bool split_ok = workspace && need && workspace_bytes >= need;
+  if (mq::wide_route(M, N, K, bits, group_size, cus, split_ok)) {
+    int nl = 0;
     rc = dispatch_16<mq::WideLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
-                                     st);
+                                     split_ok ? workspace : nullptr,
+                                     split_ok ? workspace_bytes : (size_t)0, st, &nl);
     if (rc) return fail(rc, "quantized_matmul: no wide kernel for this configuration");
-    return check_launch("quantized_matmul(wide)");
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      return fail((int)e, "quantized_matmul(wide): launch failed: %s", hipGetErrorString(e));
+    g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+    return MQ_OK;
   }
   rc = dispatch_16<mq::SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
                                      st);
   if (rc) return fail(rc, "quantized_matmul: no kernel for dtype=%d bits=%d group_size=%d", dtype,
                       bits, group_size);
   return check_launch("quantized_matmul(skinny)");
+}
+
+int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, int dtype, int transpose, void* hip_stream) {
+  return mq_quantized_matmul_ws(x, w, scales, biases, out, M, N, K, group_size, bits, dtype,
+                                transpose, nullptr, 0, hip_stream);
 }
 
 size_t mq_gather_qmm_workspace_size(int64_t P, int64_t M) {

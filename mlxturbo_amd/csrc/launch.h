@@ -24,11 +24,15 @@ struct SkinnyLaunch {
                  int64_t M, int64_t N, int64_t K, hipStream_t st);
 };
 
-// quantized_matmul for M > 16 rows on the MFMA tile kernel (qmm_wide.cuh).
+// quantized_matmul for M > 16 rows on the MFMA tile kernel (qmm_wide.cuh);
+// with a workspace of wide_workspace_bytes(wide_plan(...), M, N) bytes the
+// K range may be split over workgroups (float partial planes plus a reduce
+// kernel).  *nlaunch counts the kernels enqueued.
 template <int DT, int BITS, int GS>
 struct WideLaunch {
   static int run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
-                 int64_t M, int64_t N, int64_t K, hipStream_t st);
+                 int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t st,
+                 int* nlaunch);
 };
 
 // gather_qmm over P (x batch, expert) pairs (gather.cuh); *nlaunch counts the
@@ -69,29 +73,49 @@ inline int device_cu_count() {
   return n;
 }
 
-// Row-tile height of the wide kernel: the one with the fewest (rounds of one
-// workgroup per CU; every height needs 92-147 KB of LDS) x (time of one tile),
-// tile times relative to BM = 256 measured at K=5120: 0.62 (64 rows), 0.71
-// (128), 1.0 (256).  A last round that fills few CUs costs as much as a full
-// one (K=5120 N=17408, 68 column tiles on 256 CUs: M=256 81 us with BM 128
-// against 112 with 256; M=512 119 with 256 against 172 with 128).
-inline int wide_bm_for(int64_t M, int64_t N, int cus, double* cost_us = nullptr,
-                       int64_t K = 5120) {
+// Launch plan of the wide kernel: row-tile height and K splits, the pair
+// with the fewest (rounds of one workgroup per CU; every height needs 92-147
+// KB of LDS) x (time of one tile), plus the split reduction.  Tile times at
+// K=5120, measured: 71 us (64 rows), 81 (128), 119 (256); a tile over a
+// K slice costs ~3 us plus its share.  A last round that fills few CUs costs
+// as much as a full one (K=5120 N=17408, 68 column tiles on 256 CUs: M=256
+// 81 us with BM 128 against 112 with 256; M=512 119 with 256 against 172 with
+// 128).  Splitting K serves narrow matrices, whose few column tiles leave
+// most CUs idle (K=17408 N=5120 has 20).  Partial planes are float [M, N]
+// per split, written by the tile kernel and summed in split order by a
+// reduce kernel: (8 S + 2) M N bytes at ~3.5 TB/s.
+struct WidePlan {
+  int bm = 256, splits = 1;
+  double cost_us = 0.0;
+};
+
+inline WidePlan wide_plan(int64_t M, int64_t N, int64_t K, int cus, int max_splits = 8) {
   const int64_t cols = (N + 255) / 256;
+  const int64_t nk = K / 64;
   const int bms[3] = {64, 128, 256};
   const double tile_us[3] = {71.0, 81.0, 119.0};   // one tile at K=5120, measured
-  int best = 256;
-  double best_cost = 0.0;
-  for (int i = 2; i >= 0; --i) {
-    const int64_t wgs = cols * ((M + bms[i] - 1) / bms[i]);
-    const double cost = (double)((wgs + cus - 1) / cus) * tile_us[i] * (double)K / 5120.0;
-    if (i == 2 || cost < best_cost) {
-      best = bms[i];
-      best_cost = cost;
+  WidePlan best;
+  bool first = true;
+  for (int sp = 1; sp <= max_splits; sp *= 2) {
+    if (sp > 1 && nk / sp < 8) break;                 // at least 8 k-steps per split
+    for (int i = 2; i >= 0; --i) {
+      const int64_t wgs = cols * ((M + bms[i] - 1) / bms[i]) * sp;
+      const double tile = (sp > 1 ? 3.0 : 0.0) + tile_us[i] * ((double)K / sp) / 5120.0;
+      double cost = (double)((wgs + cus - 1) / cus) * tile;
+      if (sp > 1) cost += (8.0 * sp + 2.0) * (double)M * (double)N / 3.5e6;
+      if (first || cost < best.cost_us) {
+        best.bm = bms[i];
+        best.splits = sp;
+        best.cost_us = cost;
+        first = false;
+      }
     }
   }
-  if (cost_us) *cost_us = best_cost;
   return best;
+}
+
+inline size_t wide_workspace_bytes(const WidePlan& plan, int64_t M, int64_t N) {
+  return plan.splits > 1 ? (size_t)plan.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 // The wide kernel takes M > 16 rows, K in whole 64-code steps, 4/8-bit codes
@@ -107,11 +131,11 @@ inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 // in 16-row launches; K=4096 N=4096: 48 against 12-29), while at K=5120
 // N=17408 the wide tile wins from M ~ 56.  Skinny launch time: about 3 us
 // plus the weight bytes at 3.6 TB/s for one row, x1.15 for 2-4 rows, x1.4
-// for 5-8, x1.65 for 9-16.
-inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus) {
+// for 5-8, x1.65 for 9-16.  split_ok: a workspace is available for K splits.
+inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus,
+                       bool split_ok) {
   if (!wide_eligible(M, N, K, bits, gs)) return false;
-  double wide_us = 0.0;
-  wide_bm_for(M, N, cus, &wide_us, K);
+  const double wide_us = wide_plan(M, N, K, cus, split_ok ? 8 : 1).cost_us;
   const double one = 3.0 + (double)N * (double)K * bits / 8.0 / 3.6e6;
   double skinny_us = 0.0;
   for (int64_t m0 = 0; m0 < M; m0 += 16) {
@@ -119,6 +143,13 @@ inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cu
     skinny_us += one * (m > 8 ? 1.65 : m > 4 ? 1.4 : m > 1 ? 1.15 : 1.0);
   }
   return wide_us < skinny_us;
+}
+
+// Workspace bytes of quantized_matmul (K splits of the wide kernel), 0 when
+// the chosen plan needs none.
+inline size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus) {
+  if (!wide_route(M, N, K, bits, gs, cus, true)) return 0;
+  return wide_workspace_bytes(wide_plan(M, N, K, cus), M, N);
 }
 
 // gather_qmm: up to kGatherFusedMaxP pairs are grouped by expert inside the

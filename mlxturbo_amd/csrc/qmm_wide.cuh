@@ -60,16 +60,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_rsrc(const void* base, in
                                            0x00020000);
 }
 
-// One BM x 256 output tile.  x rows come from xrsrc at per-row byte offsets
-// xrow_off(r) (past the range for rows that do not exist); w / scales /
-// biases point at the tile's first weight row, of which nrows (<= 256) exist;
-// store(r, c, v) writes row r, tile column c (< nrows) of the output.
+// One BM x 256 output tile over k-steps kt0 .. kt0 + nkl - 1 (64 codes each).
+// x rows come from xrsrc at per-row byte offsets xrow_off(r) (past the range
+// for rows that do not exist); w / scales / biases point at the tile's first
+// weight row, of which nrows (<= 256) exist; store(r, c, v) receives the
+// float sum of row r, tile column c (< nrows).
 template <int DT, int BITS, int GS, int BM, class XRowOff, class Store>
 __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff xrow_off,
                                           const uint32_t* __restrict__ w,
                                           const uint16_t* __restrict__ scales,
                                           const uint16_t* __restrict__ biases, int nrows, int K,
-                                          Store store, uint16_t* wide_smem) {
+                                          int kt0, int nkl, Store store, uint16_t* wide_smem) {
   constexpr int BN = kWideBN, BK = kWideBK, LD = kWideLD, NT = kWideNT;
   constexpr int WGM = BM == 256 ? 4 : 2;        // waves along M
   constexpr int WGN = 8 / WGM;                  // waves along N
@@ -93,7 +94,7 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
   const int wm = wave / WGN, wn = wave % WGN;
   const int64_t Kw = (int64_t)K * BITS / 32;
   const int G = K / GS;
-  const int nk = K / BK;
+  const int nk = nkl;
 
   // rows past nrows are past the weight range and read zeros
   const auto rwd = wide_rsrc(w, (int64_t)nrows * Kw * 4);
@@ -125,7 +126,7 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
   };
   Set S0, S1;
   auto gload = [&](Set& st, int kt) {
-    const int k0 = kt * BK;
+    const int k0 = (kt0 + kt) * BK;
 #pragma unroll
     for (int i = 0; i < XPT; ++i)
       st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, xo[i], k0 * 2, 0);
@@ -238,34 +239,70 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = 32 * TM * wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (c < nrows) store(r, c, T::round1(acc[i][j][e]));
+        if (c < nrows) store(r, c, acc[i][j][e]);
       }
     }
 }
 
-// Dense rows: grid (ceil(N / 256), ceil(M / BM)), 512 threads, dynamic LDS
-// wide_lds_bytes<BM>(); 256 * K * 2 < 2^31 and 256 * K * BITS / 8 < 2^31.
+// Dense rows: grid (ceil(N / 256), ceil(M / BM), splits), 512 threads,
+// dynamic LDS wide_lds_bytes<BM>(); 256 * K * 2 < 2^31 and 256 * K * BITS / 8
+// < 2^31.  With part == nullptr (splits == 1) the tile rounds its sums into
+// out; otherwise split z sums k-steps [z nk / splits, (z + 1) nk / splits)
+// into the float plane part[z] ([M, N]) and wide_reduce_kernel adds the
+// planes in split order.
 template <int DT, int BITS, int GS, int BM>
 __global__ __launch_bounds__(kWideNT) void qmm_wide_kernel(const uint16_t* __restrict__ x,
                                                            const uint32_t* __restrict__ w,
                                                            const uint16_t* __restrict__ scales,
                                                            const uint16_t* __restrict__ biases,
-                                                           uint16_t* __restrict__ out, int M,
+                                                           uint16_t* __restrict__ out,
+                                                           float* __restrict__ part, int M,
                                                            int N, int K) {
   extern __shared__ __align__(16) uint16_t wide_smem[];
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kWideBN;
   const int mrows = min(BM, M - m0);
   const int64_t G = K / GS;
+  const int nk = K / kWideBK, z = blockIdx.z, splits = gridDim.z;
+  const int kt0 = (int)((int64_t)nk * z / splits), kt1 = (int)((int64_t)nk * (z + 1) / splits);
   // descriptors cover this tile's rows only: rows past M read zeros, no
   // 64-bit offsets inside the tile
   const auto xr = wide_rsrc(x + (int64_t)m0 * K, (int64_t)mrows * K * 2);
   auto xrow_off = [&](int r) { return (uint32_t)r * (uint32_t)K * 2u; };
-  uint16_t* ot = out + (int64_t)m0 * N + n0;
-  auto store = [&](int r, int c, uint16_t v) {
-    if (r < mrows) ot[(int64_t)r * N + c] = v;
-  };
-  wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + (int64_t)n0 * K * BITS / 32, scales + n0 * G,
-                              biases + n0 * G, min(kWideBN, N - n0), K, store, wide_smem);
+  if (part) {
+    float* pt = part + ((int64_t)z * M + m0) * N + n0;
+    auto store = [&](int r, int c, float v) {
+      if (r < mrows) pt[(int64_t)r * N + c] = v;
+    };
+    wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + (int64_t)n0 * K * BITS / 32, scales + n0 * G,
+                                biases + n0 * G, min(kWideBN, N - n0), K, kt0, kt1 - kt0, store,
+                                wide_smem);
+  } else {
+    uint16_t* ot = out + (int64_t)m0 * N + n0;
+    auto store = [&](int r, int c, float v) {
+      if (r < mrows) ot[(int64_t)r * N + c] = T16<DT>::round1(v);
+    };
+    wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + (int64_t)n0 * K * BITS / 32, scales + n0 * G,
+                                biases + n0 * G, min(kWideBN, N - n0), K, kt0, kt1 - kt0, store,
+                                wide_smem);
+  }
+}
+
+// out = round(sum over splits of part[s]) in split order, 4 elements per
+// thread; grid ceil(M * N / 1024), 256 threads.
+template <int DT>
+__global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restrict__ part,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t MN, int splits) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t i = i0 + e;
+    if (i < MN) {
+      float v = part[i];
+      for (int z = 1; z < splits; ++z) v += part[(int64_t)z * MN + i];
+      out[i] = T16<DT>::round1(v);
+    }
+  }
 }
 
 // Expert-grouped rows (prefill gather_qmm, reference moe_grouped_gemm.py:
@@ -314,38 +351,53 @@ __global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
   const auto xr = wide_rsrc(x, (int64_t)B * Mi * K * 2);
   auto xrow_off = [&](int r) { return s_xoff[r]; };
   uint16_t* ot = out + n0;
-  auto store = [&](int r, int c, uint16_t v) {
+  auto store = [&](int r, int c, float v) {
     const int o = s_orow[r];
-    if (o >= 0) ot[(int64_t)o * N + c] = v;
+    if (o >= 0) ot[(int64_t)o * N + c] = T16<DT>::round1(v);
   };
   wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + wrow * K * BITS / 32, scales + wrow * G,
-                              biases + wrow * G, ncols, K, store, wide_smem);
+                              biases + wrow * G, ncols, K, 0, K / kWideBK, store, wide_smem);
 }
 
 template <int DT, int BITS, int GS, int BM>
 inline int wide_launch_bm(const void* x, const uint32_t* w, const void* s, const void* b,
-                          void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+                          void* out, int64_t M, int64_t N, int64_t K, int splits, void* ws,
+                          hipStream_t st) {
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_wide_kernel<DT, BITS, GS, BM>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds_bytes<BM>());
   if (attr != hipSuccess) return (int)attr;
-  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)((M + BM - 1) / BM));
+  float* part = splits > 1 ? static_cast<float*>(ws) : nullptr;
+  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)((M + BM - 1) / BM),
+                  (unsigned)splits);
   hipLaunchKernelGGL((qmm_wide_kernel<DT, BITS, GS, BM>), grid, dim3(kWideNT),
                      wide_lds_bytes<BM>(), st, (const uint16_t*)x, w, (const uint16_t*)s,
-                     (const uint16_t*)b, (uint16_t*)out, (int)M, (int)N, (int)K);
+                     (const uint16_t*)b, (uint16_t*)out, part, (int)M, (int)N, (int)K);
+  if (splits > 1) {
+    const int64_t MN = M * N;
+    hipLaunchKernelGGL((wide_reduce_kernel<DT>), dim3((unsigned)((MN + 1023) / 1024)), dim3(256),
+                       0, st, (const float*)part, (uint16_t*)out, MN, splits);
+  }
   return 0;
 }
 
 template <int DT, int BITS, int GS>
 int WideLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s, const void* b,
-                                  void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+                                  void* out, int64_t M, int64_t N, int64_t K, void* ws,
+                                  size_t ws_bytes, hipStream_t st, int* nlaunch) {
   // one tile's x rows and weight rows must fit a 31-bit buffer range
   if (K * 2 * 256 >= ((int64_t)1 << 31) || M > ((int64_t)1 << 31) / 256 * 256)
     return kStatusUnsupported;
-  switch (wide_bm_for(M, N, device_cu_count(), nullptr, K)) {
-    case 64: return wide_launch_bm<DT, BITS, GS, 64>(x, w, s, b, out, M, N, K, st);
-    case 128: return wide_launch_bm<DT, BITS, GS, 128>(x, w, s, b, out, M, N, K, st);
-    default: return wide_launch_bm<DT, BITS, GS, 256>(x, w, s, b, out, M, N, K, st);
+  const int cus = device_cu_count();
+  WidePlan plan = wide_plan(M, N, K, cus);
+  if (plan.splits > 1 && (!ws || ws_bytes < wide_workspace_bytes(plan, M, N)))
+    plan = wide_plan(M, N, K, cus, 1);
+  const int splits = plan.splits;
+  *nlaunch += splits > 1 ? 2 : 1;
+  switch (plan.bm) {
+    case 64: return wide_launch_bm<DT, BITS, GS, 64>(x, w, s, b, out, M, N, K, splits, ws, st);
+    case 128: return wide_launch_bm<DT, BITS, GS, 128>(x, w, s, b, out, M, N, K, splits, ws, st);
+    default: return wide_launch_bm<DT, BITS, GS, 256>(x, w, s, b, out, M, N, K, splits, ws, st);
   }
 }
 

@@ -160,9 +160,15 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         return out
     x_ = _aligned(x.reshape(M, K))
     w_, s_, b_ = _aligned(w), _aligned(scales), _aligned(biases)
-    rc = _lib.lib().mq_quantized_matmul(x_.data_ptr(), w_.data_ptr(), s_.data_ptr(),
-                                        b_.data_ptr(), out.data_ptr(), M, N, K, group_size, bits,
-                                        code, 1, _stream_ptr(out))
+    lib = _lib.lib()
+    # wide problems on narrow matrices split K over workgroups into this
+    # stream's workspace
+    nbytes = int(lib.mq_quantized_matmul_workspace_size(M, N, K, group_size, bits))
+    ws = _workspace(dev, nbytes) if nbytes else None
+    rc = lib.mq_quantized_matmul_ws(x_.data_ptr(), w_.data_ptr(), s_.data_ptr(), b_.data_ptr(),
+                                    out.data_ptr(), M, N, K, group_size, bits, code, 1,
+                                    ws.data_ptr() if ws is not None else None,
+                                    ws.numel() if ws is not None else 0, _stream_ptr(out))
     _lib.check(rc, "quantized_matmul")
     return out
 

@@ -80,6 +80,19 @@ def test_qmm_argument_validation(lib, kw, code, needle):
     assert needle in lib.mq_last_error().decode()
 
 
+def test_qmm_workspace_sizing(lib):
+    # narrow matrix at a prefill width: K split over workgroups, float partials
+    need = lib.mq_quantized_matmul_workspace_size(512, 5120, 17408, 64, 4)
+    assert need > 0 and need % (512 * 5120 * 4) == 0
+    # decode widths and the wide matrix at large M need none
+    assert lib.mq_quantized_matmul_workspace_size(1, 5120, 17408, 64, 4) == 0
+    assert lib.mq_quantized_matmul_workspace_size(8192, 17408, 5120, 64, 4) == 0
+    assert lib.mq_quantized_matmul_workspace_size(0, 5120, 17408, 64, 4) == 0
+    rc = lib.mq_quantized_matmul_ws(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 16, 256, 64, 4, 0, 1,
+                                    FAKE + 4, 1024, None)
+    assert rc == -1 and b"workspace" in lib.mq_last_error()
+
+
 def test_empty_problem_is_a_noop(lib):
     assert _qmm(lib, M=0) == 0
     assert _qmm(lib, N=0) == 0
@@ -138,6 +151,14 @@ class _FakeLib:
         self.calls.append(("qmm", dict(M=M, N=N, K=K, gs=gs, bits=bits, dtype=dtype,
                                        transpose=transpose)))
         return 0
+
+    def mq_quantized_matmul_workspace_size(self, M, N, K, gs, bits):
+        return 0
+
+    def mq_quantized_matmul_ws(self, x, w, s, b, out, M, N, K, gs, bits, dtype, transpose, ws,
+                               wsb, stream):
+        return self.mq_quantized_matmul(x, w, s, b, out, M, N, K, gs, bits, dtype, transpose,
+                                        stream)
 
     def mq_gather_qmm_workspace_size(self, P, M):
         return 0

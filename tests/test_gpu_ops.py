@@ -243,6 +243,36 @@ def test_skinny_long_k_many_rows(M):
     np.testing.assert_array_equal(bits16(out)[M - 1], one[0])
 
 
+@pytest.mark.parametrize("M", [24, 256, 512, 1000])
+def test_wide_split_k_narrow_matrix(cfg2_weights, M):
+    """The down-proj shape (K=17408, N=5120) at prefill widths: 20 column
+    tiles, so the wide kernel splits K over workgroups into the workspace
+    (float partials, reduce kernel).  Checked on sampled rows and columns
+    against the oracle, and against the unsplit launch of the plain entry
+    point (no workspace) to the same tolerance."""
+    K, N = 17408, 5120
+    w, s, b, deq, dev = cfg2_weights[(K, N)]
+    lib = _lib.lib()
+    assert M < 256 or lib.mq_quantized_matmul_workspace_size(M, N, K, 64, 4) > 0
+    rng = np.random.default_rng(400 + M)
+    x = act(rng, (M, K))
+    xd = to_dev(x, "bfloat16")
+    n0 = mq.launch_count()
+    out = mq.quantized_matmul(xd, *dev)
+    assert mq.launch_count() > n0
+    rows = np.sort(rng.choice(M, size=min(M, 48), replace=False))
+    cols = np.sort(rng.choice(N, size=384, replace=False))
+    ref = (O.bf16_to_f32(x[rows]).astype(np.float64) @ deq[cols].T).astype(np.float32)
+    sel = lambda t: t[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()]  # noqa: E731
+    _check(sel(out), ref)
+    plain = torch.empty_like(out)
+    rc = lib.mq_quantized_matmul(xd.data_ptr(), dev[0].data_ptr(), dev[1].data_ptr(),
+                                 dev[2].data_ptr(), plain.data_ptr(), M, N, K, 64, 4, 0, 1,
+                                 torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    _check(sel(plain), ref)
+
+
 # ------------------------------------------------- BASELINE config 3 (wide)
 
 @pytest.mark.parametrize("M", [40, 100, 300, 600, 512, 2048, 8192])
