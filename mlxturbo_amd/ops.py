@@ -41,7 +41,7 @@ _BITS = (2, 3, 4, 5, 6, 8)
 
 
 def _stream_ptr(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def _require_gpu(*ts: torch.Tensor) -> torch.device:
@@ -173,8 +173,66 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+class PreparedWeights:
+    """Weight-side arguments of :func:`quantized_matmul`, validated once
+    (the per-call cost of a layer that reuses its weights is then the x
+    checks and the launch).  ``matches`` tells whether the tensors are still
+    the ones validated."""
+
+    __slots__ = ("w", "s", "b", "N", "K", "group_size", "bits", "dtype", "dev", "key")
+
+    def __init__(self, w, scales, biases, group_size: int = 64, bits: int = 4,
+                 mode: str = "affine"):
+        _check_mode(mode, biases)
+        self.dev = _require_gpu(w, scales, biases)
+        if w.ndim != 2:
+            raise NotImplementedError("batched w: only 2-D weights are on this path")
+        self.K = _check_quant(w, scales, biases, group_size, bits)
+        self.N = w.shape[0]
+        self.w, self.s, self.b = _aligned(w), _aligned(scales), _aligned(biases)
+        self.group_size, self.bits, self.dtype = group_size, bits, scales.dtype
+        self.key = (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits)
+
+    def matches(self, w, scales, biases, group_size: int, bits: int) -> bool:
+        return self.key == (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits)
+
+
+_QMM_WS_BYTES: dict = {}
+
+
+def quantized_matmul_prepared(x: torch.Tensor, p: PreparedWeights) -> torch.Tensor:
+    """:func:`quantized_matmul` with weights validated by :class:`PreparedWeights`."""
+    if x.device != p.dev or x.dtype != p.dtype or x.ndim < 1 or x.shape[-1] != p.K:
+        return quantized_matmul(x, p.w, p.s, p.b, group_size=p.group_size, bits=p.bits)
+    N, K = p.N, p.K
+    M = x.numel() // K
+    out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=p.dev)
+    if M == 0 or N == 0:
+        return out
+    x_ = x if x.is_contiguous() and x.data_ptr() % 16 == 0 else _aligned(x)
+    lib = _lib.lib()
+    ws = None
+    if M > 16:
+        key = (M, N, K, p.group_size, p.bits)
+        nbytes = _QMM_WS_BYTES.get(key)
+        if nbytes is None:
+            nbytes = int(lib.mq_quantized_matmul_workspace_size(M, N, K, p.group_size, p.bits))
+            if len(_QMM_WS_BYTES) > 256:
+                _QMM_WS_BYTES.clear()
+            _QMM_WS_BYTES[key] = nbytes
+        ws = _workspace(p.dev, nbytes) if nbytes else None
+    rc = lib.mq_quantized_matmul_ws(x_.data_ptr(), p.w.data_ptr(), p.s.data_ptr(),
+                                    p.b.data_ptr(), out.data_ptr(), M, N, K, p.group_size,
+                                    p.bits, _DTYPE_CODE[x.dtype], 1,
+                                    ws.data_ptr() if ws is not None else None,
+                                    ws.numel() if ws is not None else 0, _stream_ptr(out))
+    _lib.check(rc, "quantized_matmul")
+    return out
+
+
 def _stream_of(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 _WS_CACHE: dict = {}
@@ -184,7 +242,8 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     """The gather workspace of the current stream (kernels on one stream run
     in order, so consecutive calls can share it; calls on other streams get
     their own, as concurrent calls must not share one)."""
-    key = (dev.type, dev.index, _stream_of(dev))
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device(),
+           _stream_of(dev))
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
@@ -391,5 +450,6 @@ def launch_count() -> int:
     return _lib.launch_count()
 
 
-__all__: Sequence[str] = ("dequantize", "quantized_matmul", "gather_qmm", "gather_glu",
-                          "moe_combine", "launch_count")
+__all__: Sequence[str] = ("dequantize", "quantized_matmul", "quantized_matmul_prepared",
+                          "PreparedWeights", "gather_qmm", "gather_glu", "moe_combine",
+                          "launch_count")

@@ -221,3 +221,28 @@ def test_switch_glu_fused_gate_up(T):
     got = glu(to_dev(x, "bfloat16"), torch.from_numpy(idx).cuda(), scores)
     want = (y.float() * scores[..., None]).sum(-2)
     assert O.check_output(from_dev(got), want.cpu().numpy())["ok"]
+
+
+@pytest.mark.gpu
+def test_prepared_weights_follow_buffer_changes():
+    """QuantizedLinear validates its weights once; replacing a buffer (new
+    tensor) or loading new values in place both reach the kernel."""
+    rng = np.random.default_rng(90)
+    N, K = 96, 256
+    w1, s1, b1 = quantized(rng, N, K)
+    w2, s2, b2 = quantized(rng, N, K)
+    layer = QuantizedLinear(to_dev(w1), to_dev(s1, "bfloat16"), to_dev(b1, "bfloat16"))
+    x = to_dev(act(rng, (3, K)), "bfloat16")
+    first = bits16(layer(x))
+    layer.weight = to_dev(w2)
+    layer.scales = to_dev(s2, "bfloat16")
+    layer.biases = to_dev(b2, "bfloat16")
+    want = bits16(mq.quantized_matmul(x, layer.weight, layer.scales, layer.biases))
+    np.testing.assert_array_equal(bits16(layer(x)), want)
+    layer.weight.copy_(to_dev(w1))
+    layer.scales.copy_(to_dev(s1, "bfloat16"))
+    layer.biases.copy_(to_dev(b1, "bfloat16"))
+    np.testing.assert_array_equal(bits16(layer(x)), first)
+    # a wrong activation dtype still raises the operator's error
+    with pytest.raises(NotImplementedError):
+        layer(x.half())
