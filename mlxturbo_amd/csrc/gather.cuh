@@ -510,9 +510,19 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
   int R = M <= kQmvMaxXM ? (int)(kQmvMaxXM / M) : 1;
   if (R > B) R = (int)(B > 0 ? B : 1);
   const int XM = (B * M * K * 2 < ((int64_t)1 << 31)) ? qmv_xm_for(R * M) : 0;
-  // waves per tile: the K split only pays when each wave gets a step
+  int64_t max_seg = P;
+  if (P > kGatherFusedMaxP) {
+    const int64_t bound = (P + R - 1) / R + E + 1;
+    if (bound < max_seg) max_seg = bound;
+  }
+  // waves per tile: split K over 4 or 2 waves only while the tiles are few
+  // (about 2048 waves in all) and each wave gets a step.  Config-4 banks,
+  // zipf routing: gate/up T=1 6.9 us split 4 ways against 8.8 unsplit, T=8
+  // 22 unsplit against 30 split 4 ways; down T=4 10.0 unsplit against 12.2.
   const int64_t nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
-  const int nwt = nsteps >= 4 ? 4 : nsteps >= 2 ? 2 : 1;
+  const int64_t tiles = max_seg * ((N + 15) / 16);
+  int nwt = 4;
+  while (nwt > 1 && (nwt > nsteps || tiles * nwt > 2048)) nwt /= 2;
   const int ng = C::NW / nwt;
   constexpr int TJ = GLU ? 2 : 1;
   const bool sbl =
@@ -523,20 +533,18 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
     return (size_t)(C::NW / wpt) *
            gather_group_lds<BITS, GS, C::GPL>(wpt, xmax, with_sb, (int)(K / GS), TJ);
   };
-  int64_t max_seg = P;
   const int32_t* wsp = nullptr;
   if (P > kGatherFusedMaxP) {
-    const int64_t bound = (P + R - 1) / R + E + 1;
-    if (bound < max_seg) max_seg = bound;
     if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
     wsp = (const int32_t*)ws;
     *nlaunch += 1;
   }
   // tile rounds per workgroup: enough rows per workgroup to amortize segment
-  // discovery, while keeping at least ~1024 workgroups for small problems
+  // discovery while keeping ~512 workgroups or more (down bank T=8: 18.6 us
+  // with 4 rounds against 25.8 with 1)
   const int64_t slots = (N + 16 * ng - 1) / (16 * ng);
   int tpw = 1;
-  while (tpw < 8 && slots % (2 * tpw) == 0 && max_seg * (slots / (2 * tpw)) >= 1024) tpw *= 2;
+  while (tpw < 8 && slots % (2 * tpw) == 0 && max_seg * (slots / (2 * tpw)) >= 512) tpw *= 2;
   const dim3 grid((unsigned)max_seg, (unsigned)((slots + tpw - 1) / tpw));
 #define MQ_GX(WPT, X, SB)                                                                    \
   if (nwt == WPT && xml == X && sbl == SB) {                                                  \
