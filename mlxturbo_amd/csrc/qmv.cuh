@@ -542,8 +542,26 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   }
 }
 
-// grid.x = ceil(N / (16 TJ)) workgroups of TJ tiles, block = 64 * NW threads,
-// dynamic LDS qmv_x_lds<BITS, GS, GPL>(NW, XM) (+ TJ qmv_sb_lds(K / GS) when
+// Workgroups of the skinny kernel.  By default one per 16 TJ rows.  When the
+// tiles do not divide evenly over the CUs, some CUs run one workgroup more
+// than others and finish last (K=5120 N=17408: 1088 tiles on 256 CUs, the
+// CUs holding 5 workgroups ended 1.3 us after those holding 4).  For one
+// streamed row the launch then spreads the rows evenly over R workgroups per
+// CU (1280 x 13.6 rows: 14.0 against 14.5 us), as long as a workgroup keeps
+// at least 13 of its 16 rows and R workgroups stay resident together.  The
+// grouping of rows never changes a row's arithmetic.
+inline unsigned qmv_grid(int64_t N, int TJ, int NW, int xm, int cus) {
+  const int64_t tiles = (N + 16 * TJ - 1) / (16 * TJ);
+  if (TJ == 1 && xm == 1 && cus > 0 && tiles % cus != 0) {
+    const int64_t R = (tiles + cus - 1) / cus;
+    if (R * NW <= 24 && N >= 13 * cus * R) return (unsigned)(cus * R);
+  }
+  return (unsigned)tiles;
+}
+
+// grid.x >= ceil(N / (16 TJ)) workgroups (qmv_grid), block = 64 * NW threads;
+// workgroup i owns rows [i N / grid, (i + 1) N / grid) as TJ tiles of <= 16.
+// Dynamic LDS qmv_x_lds<BITS, GS, GPL>(NW, XM) (+ TJ qmv_sb_lds(K / GS) when
 // SBL) bytes; M <= XM unless XM == 0, and then ((M - 1) * ldx + K) * 2 < 2^31.
 template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ>
 __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict__ x,
@@ -554,14 +572,15 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
                                                       int K, int64_t ldx, int64_t ldo) {
   extern __shared__ __align__(16) unsigned char qmv_smem[];
   __shared__ f32x4 red[NW * TJ][64];
-  const int n0 = blockIdx.x * 16 * TJ;
+  const int n0 = (int)((int64_t)blockIdx.x * N / gridDim.x);
+  const int n1 = (int)((int64_t)(blockIdx.x + 1) * N / gridDim.x);
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const uint32_t sRowB = (uint32_t)(K / GS) * 2;
   QmvTiles<TJ> tl;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int nj = n0 + 16 * j;
-    const int rj = min(16, N - nj);
+    const int rj = min(16, n1 - nj);
     const int64_t base = rj > 0 ? nj : 0;
     tl.w[j] = reinterpret_cast<const char*>(w) + base * rowB;
     tl.s[j] = reinterpret_cast<const char*>(scales) + base * sRowB;
@@ -588,8 +607,8 @@ inline int skinny_launch_one(const uint16_t* x, const uint32_t* w, const void* s
         (int)qmv_lds_bound<BITS, GS, C::GPL>(NW, XM, SBL, TJ));
     if (attr != hipSuccess) return (int)attr;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * TJ - 1) / (16 * TJ))), dim3(64 * NW), lds, st,
-                     x, w, (const uint16_t*)s, (const uint16_t*)b, out, M, (int)N, (int)K,
+  hipLaunchKernelGGL(kern, dim3(qmv_grid(N, TJ, NW, XM, device_cu_count())), dim3(64 * NW), lds,
+                     st, x, w, (const uint16_t*)s, (const uint16_t*)b, out, M, (int)N, (int)K,
                      (int64_t)K, (int64_t)N);
   return 0;
 }

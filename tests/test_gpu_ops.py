@@ -162,6 +162,24 @@ def test_qmm_rows_bit_identical_across_widths():
         np.testing.assert_array_equal(one[0], full[v])
 
 
+@pytest.mark.parametrize("N, K", [(3500, 1024), (17408, 5120)])
+def test_qmv_balanced_rows_match_tiles(N, K):
+    """One-row launches spread the rows evenly over the CUs when the 16-row
+    tiles do not divide over them (N=17408 on 256 CUs: 1280 workgroups of 13
+    or 14 rows; N=3500: 256 of 13-14).  Each row must be bit-identical to the
+    tiled launch of a two-row call, whose first row it is."""
+    rng = np.random.default_rng(11)
+    w, s, b = random_packed(rng, N, K)
+    x = act(rng, (2, K), scale=0.1)
+    args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    xd = to_dev(x, "bfloat16")
+    two = bits16(mq.quantized_matmul(xd, *args))
+    one = mq.quantized_matmul(xd[:1], *args)
+    np.testing.assert_array_equal(bits16(one)[0], two[0])
+    if N * K <= 4 << 20:
+        _check(one, O.quantized_matmul_ref(x[:1], w, s, b))
+
+
 def test_qmm_writes_every_element():
     """Output poisoned with NaN before the call; no element may stay NaN."""
     rng = np.random.default_rng(8)
