@@ -19,7 +19,10 @@ packed weights N*K*b/8 + scales and biases 2*2*N*K/64 + x 2*M*K + out 2*M*N.
 ``sweep`` reports the same measurement for configs 1, 2 (both shapes,
 M = 1..16) and 5 (8-bit lm_head); ``cpu_baseline`` times the C restatement
 of the oracle (oracle/qmm_oracle.c, OpenMP) on this host's cores over a
-bounded sample of the headline workload.
+bounded sample of the headline workload, and ``cpu_sweep`` does the same
+beside one case of each swept row family (skinny M=16, 8-bit lm_head, wide
+M=512, gather decode and prefill) on a slice of N or of the pairs, scaled
+to the whole call.
 """
 
 from __future__ import annotations
@@ -350,6 +353,76 @@ def cpu_baseline(N, K, seconds):
     }
 
 
+def cpu_rows(seconds):
+    """The C oracle beside each swept row family, on a bounded slice of the
+    same workload (a fraction of N, or of the pairs), timed for about
+    `seconds` and scaled to the whole call; units as in the GPU sweep."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import cref
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    rng = np.random.default_rng(5)
+
+    def timed(fn):
+        fn()                                              # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or reps >= 50:
+                return el / reps
+
+    def packed(N, K, bits, E=1):
+        w = rng.integers(0, 2**32, size=(E * N, K * bits // 32), dtype=np.uint64).astype(np.uint32)
+        s = np.full((E * N, K // 64), 0x3B00, np.uint16)
+        b = np.full((E * N, K // 64), 0xBC00, np.uint16)
+        return w, s, b
+
+    rows = {}
+    # dense skinny / wide / lm_head: a 1/frac slice of N, scaled back up
+    for key, (M, K, N, bits, frac, unit) in {
+            "b4_K5120_N17408_M16": (16, 5120, 17408, 4, 8, "GBps"),
+            "b8_K5120_N248320_M1": (1, 5120, 248320, 8, 16, "GBps"),
+            "b4_K5120_N17408_M512": (512, 5120, 17408, 4, 32, "TFLOPs")}.items():
+        n = N // frac
+        w, s, b = packed(n, K, bits)
+        x = np.full((M, K), 0x3F80, np.uint16)
+        us = timed(lambda: cref.qmm(x, w, s, b, 64, bits, threads=threads)) * frac * 1e6
+        r = {"us": round(us, 1), "sample": f"M={M} K={K} N={n} (1/{frac} of N), x{frac}"}
+        if unit == "GBps":
+            r["GBps"] = round(algo_bytes(M, N, K, bits) / us / 1e3, 3)
+        else:
+            r["TFLOPs"] = round(2.0 * M * N * K / us / 1e6, 4)
+        rows[key] = r
+    # MoE gather over the config-4 gate/up bank: decode T=8 (all 64 pairs) and
+    # prefill T=2048 (1/64 of the 16384 pairs), zipf routing
+    E, N, K = 512, 1024, 2048
+    w, s, b = packed(N, K, 4, E)
+    w, s, b = w.reshape(E, N, -1), s.reshape(E, N, -1), b.reshape(E, N, -1)
+    for key, (T, frac) in {"gather_gate_up_zipf_T8": (8, 1),
+                           "gather_prefill_gate_up_zipf_T2048": (2048, 64)}.items():
+        idx = zipf_routing(np.random.default_rng(4 + T), T, 8, E).reshape(-1)
+        P = idx.size // frac
+        rhs = np.ascontiguousarray(idx[:P])
+        lhs = np.arange(P, dtype=np.int32) // 8
+        x = np.full((T, 1, K), 0x3F80, np.uint16)
+        us = timed(lambda: cref.gather_qmm(x, w, s, b, lhs, rhs, 64, 4, threads=threads))
+        us *= frac * 1e6
+        U = len(np.unique(idx))
+        r = {"us": round(us, 1), "sample": f"{P} of {idx.size} pairs, x{frac}"}
+        if frac == 1:
+            byt = U * (N * K // 2 + 4 * N * (K // 64)) + 2 * T * K + 2 * idx.size * N
+            r["GBps"] = round(byt / us / 1e3, 3)
+        else:
+            r["TFLOPs"] = round(2.0 * idx.size * N * K / us / 1e6, 4)
+        rows[key] = r
+    return {"threads": threads, "kind": "port",
+            "what": "C oracle (oracle/qmm_oracle.c, OpenMP): exact bf16 dequant per weight, "
+                    "fp32 accumulation; gather loops over pairs as the reference's contract "
+                    "defines it",
+            "rows": rows}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -420,6 +493,7 @@ def main():
         sweep["dequant_b4_K5120_N17408"] = measure_dequant(torch, mq, N, K, 50, 3)
 
     cpu = None if args.no_cpu else cpu_baseline(N, K, args.cpu_seconds)
+    cpu_sweep = None if (args.no_cpu or args.no_sweep) else cpu_rows(2.0)
 
     line = {
         "metric": METRIC,
@@ -456,6 +530,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "cpu_sweep": cpu_sweep,
     }
     print(json.dumps(line), flush=True)
 

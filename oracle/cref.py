@@ -70,3 +70,22 @@ def qmm(x, w, s, b, group_size, bits, dtype="bfloat16", threads=0) -> np.ndarray
     if rc:
         raise ValueError(f"oracle_qmm rc={rc}")
     return out
+
+
+def gather_qmm(x, w, s, b, lhs, rhs, group_size, bits, dtype="bfloat16", threads=0) -> np.ndarray:
+    """x [B, M, K], w [E, N, Kw] -> out [P, M, N] float32 (C oracle's per-pair loop)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    lhs = np.ascontiguousarray(lhs, dtype=np.int32)
+    rhs = np.ascontiguousarray(rhs, dtype=np.int32)
+    B, M, K = x.shape
+    E, N = w.shape[0], w.shape[1]
+    P = rhs.shape[0]
+    out = np.empty((P, M, N), dtype=np.float32)
+    rc = lib().oracle_gather_qmm(_p(x), _p(w), _p(s), _p(b), _p(lhs), _p(rhs), _p(out), P, M, N,
+                                 K, E, B, group_size, bits, DTYPE_CODE[dtype], threads)
+    if rc:
+        raise ValueError(f"oracle_gather_qmm rc={rc}")
+    return out
