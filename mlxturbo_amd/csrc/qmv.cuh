@@ -543,18 +543,25 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
 }
 
 // Workgroups of the skinny kernel.  By default one per 16 TJ rows.  When the
-// tiles do not divide evenly over the CUs, some CUs run one workgroup more
-// than others and finish last (K=5120 N=17408: 1088 tiles on 256 CUs, the
-// CUs holding 5 workgroups ended 1.3 us after those holding 4).  For one
-// streamed row the launch then spreads the rows evenly over R workgroups per
-// CU (1280 x 13.6 rows: 14.0 against 14.5 us), as long as a workgroup keeps
-// at least 13 of its 16 rows and R workgroups stay resident together.  The
-// grouping of rows never changes a row's arithmetic.
+// workgroups do not divide evenly over the CUs, some CUs run one more than
+// others and finish last (K=5120 N=17408: 1088 tiles on 256 CUs, the CUs
+// holding 5 workgroups ended 1.3 us after those holding 4), or some CUs get
+// none (K=17408 N=5120 with two tiles per workgroup: 160 workgroups).  The
+// launch then spreads the rows evenly over R workgroups per CU, as long as R
+// workgroups stay resident together and the idle lanes of the partial tiles
+// cost less than the balance gains, which measurement put at: one streamed
+// row with at least 13 of 16 rows per workgroup (1280 x 13.6 rows: 14.0
+// against 14.5 us; 10 rows lost), and two tiles per workgroup with more than
+// one full tile (M=16, two boxes: 768 x 22.7 rows 21.5-21.7 against 22.7 us
+// at K=5120, 256 x 20 rows 23.2-23.3 against 24.7 us at K=17408; M=8 0-6%).
+// 2..4-row calls keep the default (balanced lost 0.3-0.6 us).  The grouping
+// of rows never changes a row's arithmetic.
 inline unsigned qmv_grid(int64_t N, int TJ, int NW, int xm, int cus) {
   const int64_t tiles = (N + 16 * TJ - 1) / (16 * TJ);
-  if (TJ == 1 && xm == 1 && cus > 0 && tiles % cus != 0) {
+  if (cus > 0 && tiles % cus != 0 && (xm == 1 || TJ == 2)) {
     const int64_t R = (tiles + cus - 1) / cus;
-    if (R * NW <= 24 && N >= 13 * cus * R) return (unsigned)(cus * R);
+    const bool enough = TJ == 1 ? N >= 13 * cus * R : N > 16 * cus * R;
+    if (R * NW <= 24 && enough) return (unsigned)(cus * R);
   }
   return (unsigned)tiles;
 }

@@ -162,22 +162,26 @@ def test_qmm_rows_bit_identical_across_widths():
         np.testing.assert_array_equal(one[0], full[v])
 
 
-@pytest.mark.parametrize("N, K", [(3500, 1024), (17408, 5120)])
+@pytest.mark.parametrize("N, K", [(3500, 1024), (17408, 5120), (5120, 17408)])
 def test_qmv_balanced_rows_match_tiles(N, K):
-    """One-row launches spread the rows evenly over the CUs when the 16-row
-    tiles do not divide over them (N=17408 on 256 CUs: 1280 workgroups of 13
-    or 14 rows; N=3500: 256 of 13-14).  Each row must be bit-identical to the
-    tiled launch of a two-row call, whose first row it is."""
+    """Launches spread the rows evenly over the CUs when the workgroups do not
+    divide over them: one-row calls (N=17408 on 256 CUs: 1280 workgroups of
+    13-14 rows; N=3500: 256 of 13-14) and two-tile calls of 8+ rows (N=17408:
+    768 workgroups of 22-23 rows; N=5120: 256 of 20).  Every row must be
+    bit-identical to the tiled launch of a two-row call."""
     rng = np.random.default_rng(11)
     w, s, b = random_packed(rng, N, K)
-    x = act(rng, (2, K), scale=0.1)
+    x = act(rng, (9, K), scale=0.1)
     args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
     xd = to_dev(x, "bfloat16")
-    two = bits16(mq.quantized_matmul(xd, *args))
+    two = bits16(mq.quantized_matmul(xd[:2], *args))
     one = mq.quantized_matmul(xd[:1], *args)
     np.testing.assert_array_equal(bits16(one)[0], two[0])
+    nine = bits16(mq.quantized_matmul(xd, *args))
+    np.testing.assert_array_equal(nine[:2], two)
     if N * K <= 4 << 20:
         _check(one, O.quantized_matmul_ref(x[:1], w, s, b))
+        _check(mq.quantized_matmul(xd, *args), O.quantized_matmul_ref(x, w, s, b))
 
 
 def test_qmm_writes_every_element():
