@@ -245,7 +245,16 @@ __host__ __device__ inline size_t gather_group_lds(int NWT, int XM, bool sbl, in
   return qmv_x_lds<BITS, GS, GPL>(NWT, XM) + (sbl ? TJ * qmv_sb_lds(G) : 0);
 }
 
-// grid = (segments upper bound, ceil(N / (16 * NW / NWT * tpw))); block 64 * NW.
+// 1-D grid, block 64 * NW.  Column slot = 16 * NW / NWT rows of N; once the
+// workgroup knows the number of segments it takes tpw = 1, 2, 4 or 8 slots
+// (doubled while more than wg_target workgroups would be busy; tpw divides
+// the slots of a segment) and workgroup i serves slots [i tpw, i tpw + tpw)
+// of the concatenated segments' slots; workgroups past the end return.
+// Consecutive workgroups are the slots of one segment, so idle workgroups
+// form a contiguous tail instead of holes spread over the CUs: workgroups
+// are placed on CUs in launch order, and with segments fastest the busy
+// ones of every slot landed on the same CUs (config-4 banks, zipf, 64
+// pairs: gate/up 22.4 -> 17.6 us, down 18.5 -> 13.8 us).
 // Segment = up to R pairs that share an expert (R * Mi <= 16 A rows); pairs
 // whose expert or x index is out of range form their own segments and get
 // zero outputs.  The workgroup's NW waves form NW / NWT groups of NWT waves;
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const uint32_t* __restrict__ w2, const uint16_t* __restrict__ scales2,
     const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
     const int32_t* __restrict__ rhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E, int R, int tpw) {
+    int P, int B, int Mi, int N, int K, int E, int R, int wg_target) {
   extern __shared__ __align__(16) unsigned char qmv_smem[];
   constexpr int TJ = GLU ? 2 : 1;
   __shared__ f32x4 red[NW * TJ][64];
@@ -275,9 +284,23 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   __shared__ int s_xbase[16];
   __shared__ int s_expert;
   __shared__ int s_found;
+  __shared__ int s_nseg;
   const int t = threadIdx.x;
   const int nt = blockDim.x;
-  const int seg = blockIdx.x;
+  constexpr int NG = NW / NWT;                 // tile groups per workgroup
+  const int nsl = (N + 16 * NG - 1) / (16 * NG);  // column slots of a segment
+  // Once the number of segments is known: tile rounds per workgroup (tpw),
+  // doubled while more than wg_target workgroups would be busy, and this
+  // workgroup's segment and first column slot (false: nothing to do).
+  int tpw = 1, seg = 0, slot = 0;
+  auto place = [&](int nseg) {
+    while (tpw < 8 && nsl % (2 * tpw) == 0 && nseg * (nsl / tpw) > wg_target) tpw *= 2;
+    const int64_t item = (int64_t)blockIdx.x * tpw;
+    if (item >= (int64_t)nseg * nsl) return false;
+    seg = (int)(item / nsl);
+    slot = (int)(item - (int64_t)seg * nsl);
+    return true;
+  };
   // key of a pair: its expert, or E when the expert or the x index is invalid
   auto key_of = [&](int p) {
     const int e = rhs[p];
@@ -297,9 +320,9 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     }
     const bool lead = lane < P && (cb % R) == 0;
     const uint64_t lmask = __builtin_amdgcn_ballot_w64(lead);
+    if (!place(__builtin_popcountll(lmask))) return;  // identical in every wave
     const int rank = __builtin_popcountll(lmask & ((1ull << lane) - 1ull));
     const uint64_t mine = __builtin_amdgcn_ballot_w64(lead && rank == seg);
-    if (mine == 0) return;                            // identical in every wave
     const int leader = __builtin_ctzll(mine);
     const int e = __builtin_amdgcn_readlane(key, leader);
     const int cb0 = __builtin_amdgcn_readlane(cb, leader);
@@ -315,7 +338,10 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     __syncthreads();
   } else if (ws == nullptr) {
     if (t < 16) s_members[t] = -1;
-    if (t == 0) s_found = 0;
+    if (t == 0) {
+      s_found = 0;
+      s_nseg = 0;
+    }
     // In-workgroup segment discovery (P <= kGatherFusedMaxP): pair p leads a
     // segment when the number of earlier pairs with its key is a multiple of
     // R; segments are numbered by leader position.
@@ -326,8 +352,10 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
       int cb = 0;
       for (int q = 0; q < p; ++q) cb += (s_key[q] == e);
       s_cb[p] = cb;
+      if (cb % R == 0) atomicAdd(&s_nseg, 1);
     }
     __syncthreads();
+    if (!place(s_nseg)) return;                       // uniform in the workgroup
     for (int p = t; p < P; p += nt) {
       if (s_cb[p] % R) continue;
       int rank = 0;
@@ -349,7 +377,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     }
     __syncthreads();
   } else {
-    if (seg >= ws[0]) return;
+    if (!place(ws[0])) return;
     const int32_t* perm = ws + 1;
     const int32_t* seg_start = perm + P;
     const int32_t* seg_len = seg_start + P;
@@ -370,10 +398,9 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     }
     __syncthreads();
   }
-  constexpr int NG = NW / NWT;                 // tile groups per workgroup
   const int e = __builtin_amdgcn_readfirstlane(s_expert);
   const int M = nmem * Mi;
-  const int nb = blockIdx.y * 16 * NG * tpw;
+  const int nb = slot * 16 * NG;
   if (e >= E) {
     // invalid pairs: zero rows
     const int cols = min(16 * NG * tpw, N - nb);
@@ -539,20 +566,32 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
     wsp = (const int32_t*)ws;
     *nlaunch += 1;
   }
-  // tile rounds per workgroup: enough rows per workgroup to amortize segment
-  // discovery while keeping ~512 workgroups or more (down bank T=8: 18.6 us
-  // with 4 rounds against 25.8 with 1)
+  // One workgroup per (segment bound, column slot); the kernel gives each
+  // busy workgroup 1, 2, 4 or 8 slots in turn so that at most ~3 per CU are
+  // busy, as it learns the number of distinct experts (config-4 banks, 64
+  // pairs: the best count was 490-670 busy workgroups for zipf and uniform
+  // routing alike: gate/up zipf 18.4 us with one slot each, uniform 22.8
+  // with two; down zipf 14.5 with two, uniform 17.9 with four).
+  // The grid covers the most workgroups any segment count can keep busy:
+  // wg_target, or the bound's slots at the largest round count.  Launching
+  // one workgroup per (bound, slot) instead cost the down bank 4 us (2048
+  // workgroups, most of them exiting after discovery).
   const int64_t slots = (N + 16 * ng - 1) / (16 * ng);
-  int tpw = 1;
-  while (tpw < 8 && slots % (2 * tpw) == 0 && max_seg * (slots / (2 * tpw)) >= 512) tpw *= 2;
-  const dim3 grid((unsigned)max_seg, (unsigned)((slots + tpw - 1) / tpw));
+  const int wg_target = 25 * device_cu_count() / 8;
+  int tpw_cap = 1;
+  while (tpw_cap < 8 && slots % (2 * tpw_cap) == 0) tpw_cap *= 2;
+  int64_t nwg = max_seg * slots / tpw_cap;
+  if (nwg < wg_target) nwg = wg_target;
+  if (nwg > max_seg * slots) nwg = max_seg * slots;
+  if (nwg > INT32_MAX) return kStatusUnsupported;
+  const dim3 grid((unsigned)nwg);
 #define MQ_GX(WPT, X, SB)                                                                    \
   if (nwt == WPT && xml == X && sbl == SB) {                                                  \
     hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, WPT, C::PF, X, SB, GLU>), \
                        grid, dim3(64 * C::NW), lds_for(X, WPT, SB), st, (const uint16_t*)x, w, \
                        (const uint16_t*)s, (const uint16_t*)b, w2, (const uint16_t*)s2,       \
                        (const uint16_t*)b2, lhs, rhs, (uint16_t*)out, wsp, (int)P, (int)B,    \
-                       (int)M, (int)N, (int)K, (int)E, R, tpw);                              \
+                       (int)M, (int)N, (int)K, (int)E, R, wg_target);                        \
   }
 #define MQ_GXW(WPT)                                                                          \
   MQ_GX(WPT, 0, true) MQ_GX(WPT, 1, true) MQ_GX(WPT, 2, true) MQ_GX(WPT, 4, true)            \
