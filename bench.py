@@ -16,6 +16,11 @@ duration, the denominator of ``roofline.achieved``.
 Algorithmic bytes per call (M rows, K, N, b bits, group 64, 16-bit T):
 packed weights N*K*b/8 + scales and biases 2*2*N*K/64 + x 2*M*K + out 2*M*N.
 
+``roofline`` carries two denominators: MI355X's published 8 TB/s (``peak``,
+``frac``) and a plain streaming read of the same byte count measured the
+same way on the same GPU (``measured_read``, ``frac_of_measured_read``;
+mlxturbo_amd/csrc/read_probe.hip, a measurement helper outside the ABI).
+
 ``sweep`` reports the same measurement for configs 1, 2 (both shapes,
 M = 1..16) and 5 (8-bit lm_head); ``cpu_baseline`` times the C restatement
 of the oracle (oracle/qmm_oracle.c, OpenMP) on this host's cores over a
@@ -302,6 +307,38 @@ def measure_dequant(torch, mq, N, K, steps, warmup):
     return {"us": round(per_step * 1e6, 2), "GBps": round(per / per_step / 1e9, 1)}
 
 
+def measure_stream_read(torch, nbytes, steps=200, warmup=10):
+    """The second roofline denominator: a plain streaming read of `nbytes`
+    (mlxturbo_amd/csrc/read_probe.hip, contiguous 16-byte loads, eight
+    workgroups per CU) over rotated copies that exceed the MALL, timed the
+    same way as the kernel (one HIP graph of `steps` launches).  What one
+    MI355X reads per second at this size, launch and ramp included."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "mlxturbo_amd",
+                                   "libmq_read_probe.so"))
+    lib.mq_read_probe.restype = ctypes.c_int
+    lib.mq_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
+                                  ctypes.c_void_p]
+    nbytes -= nbytes % 16
+    R = copies_for(nbytes)
+    bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(R)]
+    sink = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    wgs = 8 * torch.cuda.get_device_properties(0).multi_processor_count
+
+    def fn(i):
+        rc = lib.mq_read_probe(bufs[i % R].data_ptr(), nbytes, sink.data_ptr(), wgs,
+                               torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"mq_read_probe failed: {rc}")
+
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    del bufs
+    torch.cuda.empty_cache()
+    return {"us": round(per_step * 1e6, 2), "GBps": round(nbytes / per_step / 1e9, 1),
+            "bytes": nbytes, "how": "plain 16-byte loads, 8 workgroups per CU, rotated copies, "
+                                    "one HIP graph (mlxturbo_amd/csrc/read_probe.hip)"}
+
+
 def copy_probe(torch, nbytes, reps=4):
     """A plain device copy of known size, for calibrating rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters against the bytes actually moved."""
@@ -442,6 +479,7 @@ def main():
     head = measure_qmm(torch, mq, 1, N, K, 4, args.steps, args.warmup, args.copies)
     value = head["GBps"]
     ms_per_step = head["us"] * 1e-3
+    read = measure_stream_read(torch, head["bytes"])
 
     sweep = {}
     if not args.no_sweep:
@@ -527,6 +565,8 @@ def main():
             "traffic": recorded_traffic(),
             "kernel": "mq::qmv_kernel<bf16,4,64,...>",
             "avg_launch_us": round(head["us"], 3),
+            "measured_read": read,
+            "frac_of_measured_read": round(value / read["GBps"], 4),
         },
         "cpu_baseline": cpu,
         "sweep": sweep,

@@ -17,6 +17,9 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libmlxturbo_amd.so")
+# measurement helper for bench.py (a plain streaming read), not part of the ABI
+PROBE_SRC = os.path.join(CSRC, "read_probe.hip")
+PROBE_OUT = os.path.join(HERE, "libmq_read_probe.so")
 ARCH = os.environ.get("MQ_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (hipcc's host pass warns
@@ -60,6 +63,11 @@ def _filtered(stderr: str) -> str:
 def build(verbose: bool = False) -> str:
     compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
     with tempfile.TemporaryDirectory(prefix="mq_build_") as tmpdir:
+        probe_cmd = [hipcc(), *HIPCC_FLAGS, "-o", PROBE_OUT + ".tmp", PROBE_SRC]
+        if verbose:
+            print(" ".join(probe_cmd), flush=True)
+        probe = subprocess.Popen(probe_cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                 text=True)
         procs = []
         for i, (src, defs) in enumerate(UNITS):
             obj = os.path.join(tmpdir, f"unit{i}.o")
@@ -77,8 +85,12 @@ def build(verbose: bool = False) -> str:
             elif verbose and _filtered(err).strip():
                 print(_filtered(err), file=sys.stderr)
             objs.append(obj)
+        _, err = probe.communicate()
+        if probe.returncode != 0:
+            failed.append(f"{' '.join(probe_cmd)}\n{_filtered(err)}")
         if failed:
             raise RuntimeError("hipcc failed:\n" + "\n\n".join(failed))
+        os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
         tmp = OUT + ".tmp"
         cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
         if verbose:
