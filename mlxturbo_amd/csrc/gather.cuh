@@ -195,13 +195,14 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
   }
 }
 
-// One prep launch; its LDS can pass 64 KiB, so the limit is raised once.
+// One prep launch; its LDS can pass 64 KiB, so the limit is raised once per
+// device.
 inline int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, int64_t B,
                        int R, void* ws, hipStream_t st) {
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&gather_prep_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-      (int)gather_prep_lds(kPrepLdsKeys, kGatherPrepMaxE));
-  if (attr != hipSuccess) return (int)attr;
+  static std::atomic<uint64_t> lds_set{0};
+  if (hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(&gather_prep_kernel),
+                                      (int)gather_prep_lds(kPrepLdsKeys, kGatherPrepMaxE), lds_set))
+    return (int)e;
   hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), gather_prep_lds(P, E), st, rhs, lhs,
                      (int)P, (int)E, (int)B, R, (int32_t*)ws);
   return 0;
@@ -459,10 +460,11 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
                              const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
                              int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
                              hipStream_t st, int* nlaunch) {
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_grouped_kernel<DT, BITS, GS, BM>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds_bytes<BM>());
-  if (attr != hipSuccess) return (int)attr;
+  static std::atomic<uint64_t> lds_set{0};
+  if (hipError_t e = ensure_lds_limit(
+          reinterpret_cast<const void*>(&qmm_grouped_kernel<DT, BITS, GS, BM>),
+          (int)wide_lds_bytes<BM>(), lds_set))
+    return (int)e;
   const int R = (int)(BM / M);
   if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
   const int64_t bound = (P + R - 1) / R + E + 1;

@@ -58,6 +58,21 @@ struct GluLaunch {
 
 // ---- host-side routing and sizing ------------------------------------------
 
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per device (the attribute is held per device; `done` is the call site's
+// bit mask of devices already set).  Returns the HIP error of the first
+// failing attempt, which is retried on the next call.
+inline hipError_t ensure_lds_limit(const void* kern, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
+
 // Compute units of the current device, cached per device.
 inline int device_cu_count() {
   static std::atomic<int> cached[64];

@@ -363,10 +363,11 @@ template <int DT, int BITS, int GS, int BM>
 inline int wide_launch_bm(const void* x, const uint32_t* w, const void* s, const void* b,
                           void* out, int64_t M, int64_t N, int64_t K, int splits, void* ws,
                           hipStream_t st) {
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_wide_kernel<DT, BITS, GS, BM>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds_bytes<BM>());
-  if (attr != hipSuccess) return (int)attr;
+  static std::atomic<uint64_t> lds_set{0};
+  if (hipError_t e = ensure_lds_limit(
+          reinterpret_cast<const void*>(&qmm_wide_kernel<DT, BITS, GS, BM>),
+          (int)wide_lds_bytes<BM>(), lds_set))
+    return (int)e;
   float* part = splits > 1 ? static_cast<float*>(ws) : nullptr;
   const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)((M + BM - 1) / BM),
                   (unsigned)splits);

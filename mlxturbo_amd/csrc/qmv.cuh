@@ -601,7 +601,8 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
 }
 
 // One skinny launch of M <= 16 rows.  Launches above 64 KiB of dynamic LDS
-// (16 streamed rows with 8 waves) need the kernel's limit raised once.
+// (16 streamed rows with 8 waves) need the kernel's limit raised once per
+// device.
 template <int DT, int BITS, int GS, int NW, int XM, bool SBL, int TJ>
 inline int skinny_launch_one(const uint16_t* x, const uint32_t* w, const void* s, const void* b,
                              uint16_t* out, int M, int64_t N, int64_t K, size_t lds,
@@ -609,10 +610,11 @@ inline int skinny_launch_one(const uint16_t* x, const uint32_t* w, const void* s
   using C = QmvConf<BITS, GS>;
   auto kern = &qmv_kernel<DT, BITS, GS, C::GPL, NW, C::PF, XM, SBL, TJ>;
   if (lds > 65536) {
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)qmv_lds_bound<BITS, GS, C::GPL>(NW, XM, SBL, TJ));
-    if (attr != hipSuccess) return (int)attr;
+    static std::atomic<uint64_t> lds_set{0};
+    if (hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(kern),
+                                        (int)qmv_lds_bound<BITS, GS, C::GPL>(NW, XM, SBL, TJ),
+                                        lds_set))
+      return (int)e;
   }
   hipLaunchKernelGGL(kern, dim3(qmv_grid(N, TJ, NW, XM, device_cu_count())), dim3(64 * NW), lds,
                      st, x, w, (const uint16_t*)s, (const uint16_t*)b, out, M, (int)N, (int)K,
