@@ -469,7 +469,9 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
   if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
   const int64_t bound = (P + R - 1) / R + E + 1;
   const int64_t segs = bound < P ? bound : P;
-  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)segs);
+  const int64_t ntiles = (N + kWideBN - 1) / kWideBN * segs;
+  if (ntiles > INT32_MAX - 8) return kStatusUnsupported;
+  const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   hipLaunchKernelGGL((qmm_grouped_kernel<DT, BITS, GS, BM>), grid, dim3(kWideNT),
                      wide_lds_bytes<BM>(), st, (const uint16_t*)x, w, (const uint16_t*)s,
                      (const uint16_t*)b, lhs, (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B,
@@ -489,7 +491,9 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
   if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
   const int64_t bound = (P + R - 1) / R + E + 1;
   const int64_t segs = bound < P ? bound : P;
-  const dim3 grid((unsigned)((N + kWideBN - 1) / kWideBN), (unsigned)segs);
+  const int64_t ntiles = (N + kWideBN - 1) / kWideBN * segs;
+  if (ntiles > INT32_MAX - 8) return kStatusUnsupported;
+  const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2>), grid, dim3(kThinNT), 0, st,
                      (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,
                      (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K,

@@ -33,7 +33,8 @@ namespace mq {
 
 constexpr int kThinBM = 64, kThinNT = 256;
 
-// grid (ceil(N / 256), segment bound), 256 threads; segments of the prep
+// 1-D grid of ceil(N / 256) x segment bound workgroups (tiles placed by
+// grouped_tile), 256 threads; segments of the prep
 // tables in ws hold up to 64 / Mi pairs of one expert; pair p contributes
 // rows p*Mi .. p*Mi+Mi-1 and reads x batch lhs[p] (or p).  Segments of
 // out-of-range experts write zeros.  K % 64 == 0, B * Mi * K * 2 < 2^31.
@@ -50,8 +51,9 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
   __shared__ __align__(16) uint16_t As[2][BM * LD];
   __shared__ uint32_t s_xoff[BM];
   __shared__ int s_orow[BM];
-  const int seg = blockIdx.y, n0 = blockIdx.x * BN;
-  if (seg >= ws[0]) return;
+  int seg, col;
+  if (!grouped_tile(blockIdx.x, ws[0], (N + BN - 1) / BN, seg, col)) return;
+  const int n0 = col * BN;
   const int32_t* perm = ws + 1;
   const int st0 = perm[P + seg], len = perm[2 * P + seg];
   const int e = __builtin_amdgcn_readfirstlane(perm[3 * P + seg]);

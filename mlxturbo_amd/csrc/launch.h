@@ -73,6 +73,25 @@ inline hipError_t ensure_lds_limit(const void* kern, int bytes, std::atomic<uint
   return e;
 }
 
+// Expert-grouped tile of workgroup i (1-D grid), or false for a workgroup
+// with nothing to do.  Tiles are (segment, column tile) pairs, column tiles
+// fastest; nseg of the bound's segments exist.  Workgroups are dealt to the
+// eight XCDs (each with its own L2) in launch order, i on XCD i % 8, so XCD x
+// gets the contiguous tile range [x * per, (x + 1) * per): the column tiles
+// of a segment and the segments of one expert, which read the same x rows
+// and the same weights, then share an L2 instead of fetching them on every
+// XCD.  Busy workgroups are the first 8 * per of the grid.
+__device__ __forceinline__ bool grouped_tile(int i, int nseg, int ncol, int& seg, int& col) {
+  const int n = nseg * ncol;
+  const int per = (n + 7) / 8;
+  if (i >= 8 * per) return false;
+  const int tile = (i % 8) * per + i / 8;
+  if (tile >= n) return false;
+  seg = tile / ncol;
+  col = tile - seg * ncol;
+  return true;
+}
+
 // Compute units of the current device, cached per device.
 inline int device_cu_count() {
   static std::atomic<int> cached[64];

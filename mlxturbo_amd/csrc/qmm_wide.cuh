@@ -306,7 +306,8 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
 }
 
 // Expert-grouped rows (prefill gather_qmm, reference moe_grouped_gemm.py:
-// 913-1066): grid (ceil(N / 256), segment bound), 512 threads, dynamic LDS
+// 913-1066): 1-D grid of ceil(N / 256) x segment bound workgroups (tiles
+// placed by grouped_tile), 512 threads, dynamic LDS
 // wide_lds_bytes<BM>().  Segment s of the prep tables in ws holds up to BM / Mi
 // pairs of one expert (pairs sorted by expert); pair p contributes rows
 // p*Mi .. p*Mi+Mi-1 of the output and reads x batch lhs[p] (or p).  Segments
@@ -320,8 +321,9 @@ __global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
   extern __shared__ __align__(16) uint16_t wide_smem[];
   __shared__ uint32_t s_xoff[BM];
   __shared__ int s_orow[BM];
-  const int seg = blockIdx.y, n0 = blockIdx.x * kWideBN;
-  if (seg >= ws[0]) return;
+  int seg, col;
+  if (!grouped_tile(blockIdx.x, ws[0], (N + kWideBN - 1) / kWideBN, seg, col)) return;
+  const int n0 = col * kWideBN;
   const int32_t* perm = ws + 1;
   const int st0 = perm[P + seg], len = perm[2 * P + seg], e = perm[3 * P + seg];
   const int rows = len * Mi;                      // <= BM
