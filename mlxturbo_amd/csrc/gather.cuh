@@ -50,13 +50,21 @@ inline size_t gather_prep_lds(int64_t P, int64_t E) {
 // order (perm = identity): each key's run is read off its boundaries, with
 // no atomics; other orders are counting-sorted.  Internal linkage: every translation
 // unit that launches it has its own copy.
-static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t* __restrict__ rhs,
-                                                           const int32_t* __restrict__ lhs, int P,
-                                                           int E, int B, int R,
-                                                           int32_t* __restrict__ ws) {
+//
+// Segment sizes by class: an expert with c pairs is cut into segments of R2
+// pairs when R2 > 0 and c >= C2 (class 2), of R1 when R1 > 0 and c >= C1
+// (class 1), else of R0 (class 0).  The tables hold class 2's segments first,
+// then class 1's, then class 0's (each in key order); the header after them
+// (gather_ws_header) gives the class boundaries, ws[0] the total.
+static __global__ __launch_bounds__(1024) void gather_prep_kernel(
+    const int32_t* __restrict__ rhs, const int32_t* __restrict__ lhs, int P, int E, int B,
+    int R0, int R1, int C1, int R2, int C2, int32_t* __restrict__ ws) {
   extern __shared__ int sh[];
   const int NE = E + 1;  // bucket E collects out-of-range experts
   __shared__ int wtot[16];
+  __shared__ int ctot[3];
+  auto cls_of = [&](int c) { return (R2 > 0 && c >= C2) ? 2 : (R1 > 0 && c >= C1) ? 1 : 0; };
+  auto r_of = [&](int k) { return k == 2 ? R2 : k == 1 ? R1 : R0; };
   const int t = threadIdx.x;
   const int nt = blockDim.x;
   const int lane = t & 63, wv = t >> 6, nw = nt >> 6;
@@ -89,6 +97,7 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
   int32_t* seg_start = perm + P;
   int32_t* seg_len = seg_start + P;
   int32_t* seg_exp = seg_len + P;
+  int32_t* hdr = ws + gather_ws_header(P);
   // exclusive workgroup scan (sum, or max with identity -1) of one int per
   // thread: wave scans with cross-lane reads, then one wave over the totals
   auto wg_scan = [&](int v, bool is_max) {
@@ -119,6 +128,29 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
     return excl;
   };
 
+  // Segment numbering by class: thread-chunk counts ss[k] -> first segment
+  // id of the chunk in each class, in table order (class 2, 1, 0); thread 0
+  // writes the header and the total.
+  auto class_ids = [&](const int (&ss)[3], int (&sid)[3]) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) sid[k] = wg_scan(ss[k], false);
+    if (t == nt - 1) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) ctot[k] = sid[k] + ss[k];
+    }
+    __syncthreads();
+    const int start[3] = {ctot[2] + ctot[1], ctot[2], 0};
+#pragma unroll
+    for (int k = 0; k < 3; ++k) sid[k] += start[k];
+    if (t == 0) {
+      hdr[0] = 0;
+      hdr[1] = ctot[2];
+      hdr[2] = ctot[2] + ctot[1];
+      hdr[3] = ctot[2] + ctot[1] + ctot[0];
+      ws[0] = hdr[3];
+    }
+  };
+
   // ---- keys already in order: runs from their boundaries, no atomics --------
   bool ordered = true;
   for (int p = t + 1; p < P; p += nt) ordered &= key_at(p) >= key_at(p - 1);
@@ -135,21 +167,24 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
     __syncthreads();
     const int per = (NE + nt - 1) / nt;
     const int e0 = min(NE, t * per), e1 = min(NE, e0 + per);
-    int ss = 0;
+    int ss[3] = {0, 0, 0};
     for (int e = e0; e < e1; ++e) {
       const int c = base[e] >= 0 ? cur[e] - base[e] + 1 : 0;
-      ss += (c + R - 1) / R;
+      const int k = cls_of(c), R = r_of(k);
+      ss[k] += (c + R - 1) / R;
     }
-    int sid = wg_scan(ss, false);
+    int sid[3];
+    class_ids(ss, sid);
     for (int e = e0; e < e1; ++e) {
       const int c = base[e] >= 0 ? cur[e] - base[e] + 1 : 0;
-      for (int j = 0; j * R < c; ++j, ++sid) {
-        seg_start[sid] = base[e] + j * R;
-        seg_len[sid] = min(R, c - j * R);
-        seg_exp[sid] = e;
+      const int k = cls_of(c), R = r_of(k);
+      for (int j = 0; j * R < c; ++j) {
+        const int q = sid[k]++;
+        seg_start[q] = base[e] + j * R;
+        seg_len[q] = min(R, c - j * R);
+        seg_exp[q] = e;
       }
     }
-    if (t == nt - 1) ws[0] = sid;
     return;
   }
 
@@ -161,24 +196,27 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
   __syncthreads();
   for (int p = t; p < P; p += nt) atomicAdd(&cnt[key_at(p)], 1);
   __syncthreads();
-  // exclusive scans of cnt and ceil(cnt/R) over contiguous key chunks
+  // exclusive scans of cnt and of each class's segments over contiguous key
+  // chunks
   const int per = (NE + nt - 1) / nt;
   const int e0 = min(NE, t * per);
   const int e1 = min(NE, e0 + per);
-  int sc = 0, ss = 0;
+  int sc = 0, ss[3] = {0, 0, 0};
   for (int e = e0; e < e1; ++e) {
     sc += cnt[e];
-    ss += (cnt[e] + R - 1) / R;
+    const int k = cls_of(cnt[e]), R = r_of(k);
+    ss[k] += (cnt[e] + R - 1) / R;
   }
   int rc = wg_scan(sc, false);
-  int rs = wg_scan(ss, false);
+  int rs[3];
+  class_ids(ss, rs);
   for (int e = e0; e < e1; ++e) {
+    const int k = cls_of(cnt[e]), R = r_of(k);
     base[e] = rc;
-    segb[e] = rs;
+    segb[e] = rs[k];
     rc += cnt[e];
-    rs += (cnt[e] + R - 1) / R;
+    rs[k] += (cnt[e] + R - 1) / R;
   }
-  if (t == nt - 1) ws[0] = rs;
   __syncthreads();
   for (int p = t; p < P; p += nt) {
     const int k = key_at(p);
@@ -186,6 +224,7 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
   }
   for (int e = t; e < NE; e += nt) {
     const int c = cnt[e];
+    const int R = r_of(cls_of(c));
     for (int j = 0; j * R < c; ++j) {
       const int s = segb[e] + j;
       seg_start[s] = base[e] + j * R;
@@ -198,13 +237,14 @@ static __global__ __launch_bounds__(1024) void gather_prep_kernel(const int32_t*
 // One prep launch; its LDS can pass 64 KiB, so the limit is raised once per
 // device.
 inline int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, int64_t B,
-                       int R, void* ws, hipStream_t st) {
+                       int R, void* ws, hipStream_t st, int R1 = 0, int C1 = 0, int R2 = 0,
+                       int C2 = 0) {
   static std::atomic<uint64_t> lds_set{0};
   if (hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(&gather_prep_kernel),
                                       (int)gather_prep_lds(kPrepLdsKeys, kGatherPrepMaxE), lds_set))
     return (int)e;
   hipLaunchKernelGGL(gather_prep_kernel, dim3(1), dim3(1024), gather_prep_lds(P, E), st, rhs, lhs,
-                     (int)P, (int)E, (int)B, R, (int32_t*)ws);
+                     (int)P, (int)E, (int)B, R, R1, C1, R2, C2, (int32_t*)ws);
   return 0;
 }
 
@@ -452,30 +492,75 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   }
 }
 
-// Prefill gather_qmm: prep tables with segments of BM / M pairs, then the
-// expert-grouped MFMA tile kernel.  The row-tile height follows the expected
-// rows per expert (thin experts waste most of a tall tile).
+// One launch of the expert-grouped wide tile (BM rows) over the prep
+// tables' size class cls, whose segments number at most seg_bound.
 template <int DT, int BITS, int GS, int BM>
-inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, const void* b,
-                             const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
-                             int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
-                             hipStream_t st, int* nlaunch) {
+inline int launch_grouped_class(const void* x, const uint32_t* w, const void* s, const void* b,
+                                const int32_t* lhs, void* out, int64_t P, int64_t B, int64_t M,
+                                int64_t N, int64_t K, int64_t E, void* ws, int cls,
+                                int64_t seg_bound, hipStream_t st, int* nlaunch) {
   static std::atomic<uint64_t> lds_set{0};
   if (hipError_t e = ensure_lds_limit(
           reinterpret_cast<const void*>(&qmm_grouped_kernel<DT, BITS, GS, BM>),
           (int)wide_lds_bytes<BM>(), lds_set))
     return (int)e;
-  const int R = (int)(BM / M);
-  if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
-  const int64_t bound = (P + R - 1) / R + E + 1;
-  const int64_t segs = bound < P ? bound : P;
-  const int64_t ntiles = (N + kWideBN - 1) / kWideBN * segs;
-  if (ntiles > INT32_MAX - 8) return kStatusUnsupported;
+  const int64_t ntiles = (N + kWideBN - 1) / kWideBN * seg_bound;
   const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   hipLaunchKernelGGL((qmm_grouped_kernel<DT, BITS, GS, BM>), grid, dim3(kWideNT),
                      wide_lds_bytes<BM>(), st, (const uint16_t*)x, w, (const uint16_t*)s,
                      (const uint16_t*)b, lhs, (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B,
-                     (int)M, (int)N, (int)K, (int)E);
+                     (int)M, (int)N, (int)K, (int)E, cls);
+  *nlaunch += 1;
+  return 0;
+}
+
+// Segments of the pairs of a size class when experts with at least C pairs
+// are cut into segments of R pairs: at most P / R + P / C (one partial
+// segment per expert of the class) and never more than P.
+inline int64_t class_seg_bound(int64_t P, int64_t R, int64_t C, int64_t E) {
+  int64_t b = (P + R - 1) / R + (C > 0 ? P / C : E + 1);
+  if (b > E + 1 + (P + R - 1) / R) b = E + 1 + (P + R - 1) / R;
+  return b < P ? b : P;
+}
+
+// Prefill gather_qmm: prep tables, then the expert-grouped MFMA tile kernel.
+// One row-tile height for every expert (BM rows) when the expected rows per
+// expert call for it, or size classes: experts with 192+ rows get 256-row
+// tiles, 96+ rows 128-row tiles, the rest 64-row tiles, one launch per class
+// (zipf routing puts half the rows of config 4 in 27 experts).
+template <int DT, int BITS, int GS, int BM>
+inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, const void* b,
+                             const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
+                             int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
+                             hipStream_t st, int* nlaunch, bool classes) {
+  const int R = (int)(BM / M);
+  const int64_t ncol = (N + kWideBN - 1) / kWideBN;
+  if (ncol * (P + E + 1) > INT32_MAX - 8) return kStatusUnsupported;
+  if (!classes || M > 64) {
+    if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
+    *nlaunch += 1;
+    return launch_grouped_class<DT, BITS, GS, BM>(x, w, s, b, lhs, out, P, B, M, N, K, E, ws, 0,
+                                                  class_seg_bound(P, R, 0, E), st, nlaunch);
+  }
+  // classes (BM is the small tile, 64 rows): 128-row tiles from 96 rows per
+  // expert, 256-row tiles from 192, all in one launch
+  const int R1 = (int)(128 / M), C1 = (int)((96 + M - 1) / M);
+  const int R2 = (int)(256 / M), C2 = (int)((192 + M - 1) / M);
+  if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st, R1, C1, R2, C2)) return rc;
+  static std::atomic<uint64_t> lds_set{0};
+  if (hipError_t e = ensure_lds_limit(
+          reinterpret_cast<const void*>(&qmm_grouped_classes_kernel<DT, BITS, GS>),
+          (int)wide_lds_bytes<256>(), lds_set))
+    return (int)e;
+  int64_t nwg = 0;
+  for (const int64_t b : {class_seg_bound(P, R2, C2, E), class_seg_bound(P, R1, C1, E),
+                          class_seg_bound(P, R, 0, E)})
+    nwg += (b * ncol + 7) / 8 * 8;
+  if (nwg > INT32_MAX) return kStatusUnsupported;
+  hipLaunchKernelGGL((qmm_grouped_classes_kernel<DT, BITS, GS>), dim3((unsigned)nwg),
+                     dim3(kWideNT), wide_lds_bytes<256>(), st, (const uint16_t*)x, w,
+                     (const uint16_t*)s, (const uint16_t*)b, lhs, (uint16_t*)out,
+                     (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K, (int)E);
   *nlaunch += 2;
   return 0;
 }
@@ -489,15 +574,14 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
                                hipStream_t st, int* nlaunch) {
   const int R = (int)(kThinBM / M);
   if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
-  const int64_t bound = (P + R - 1) / R + E + 1;
-  const int64_t segs = bound < P ? bound : P;
+  const int64_t segs = class_seg_bound(P, R, 0, E);
   const int64_t ntiles = (N + kWideBN - 1) / kWideBN * segs;
   if (ntiles > INT32_MAX - 8) return kStatusUnsupported;
   const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2>), grid, dim3(kThinNT), 0, st,
                      (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,
                      (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K,
-                     (int)E);
+                     (int)E, 0);
   *nlaunch += 2;
   return 0;
 }
@@ -511,18 +595,19 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
   const int64_t rows_per_expert = P * M / (active > 0 ? active : 1);
   if (rows_per_expert >= 192)
     return launch_grouped_bm<DT, BITS, GS, 256>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
-                                                st, nlaunch);
+                                                st, nlaunch, false);
   if (rows_per_expert >= 96)
     return launch_grouped_bm<DT, BITS, GS, 128>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
-                                                st, nlaunch);
+                                                st, nlaunch, false);
   // thin experts: the register-B kernel wins on short K (config-4 down bank,
   // K=512: 201-209 against 265-270 us); at K=2048 the LDS-shared wide tile
-  // stays ahead with uniform routing (341-352 against 427 us)
+  // stays ahead with uniform routing (341-352 against 427 us), with taller
+  // tiles for the experts that turn out hot
   if (K <= 1024)
     return launch_grouped_thin<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
                                              nlaunch);
   return launch_grouped_bm<DT, BITS, GS, 64>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
-                                             nlaunch);
+                                             nlaunch, true);
 }
 
 // The streaming gather kernel over segments (GLU: fused gate+up+SiLU with the

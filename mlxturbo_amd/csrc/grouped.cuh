@@ -34,7 +34,7 @@ namespace mq {
 constexpr int kThinBM = 64, kThinNT = 256;
 
 // 1-D grid of ceil(N / 256) x segment bound workgroups (tiles placed by
-// grouped_tile), 256 threads; segments of the prep
+// grouped_tile), 256 threads; segments of size class cls of the prep
 // tables in ws hold up to 64 / Mi pairs of one expert; pair p contributes
 // rows p*Mi .. p*Mi+Mi-1 and reads x batch lhs[p] (or p).  Segments of
 // out-of-range experts write zeros.  K % 64 == 0, B * Mi * K * 2 < 2^31.
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E) {
+    int P, int B, int Mi, int N, int K, int E, int cls) {
   constexpr int BM = kThinBM, BN = kWideBN, BK = kWideBK, LD = kWideLD, NT = kThinNT;
   constexpr int WB = BITS / 4;                  // 16-byte loads per lane per block per step
   static_assert(GS >= 32, "a lane's 32 codes lie in one group");
@@ -51,8 +51,11 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
   __shared__ __align__(16) uint16_t As[2][BM * LD];
   __shared__ uint32_t s_xoff[BM];
   __shared__ int s_orow[BM];
+  const int32_t* hdr = ws + gather_ws_header(P);
+  const int s0 = hdr[2 - cls];
   int seg, col;
-  if (!grouped_tile(blockIdx.x, ws[0], (N + BN - 1) / BN, seg, col)) return;
+  if (!grouped_tile(blockIdx.x, hdr[3 - cls] - s0, (N + BN - 1) / BN, seg, col)) return;
+  seg += s0;
   const int n0 = col * BN;
   const int32_t* perm = ws + 1;
   const int st0 = perm[P + seg], len = perm[2 * P + seg];

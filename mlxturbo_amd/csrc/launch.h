@@ -196,8 +196,11 @@ constexpr int kGatherFusedMaxP = 256;
 constexpr int kGatherPrepMaxE = 2048;
 constexpr int64_t kGroupedMinRows = 1024;
 
-// Workspace (int32): [0] nseg | perm[P] | seg_start[P] | seg_len[P] | seg_expert[P]
-__host__ __device__ inline size_t gather_ws_words(int64_t P) { return 1 + 4 * (size_t)P; }
+// Workspace (int32): [0] nseg | perm[P] | seg_start[P] | seg_len[P] | seg_expert[P] |
+// header[4]: segments of size class 2 are [header[0], header[1]), class 1
+// [header[1], header[2]), class 0 [header[2], header[3]) (header[3] = nseg).
+__host__ __device__ inline size_t gather_ws_header(int64_t P) { return 1 + 4 * (size_t)P; }
+__host__ __device__ inline size_t gather_ws_words(int64_t P) { return gather_ws_header(P) + 4; }
 
 inline size_t gather_workspace_bytes(int64_t P, int64_t M) {
   if (P <= kGatherFusedMaxP && P * M < kGroupedMinRows) return 0;

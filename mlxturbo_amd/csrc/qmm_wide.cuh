@@ -305,25 +305,19 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
   }
 }
 
-// Expert-grouped rows (prefill gather_qmm, reference moe_grouped_gemm.py:
-// 913-1066): 1-D grid of ceil(N / 256) x segment bound workgroups (tiles
-// placed by grouped_tile), 512 threads, dynamic LDS
-// wide_lds_bytes<BM>().  Segment s of the prep tables in ws holds up to BM / Mi
-// pairs of one expert (pairs sorted by expert); pair p contributes rows
-// p*Mi .. p*Mi+Mi-1 of the output and reads x batch lhs[p] (or p).  Segments
-// of out-of-range experts write zeros.  B * Mi * K * 2 < 2^31.
+// One expert-grouped tile (prefill gather_qmm, reference moe_grouped_gemm.py:
+// 913-1066): segment seg of the prep tables in ws (up to BM / Mi pairs of one
+// expert, pairs sorted by expert) times the 256 columns from n0.  Pair p
+// contributes rows p*Mi .. p*Mi+Mi-1 of the output and reads x batch lhs[p]
+// (or p).  Segments of out-of-range experts write zeros.  s_xoff / s_orow
+// hold BM entries of LDS; B * Mi * K * 2 < 2^31.
 template <int DT, int BITS, int GS, int BM>
-__global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
+__device__ __forceinline__ void grouped_body(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E) {
-  extern __shared__ __align__(16) uint16_t wide_smem[];
-  __shared__ uint32_t s_xoff[BM];
-  __shared__ int s_orow[BM];
-  int seg, col;
-  if (!grouped_tile(blockIdx.x, ws[0], (N + kWideBN - 1) / kWideBN, seg, col)) return;
-  const int n0 = col * kWideBN;
+    int P, int B, int Mi, int N, int K, int E, int seg, int n0, uint16_t* wide_smem,
+    uint32_t* s_xoff, int* s_orow) {
   const int32_t* perm = ws + 1;
   const int st0 = perm[P + seg], len = perm[2 * P + seg], e = perm[3 * P + seg];
   const int rows = len * Mi;                      // <= BM
@@ -359,6 +353,67 @@ __global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
   };
   wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + wrow * K * BITS / 32, scales + wrow * G,
                               biases + wrow * G, ncols, K, 0, K / kWideBK, store, wide_smem);
+}
+
+// Expert-grouped tiles of one height over the prep tables' size class cls:
+// 1-D grid of ceil(N / 256) x the class's segment bound workgroups (tiles
+// placed by grouped_tile), 512 threads, dynamic LDS wide_lds_bytes<BM>().
+template <int DT, int BITS, int GS, int BM>
+__global__ __launch_bounds__(kWideNT) void qmm_grouped_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
+    int P, int B, int Mi, int N, int K, int E, int cls) {
+  extern __shared__ __align__(16) uint16_t wide_smem[];
+  __shared__ uint32_t s_xoff[BM];
+  __shared__ int s_orow[BM];
+  const int32_t* hdr = ws + gather_ws_header(P);
+  const int s0 = hdr[2 - cls];
+  int seg, col;
+  if (!grouped_tile(blockIdx.x, hdr[3 - cls] - s0, (N + kWideBN - 1) / kWideBN, seg, col)) return;
+  grouped_body<DT, BITS, GS, BM>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E, seg + s0,
+                                 col * kWideBN, wide_smem, s_xoff, s_orow);
+}
+
+// Expert-grouped tiles of all three size classes in one launch, so the tall
+// tiles of hot experts and the short ones of thin experts share the GPU
+// (three launches in a row left most CUs idle during the first two: config 4
+// gate/up zipf 446 us against 416 with 64-row tiles for all).  Workgroups
+// [0, 8 q2) run class 2 (256-row tiles), the next 8 q1 class 1 (128 rows),
+// the rest class 0 (64 rows); each class's tiles are placed by grouped_tile
+// (q = its tiles / 8, rounded up).  Grid: the sum of 8 q over the classes'
+// segment bounds; dynamic LDS wide_lds_bytes<256>() (one workgroup per CU,
+// as for every height).
+template <int DT, int BITS, int GS>
+__global__ __launch_bounds__(kWideNT) void qmm_grouped_classes_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
+    int P, int B, int Mi, int N, int K, int E) {
+  extern __shared__ __align__(16) uint16_t wide_smem[];
+  __shared__ uint32_t s_xoff[256];
+  __shared__ int s_orow[256];
+  const int32_t* hdr = ws + gather_ws_header(P);
+  const int ncol = (N + kWideBN - 1) / kWideBN;
+  int i = blockIdx.x, cls = 2;
+  for (; cls > 0; --cls) {
+    const int q = ((hdr[3 - cls] - hdr[2 - cls]) * ncol + 7) / 8;
+    if (i < 8 * q) break;
+    i -= 8 * q;
+  }
+  const int s0 = hdr[2 - cls];
+  int seg, col;
+  if (!grouped_tile(i, hdr[3 - cls] - s0, ncol, seg, col)) return;
+  seg += s0;
+  if (cls == 2)
+    grouped_body<DT, BITS, GS, 256>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E, seg,
+                                    col * kWideBN, wide_smem, s_xoff, s_orow);
+  else if (cls == 1)
+    grouped_body<DT, BITS, GS, 128>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E, seg,
+                                    col * kWideBN, wide_smem, s_xoff, s_orow);
+  else
+    grouped_body<DT, BITS, GS, 64>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E, seg,
+                                   col * kWideBN, wide_smem, s_xoff, s_orow);
 }
 
 template <int DT, int BITS, int GS, int BM>

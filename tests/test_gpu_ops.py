@@ -507,6 +507,37 @@ def test_gather_prefill_grouped(M, bits, gs):
     _check(out.reshape(T * top, M, N), ref)
 
 
+@pytest.mark.parametrize("M,bits,gs,sort", [(1, 4, 64, True), (1, 4, 64, False),
+                                             (2, 8, 64, True), (2, 4, 32, False)])
+def test_gather_prefill_size_classes(M, bits, gs, sort):
+    """Long K with few rows per expert on average: the prep tables cut each
+    expert by its own row count (256-row tiles from 192 rows, 128-row tiles
+    from 96, 64-row tiles below) and one grouped launch runs all classes.
+    Zipf routing over 48 experts gives all three classes (43 or 85 rows per
+    expert on average: below 96, where one tile height would serve all);
+    expert-sorted pairs (mlx-lm's _gather_sort) and shuffled ones; ragged N."""
+    rng = np.random.default_rng(90 + M + bits + gs)
+    E, N, K, T, top = 48, 300, 1088, 512, 4
+    banks = [quantized(rng, N, K, gs=gs, bits=bits) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    idx = zipf_routing(rng, T, top, E).reshape(-1).astype(np.int32)
+    counts = np.bincount(idx, minlength=E) * M
+    assert counts.max() >= 192 and ((counts >= 96) & (counts < 192)).any() and counts.min() < 96
+    x = act(rng, (T, 1, M, K))
+    xb = np.repeat(np.arange(T), top)
+    order = np.argsort(idx, kind="stable") if sort else rng.permutation(idx.size)
+    rhs, lhs = idx[order], xb[order]
+    n0 = mq.launch_count()
+    out = mq.gather_qmm(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                        to_dev(b, "bfloat16"), lhs_indices=torch.from_numpy(lhs.astype(np.int32)).cuda(),
+                        rhs_indices=torch.from_numpy(rhs).cuda(), group_size=gs, bits=bits,
+                        sorted_indices=sort)
+    assert mq.launch_count() - n0 == 2                 # prep + the grouped kernel
+    ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, lhs, rhs, gs, bits)
+    _check(out.reshape(idx.size, M, N), ref)
+
+
 @pytest.mark.parametrize("M,bits,gs,dtype", [(1, 4, 64, "bfloat16"), (2, 4, 32, "float16"),
                                               (3, 8, 64, "bfloat16"), (1, 8, 128, "float16"),
                                               (5, 4, 128, "bfloat16")])
