@@ -86,7 +86,7 @@ def run_case(torch, mq, case: str) -> dict:
         return {"case": case, **measure_combine(torch, mq, 2048, 8, 2048, 50, 3)}
     if case.startswith("wide"):
         M = int(case[4:])
-        r = measure_qmm(torch, mq, M, N, K, 4, 20, 3, copies=2)
+        r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 2048 else 100, 10, copies=2)
         tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
         return {"case": case, "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
                 "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
@@ -496,7 +496,7 @@ def main():
         # configs[2] (512/2048/8192) plus points across the bandwidth/compute
         # crossover (M ~ 95 at the MFMA ridge): HBM GB/s and TFLOP/s for each
         for M in (32, 96, 256, 512, 2048, 8192):
-            r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 512 else 100, 3, copies=2)
+            r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 2048 else 100, 3, copies=2)
             tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
             sweep[f"b4_K{K}_N{N}_M{M}"] = {
                 "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
@@ -506,7 +506,7 @@ def main():
         # the transposed (down-proj) shape at prefill widths: few column
         # tiles, K split over workgroups
         for M in (64, 512, 2048):
-            r = measure_qmm(torch, mq, M, K, N, 4, 20 if M >= 512 else 100, 3, copies=2)
+            r = measure_qmm(torch, mq, M, K, N, 4, 20 if M >= 2048 else 100, 3, copies=2)
             tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
             sweep[f"b4_K{N}_N{K}_M{M}"] = {
                 "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),

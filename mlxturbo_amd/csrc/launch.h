@@ -110,11 +110,12 @@ inline int device_cu_count() {
 // Launch plan of the wide kernel: row-tile height and K splits, the pair
 // with the fewest (rounds of one workgroup per CU; every height needs 92-147
 // KB of LDS) x (time of one tile), plus the split reduction.  Tile times at
-// K=5120, measured: 71 us (64 rows), 81 (128), 119 (256); a tile over a
-// K slice costs ~3 us plus its share.  A last round that fills few CUs costs
-// as much as a full one (K=5120 N=17408, 68 column tiles on 256 CUs: M=256
-// 81 us with BM 128 against 112 with 256; M=512 119 with 256 against 172 with
-// 128).  Splitting K serves narrow matrices, whose few column tiles leave
+// K=5120, measured: 71 us (64 rows), 81 (128), 105 (192), 119 (256); a tile
+// over a K slice costs ~3 us plus its share.  A last round that fills few CUs
+// costs as much as a full one (K=5120 N=17408, 68 column tiles on 256 CUs:
+// M=256 81 us with BM 128 against 112 with 256; M=512 113 with 192 against
+// 126 with 256 and 173 with 128; M=2048 362 with 192 against 406 with 256;
+// M=8192 1332 with 256 against 1515 with 192).  Splitting K serves narrow matrices, whose few column tiles leave
 // most CUs idle (K=17408 N=5120 has 20).  Partial planes are float [M, N]
 // per split, written by the tile kernel and summed in split order by a
 // reduce kernel: (8 S + 2) M N bytes at ~3.5 TB/s.
@@ -126,13 +127,13 @@ struct WidePlan {
 inline WidePlan wide_plan(int64_t M, int64_t N, int64_t K, int cus, int max_splits = 8) {
   const int64_t cols = (N + 255) / 256;
   const int64_t nk = K / 64;
-  const int bms[3] = {64, 128, 256};
-  const double tile_us[3] = {71.0, 81.0, 119.0};   // one tile at K=5120, measured
+  const int bms[4] = {64, 128, 192, 256};
+  const double tile_us[4] = {71.0, 81.0, 105.0, 119.0};   // one tile at K=5120, measured
   WidePlan best;
   bool first = true;
   for (int sp = 1; sp <= max_splits; sp *= 2) {
     if (sp > 1 && nk / sp < 8) break;                 // at least 8 k-steps per split
-    for (int i = 2; i >= 0; --i) {
+    for (int i = 3; i >= 0; --i) {
       const int64_t wgs = cols * ((M + bms[i] - 1) / bms[i]) * sp;
       const double tile = (sp > 1 ? 3.0 : 0.0) + tile_us[i] * ((double)K / sp) / 5120.0;
       double cost = (double)((wgs + cus - 1) / cus) * tile;

@@ -83,7 +83,7 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
   constexpr int XROWS = NT / 8;                 // tile rows between a thread's x chunks
   constexpr int CPC = 128 / BITS;               // codes per chunk
   constexpr int KS = BK / 16;                   // MFMA k-substeps per step
-  static_assert(XPT >= 1 && (XPT % KS == 0 || KS % XPT == 0), "x chunks spread over substeps");
+  static_assert(XPT >= 1 && (XPT % KS == 0 || XPT < KS), "x chunks spread over substeps");
   using T = T16<DT>;
   uint16_t* As = wide_smem;                     // [2][BM*LD]
   uint16_t* Bs = wide_smem + 2 * BM * LD;       // [2][BN*LD]
@@ -455,6 +455,7 @@ int WideLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* 
   switch (plan.bm) {
     case 64: return wide_launch_bm<DT, BITS, GS, 64>(x, w, s, b, out, M, N, K, splits, ws, st);
     case 128: return wide_launch_bm<DT, BITS, GS, 128>(x, w, s, b, out, M, N, K, splits, ws, st);
+    case 192: return wide_launch_bm<DT, BITS, GS, 192>(x, w, s, b, out, M, N, K, splits, ws, st);
     default: return wide_launch_bm<DT, BITS, GS, 256>(x, w, s, b, out, M, N, K, splits, ws, st);
   }
 }

@@ -297,12 +297,13 @@ def test_wide_split_k_narrow_matrix(cfg2_weights, M):
 
 # ------------------------------------------------- BASELINE config 3 (wide)
 
-@pytest.mark.parametrize("M", [40, 100, 300, 600, 512, 2048, 8192])
+@pytest.mark.parametrize("M", [40, 100, 300, 600, 512, 1100, 2048, 8192])
 def test_config3_wide(cfg2_weights, M):
     """Prefill widths through the MFMA tile kernel, full size; the oracle checks
     64 sampled rows x 512 sampled columns.  M=40 runs as 16-row skinny
-    launches, 100 / 300 / 600 pick tile heights 64 / 128 / 256 with a ragged
-    last row tile."""
+    launches; on 256 CUs 100 / 300 / 600 / 8192 pick tile heights 64 / 128 /
+    256 / 256 and 512 / 1100 / 2048 pick 192, all but 8192 with a ragged last
+    row tile."""
     K, N = 5120, 17408
     w, s, b, deq, dev = cfg2_weights[(K, N)]
     rng = np.random.default_rng(300 + M)
@@ -314,6 +315,24 @@ def test_config3_wide(cfg2_weights, M):
     ref = (O.bf16_to_f32(x[rows]).astype(np.float64) @ deq[cols].T).astype(np.float32)
     got = out[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()]
     _check(got, ref)
+
+
+@pytest.mark.parametrize("bits,gs,dtype,M", [(8, 64, "bfloat16", 2500), (4, 32, "float16", 2500),
+                                             (8, 128, "float16", 1600)])
+def test_wide_heights_other_formats(bits, gs, dtype, M):
+    """8-bit codes, fp16 and other group sizes at widths whose plan takes the
+    taller tiles (K=1024 N=8192, 32 column tiles: on 256 CUs M=2500 runs 14
+    rows of 192, M=1600 seven rows of 256); 96 sampled rows, all columns."""
+    rng = np.random.default_rng(70 + bits + gs + M)
+    N, K = 8192, 1024
+    w, s, b = quantized(rng, N, K, gs, bits, dtype)
+    x = act(rng, (M, K), dtype)
+    out = mq.quantized_matmul(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
+                              group_size=gs, bits=bits)
+    rows = np.sort(np.concatenate([rng.choice(M, size=88, replace=False), np.arange(M - 8, M)]))
+    rows = np.unique(rows)
+    ref = O.quantized_matmul_ref(x[rows], w, s, b, gs, bits, dtype)
+    _check(out[torch.from_numpy(rows).cuda()], ref, dtype)
 
 
 @pytest.mark.parametrize("bits,gs,dtype", [(4, 64, "bfloat16"), (8, 64, "bfloat16"),
