@@ -60,12 +60,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_rsrc(const void* base, in
                                            0x00020000);
 }
 
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 // One BM x 256 output tile over k-steps kt0 .. kt0 + nkl - 1 (64 codes each).
 // x rows come from xrsrc at per-row byte offsets xrow_off(r) (past the range
 // for rows that do not exist); w / scales / biases point at the tile's first
 // weight row, of which nrows (<= 256) exist; store(r, c, v) receives the
 // float sum of row r, tile column c (< nrows).
-template <int DT, int BITS, int GS, int BM, class XRowOff, class Store>
+// FRESH: the caller's tiles do not share weight tiles through L2 (grouped
+// segments), which enables per-block scale loads below.
+template <int DT, int BITS, int GS, int BM, class XRowOff, class Store, bool FRESH = false>
 __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff xrow_off,
                                           const uint32_t* __restrict__ w,
                                           const uint16_t* __restrict__ scales,
@@ -125,6 +136,38 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
     uint16_t s[WPT], b[WPT];
   };
   Set S0, S1;
+  // Scales and biases, 64- and 128-row tiles of weights that no other tile
+  // reads through L2 (on dense tiles it cost 1.5-4%), K / GS a multiple of 8,
+  // both arrays 16-byte aligned and whose k range is whole blocks of SPB
+  // steps: each thread loads the 16-byte block (8 groups) of its rows'
+  // scales and biases with the block's first step (ns / nb) and takes it
+  // over (cs / cb) when that step is stored, instead of two 2-byte loads
+  // per step; the loop is unrolled over a block so every block load and
+  // every group index is fixed at compile time.  A tile streaming fresh
+  // weights (a thin expert) spends ~15% of its time on the per-step
+  // requests at K = 2048.
+  constexpr int SPB = GS / 8;                   // 64-code steps per block
+  constexpr bool SBLK = FRESH && BM <= 128 && SPB >= 4 && SPB <= 8;
+  const bool sblk = SBLK && G % 8 == 0 && kt0 % SPB == 0 && nk % SPB == 0 &&
+                    ((uintptr_t)scales | (uintptr_t)biases) % 16 == 0;
+  u32x4 ns[WPT], nb[WPT], cs[WPT], cb[WPT];
+  auto bload = [&](int kt) {
+    const uint32_t bo = 16u * (uint32_t)((kt0 + kt) * BK / GS / 8);
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      ns[i] = __builtin_amdgcn_raw_buffer_load_b128(rsd, so[i] + bo, 0, 0);
+      nb[i] = __builtin_amdgcn_raw_buffer_load_b128(rbd, so[i] + bo, 0, 0);
+    }
+  };
+  auto gload_w = [&](Set& st, int kt) {
+    const int k0 = (kt0 + kt) * BK;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i)
+      st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, xo[i], k0 * 2, 0);
+#pragma unroll
+    for (int i = 0; i < WPT; ++i)
+      st.wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rwd, wo[i], k0 * BITS / 8, 0);
+  };
   auto gload = [&](Set& st, int kt) {
     const int k0 = (kt0 + kt) * BK;
 #pragma unroll
@@ -139,7 +182,9 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
     }
   };
   // part ks of storing register stage st into LDS buffer buf
-  auto spart = [&](const Set& st, int buf, int ks, auto plainc) {
+  // LB >= 0: step LB of an aligned block, scales from cs / cb
+  auto spart = [&](const Set& st, int buf, int ks, auto plainc, auto lbc) {
+    constexpr int LB = decltype(lbc)::value;
     constexpr bool PLAIN = decltype(plainc)::value;
     uint16_t* A = As + buf * BM * LD;
     uint16_t* B = Bs + buf * BN * LD;
@@ -154,7 +199,19 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
 #pragma unroll
     for (int q = ks * WW / KS; q < (ks + 1) * WW / KS; ++q) {
       const int i = q / 4, j = q % 4;
-      const GroupScale g = make_group(T::to_f32(st.s[i]), T::to_f32(st.b[i]));
+      uint16_t s16, b16;
+      if constexpr (LB >= 0) {
+        // group of this chunk within the block (a constant for GS >= 64)
+        const int e = GS >= BK ? LB * BK / GS % 8 : (LB * BK + wch[i] * CPC) / GS % 8;
+        const uint32_t ws = (e & 4) ? ((e & 2) ? cs[i][3] : cs[i][2]) : ((e & 2) ? cs[i][1] : cs[i][0]);
+        const uint32_t wb = (e & 4) ? ((e & 2) ? cb[i][3] : cb[i][2]) : ((e & 2) ? cb[i][1] : cb[i][0]);
+        s16 = (uint16_t)((e & 1) ? ws >> 16 : ws);
+        b16 = (uint16_t)((e & 1) ? wb >> 16 : wb);
+      } else {
+        s16 = st.s[i];
+        b16 = st.b[i];
+      }
+      const GroupScale g = make_group(T::to_f32(s16), T::to_f32(b16));
       uint32_t o[CPC / 8];
       if constexpr (PLAIN) deq_word_plain<DT, BITS>(st.wv[i][j], g, o);
       else deq_word<DT, BITS>(st.wv[i][j], g, o);
@@ -204,8 +261,49 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
   auto run = [&](auto plainc) {
     auto stage_store = [&](const Set& st, int buf) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) spart(st, buf, ks, plainc);
+      for (int ks = 0; ks < KS; ++ks) spart(st, buf, ks, plainc, std::integral_constant<int, -1>{});
     };
+    // step LB of an aligned block; its first step takes over the block loaded
+    auto stage_store_b = [&](const Set& st, int buf, auto lbc) {
+      if constexpr (decltype(lbc)::value == 0) {
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) {
+          cs[i] = ns[i];
+          cb[i] = nb[i];
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) spart(st, buf, ks, plainc, lbc);
+    };
+    if constexpr (SBLK) {
+      if (sblk) {
+        gload_w(S0, 0);
+        bload(0);
+        gload_w(S1, 1);
+        stage_store_b(S0, 0, std::integral_constant<int, 0>{});
+        __syncthreads();
+        // Each pass runs one block (SPB steps, an even number); the loads
+        // for steps past the end reload step nk - 1 (valid memory, unused).
+        for (int kb = 0; kb < nk; kb += SPB) {
+          static_for<0, SPB / 2>([&](auto hc) {
+            constexpr int h = decltype(hc)::value;
+            constexpr bool next = 2 * h + 2 == SPB;   // step kb + 2h + 2 opens a block
+            // buffer 0 holds step kb + 2h, S1 step kb + 2h + 1, S0 is free
+            gload_w(S0, min(kb + 2 * h + 2, nk - 1));
+            if constexpr (next) bload(min(kb + SPB, nk - SPB));
+            mma(0);
+            stage_store_b(S1, 1, std::integral_constant<int, 2 * h + 1>{});
+            __syncthreads();
+            // buffer 1 holds step kb + 2h + 1, S0 step kb + 2h + 2, S1 is free
+            gload_w(S1, min(kb + 2 * h + 3, nk - 1));
+            mma(1);
+            stage_store_b(S0, 0, std::integral_constant<int, (2 * h + 2) % SPB>{});
+            __syncthreads();
+          });
+        }
+        return;
+      }
+    }
     gload(S0, 0);
     gload(S1, min(1, nk - 1));
     stage_store(S0, 0);
@@ -351,8 +449,9 @@ __device__ __forceinline__ void grouped_body(
     const int o = s_orow[r];
     if (o >= 0) ot[(int64_t)o * N + c] = T16<DT>::round1(v);
   };
-  wide_tile<DT, BITS, GS, BM>(xr, xrow_off, w + wrow * K * BITS / 32, scales + wrow * G,
-                              biases + wrow * G, ncols, K, 0, K / kWideBK, store, wide_smem);
+  wide_tile<DT, BITS, GS, BM, decltype(xrow_off), decltype(store), true>(
+      xr, xrow_off, w + wrow * K * BITS / 32, scales + wrow * G, biases + wrow * G, ncols, K, 0,
+      K / kWideBK, store, wide_smem);
 }
 
 // Expert-grouped tiles of one height over the prep tables' size class cls:

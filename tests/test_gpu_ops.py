@@ -557,6 +557,31 @@ def test_gather_prefill_size_classes(M, bits, gs, sort):
     _check(out.reshape(idx.size, M, N), ref)
 
 
+@pytest.mark.parametrize("bits,gs,dtype", [(4, 32, "float16"), (8, 64, "bfloat16"),
+                                           (8, 32, "bfloat16"), (4, 128, "bfloat16")])
+def test_gather_prefill_scale_blocks(bits, gs, dtype):
+    """K / gs a multiple of 8 (K=2048): the 64- and 128-row grouped tiles
+    read scales and biases in 16-byte blocks of 8 groups, one load per block
+    (group 32: two groups per step, the group index differs across a row's
+    chunks; group 128: per-step loads, the block would span 16 steps).
+    Ragged N, zipf routing, full oracle."""
+    rng = np.random.default_rng(90 + bits + gs)
+    E, N, K, T, top = 32, 264, 2048, 384, 4
+    banks = [quantized(rng, N, K, gs=gs, bits=bits, dtype=dtype) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    idx = zipf_routing(rng, T, top, E).astype(np.int32)
+    x = act(rng, (T, 1, 1, K), dtype)
+    n0 = mq.launch_count()
+    out = mq.gather_qmm(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
+                        rhs_indices=torch.from_numpy(idx).cuda(), group_size=gs, bits=bits)
+    assert mq.launch_count() - n0 == 2                 # prep + the grouped kernel
+    ref = O.gather_qmm_ref(x.reshape(T, 1, K), w, s, b, np.repeat(np.arange(T), top),
+                           idx.reshape(-1), gs, bits, dtype)
+    res = O.check_output(from_dev(out).reshape(T * top, 1, N), ref, dtype)
+    assert res["ok"], res
+
+
 @pytest.mark.parametrize("M,bits,gs,dtype", [(1, 4, 64, "bfloat16"), (2, 4, 32, "float16"),
                                               (3, 8, 64, "bfloat16"), (1, 8, 128, "float16"),
                                               (5, 4, 128, "bfloat16")])
