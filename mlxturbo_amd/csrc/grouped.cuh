@@ -115,7 +115,26 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
     u32x4 wv[2][WB];
     uint16_t s[2], b[2];
   };
-  auto gload = [&](Stage& st, int kt) {
+  // Scales and biases in 16-byte blocks of 8 groups, one load per block,
+  // when K / GS is a multiple of 8 and the arrays are 16-byte aligned (the
+  // scheme and its measurements are those of wide_tile's FRESH tiles): the
+  // loop below is unrolled over a block so each block load and group index
+  // is a compile-time position.
+  constexpr int SPB = GS / 8;                   // 64-code steps per block
+  constexpr bool SBLK = SPB >= PS && SPB <= 8 && SPB % PS == 0;
+  const bool sblk = SBLK && G % 8 == 0 && nk % SPB == 0 &&
+                    ((uintptr_t)scales | (uintptr_t)biases) % 16 == 0;
+  u32x4 ns[2], nb[2], cs[2], cb[2];
+  auto bload = [&](int kt) {
+    const uint32_t bo = 16u * (uint32_t)(kt * BK / GS / 8);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      ns[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, so[j] + bo, 0, 0);
+      nb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, so[j] + bo, 0, 0);
+    }
+  };
+  // per_step: also load this step's scale and bias (no block path)
+  auto gload = [&](Stage& st, int kt, bool per_step) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -125,9 +144,11 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
 #pragma unroll
       for (int q = 0; q < WB; ++q)
         st.wv[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[j] + 16u * q, k0 * BITS / 8, 0);
-      const uint32_t go = so[j] + 2u * (uint32_t)((k0 + 32 * h) / GS);
-      st.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
-      st.b[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+      if (per_step) {
+        const uint32_t go = so[j] + 2u * (uint32_t)((k0 + 32 * h) / GS);
+        st.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
+        st.b[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+      }
     }
   };
   auto store_x = [&](const Stage& st, int buf) {
@@ -146,12 +167,22 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
 
   // One k-step: dequantize codes 8 ks .. 8 ks + 7 of the lane's 32 (B of MFMA
   // ks, per 32-column block) and multiply with the x rows in LDS buffer buf.
-  auto step = [&](const Stage& st, int buf) {
+  // LB >= 0: step LB of an aligned block, scales from cs / cb
+  auto step = [&](const Stage& st, int buf, auto lbc) {
+    constexpr int LB = decltype(lbc)::value;
     GroupScale g[2];
     bool big = false;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      g[j] = make_group(T::to_f32(st.s[j]), T::to_f32(st.b[j]));
+      uint16_t s16 = st.s[j], b16 = st.b[j];
+      if constexpr (LB >= 0) {
+        const int e = GS >= BK ? LB * BK / GS % 8 : (LB * BK + 32 * h) / GS % 8;
+        const uint32_t w1 = (e & 4) ? ((e & 2) ? cs[j][3] : cs[j][2]) : ((e & 2) ? cs[j][1] : cs[j][0]);
+        const uint32_t w2 = (e & 4) ? ((e & 2) ? cb[j][3] : cb[j][2]) : ((e & 2) ? cb[j][1] : cb[j][0]);
+        s16 = (uint16_t)((e & 1) ? w1 >> 16 : w1);
+        b16 = (uint16_t)((e & 1) ? w2 >> 16 : w2);
+      }
+      g[j] = make_group(T::to_f32(s16), T::to_f32(b16));
       big |= needs_plain(g[j].s);
     }
     const bool plain = __builtin_amdgcn_ballot_w64(big) != 0;
@@ -188,24 +219,54 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
   };
 
   Stage S[PS];
+  if (sblk) {
+    if constexpr (SBLK) {
+      // nk >= SPB >= PS
 #pragma unroll
-  for (int i = 0; i < PS; ++i) gload(S[i], min(i, nk - 1));
-  store_x(S[0], 0);
-  __syncthreads();
-  // At step k: LDS buffer k & 1 holds x of step k; S[k % PS] holds step k's
-  // weights and is reloaded with step k + PS once they are multiplied;
-  // S[(k + i) % PS] holds step k + i.  The body is unrolled over lcm(PS, 2)
-  // steps so stage and buffer indices are constants; the last steps reload
-  // step nk - 1 (valid memory, unused), so the loads need no conditions.
-  constexpr int U = PS % 2 ? 2 * PS : PS;
-  for (int kt = 0; kt < nk; kt += U) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (u > 0 && kt + u >= nk) break;         // uniform
-      step(S[u % PS], u & 1);
-      gload(S[u % PS], min(kt + u + PS, nk - 1));
-      store_x(S[(u + 1) % PS], (u + 1) & 1);
+      for (int i = 0; i < PS; ++i) gload(S[i], i, false);
+      bload(0);
+      store_x(S[0], 0);
       __syncthreads();
+      // step u of a block: as the loop below, and the block of step kt + SPB
+      // is loaded with step kt + SPB's weights (PS steps ahead)
+      for (int kt = 0; kt < nk; kt += SPB) {
+        static_for<0, SPB>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          if constexpr (u == 0) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              cs[j] = ns[j];
+              cb[j] = nb[j];
+            }
+          }
+          step(S[u % PS], u & 1, uc);
+          gload(S[u % PS], min(kt + u + PS, nk - 1), false);
+          if constexpr (u + PS == SPB) bload(min(kt + SPB, nk - SPB));
+          store_x(S[(u + 1) % PS], (u + 1) & 1);
+          __syncthreads();
+        });
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < PS; ++i) gload(S[i], min(i, nk - 1), true);
+    store_x(S[0], 0);
+    __syncthreads();
+    // At step k: LDS buffer k & 1 holds x of step k; S[k % PS] holds step k's
+    // weights and is reloaded with step k + PS once they are multiplied;
+    // S[(k + i) % PS] holds step k + i.  The body is unrolled over lcm(PS, 2)
+    // steps so stage and buffer indices are constants; the last steps reload
+    // step nk - 1 (valid memory, unused), so the loads need no conditions.
+    constexpr int U = PS % 2 ? 2 * PS : PS;
+    for (int kt = 0; kt < nk; kt += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u > 0 && kt + u >= nk) break;         // uniform
+        step(S[u % PS], u & 1, std::integral_constant<int, -1>{});
+        gload(S[u % PS], min(kt + u + PS, nk - 1), true);
+        store_x(S[(u + 1) % PS], (u + 1) & 1);
+        __syncthreads();
+      }
     }
   }
 

@@ -557,16 +557,18 @@ def test_gather_prefill_size_classes(M, bits, gs, sort):
     _check(out.reshape(idx.size, M, N), ref)
 
 
-@pytest.mark.parametrize("bits,gs,dtype", [(4, 32, "float16"), (8, 64, "bfloat16"),
-                                           (8, 32, "bfloat16"), (4, 128, "bfloat16")])
-def test_gather_prefill_scale_blocks(bits, gs, dtype):
-    """K / gs a multiple of 8 (K=2048): the 64- and 128-row grouped tiles
-    read scales and biases in 16-byte blocks of 8 groups, one load per block
-    (group 32: two groups per step, the group index differs across a row's
-    chunks; group 128: per-step loads, the block would span 16 steps).
-    Ragged N, zipf routing, full oracle."""
-    rng = np.random.default_rng(90 + bits + gs)
-    E, N, K, T, top = 32, 264, 2048, 384, 4
+@pytest.mark.parametrize("bits,gs,dtype,K", [(4, 32, "float16", 2048), (8, 64, "bfloat16", 2048),
+                                             (8, 32, "bfloat16", 2048), (4, 128, "bfloat16", 2048),
+                                             (4, 64, "bfloat16", 512), (8, 32, "float16", 512)])
+def test_gather_prefill_scale_blocks(bits, gs, dtype, K):
+    """K / gs a multiple of 8: the grouped tiles (64/128-row wide tiles at
+    K=2048, the thin kernel at K=512) read scales and biases in 16-byte
+    blocks of 8 groups, one load per block (group 32: two groups per step,
+    the group index differs across a row's chunks; group 128: per-step
+    loads, the block would span 16 steps).  Ragged N, zipf routing, full
+    oracle."""
+    rng = np.random.default_rng(90 + bits + gs + K)
+    E, N, T, top = 32, 264, 384, 4
     banks = [quantized(rng, N, K, gs=gs, bits=bits, dtype=dtype) for _ in range(E)]
     w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
     b = np.stack([t[2] for t in banks])
