@@ -5,7 +5,8 @@ Metric: 4-bit qmv/qmm achieved HBM GB/s (% of peak) and
 decode qmv): one *step* is one quantized_matmul call over one of R rotated
 copies of the 4-bit weights (R copies exceed the 256 MB Infinity Cache, so
 every step streams its weights from HBM -- the reference's own "cold chain"
-rule, CLAUDE.md:13-16).  Inputs are resident in HBM before timing starts.
+rule, the reference's CLAUDE.md:13-16).  Inputs are resident in HBM before
+timing starts.
 
 Timing: the K timed steps are captured in one HIP graph on a dedicated
 stream; HIP events recorded on that same stream bracket one replay, with
