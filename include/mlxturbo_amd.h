@@ -56,10 +56,28 @@ uint64_t mq_launch_count(void);
  * Replaces mx.dequantize(w, scales, biases, group_size, bits, mode="affine"),
  * the format definer the reference's fp32 references call
  * (bench/test_qmm_wide_shapes.py:35-42, kernels/moe_verify_gather.py:932).
- * bits in {4, 8}; group_size in {32, 64, 128}; dtype any of the three.
+ * bits in {2, 3, 4, 5, 6, 8} (a row is a little-endian bitstream of K codes:
+ * kernels/_steel_flat.py:1158-1167, 1184-1254); group_size in {32, 64, 128};
+ * dtype any of the three; w and out 16-byte aligned.
  */
 int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, void* out,
                   int64_t N, int64_t K, int group_size, int bits, int dtype, void* hip_stream);
+
+/*
+ * (wq, scales, biases) = quantize(w): MLX affine quantization of w[N, K]
+ * (dtype T) into wq uint32 [N, K*bits/32] and scales/biases T [N, K/group_size].
+ * Replaces mx.quantize(w, group_size, bits, mode="affine") as the reference
+ * calls it at runtime (mlxturbo/rebit.py:119 requantizing a layer,
+ * spec.py:428) and in its tests (kernels/moe_verify_gather.py:887).  Per
+ * group, in float32: scale = max((max-min)/(2^bits-1), 1e-7), negative unless
+ * |min| > |max|, snapped so the larger-magnitude edge is a code (scale =
+ * edge / round(edge/scale) unless that rounds to 0); bias = that edge (0 when
+ * it rounded to 0); code = clamp(round_half_even((w-bias)/scale)), NaN -> 0.
+ * bits in {2, 3, 4, 5, 6, 8}; group_size in {32, 64, 128}; w and wq 16-byte
+ * aligned (scales/biases too for 16-bit T).
+ */
+int mq_quantize(const void* w, uint32_t* wq, void* scales, void* biases, int64_t N, int64_t K,
+                int group_size, int bits, int dtype, void* hip_stream);
 
 /*
  * out[M, N] = x[M, K] . dequantize(w)^T       (transpose = 1)
@@ -154,13 +172,15 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
  * Replaces kernels/moe_combine.py:160-195 (`combine(y, inv, w, rows, top_k)`,
  * the unsort + router weight + top-k sum after the down projection,
  * fused._moe_fold_block combine mode, fused.py:3283-3316).
- * y is [*, N] in expert order (dtype bf16 or fp16), inv int32 [rows*top_k]
- * gives the row of y holding token t's k-th expert output (NULL: row
- * t*top_k + k), w float32 [rows*top_k], out [rows, N].  N % 8 == 0,
- * 1 <= top_k <= 64, y and out 16-byte aligned.
+ * y is [y_rows, N] in expert order (dtype bf16 or fp16), inv int32
+ * [rows*top_k] gives the row of y holding token t's k-th expert output
+ * (NULL: row t*top_k + k, which requires y_rows >= rows*top_k); an inv entry
+ * outside [0, y_rows) contributes nothing (as a zero router weight would), so
+ * no index reads outside y.  w float32 [rows*top_k], out [rows, N].
+ * N % 8 == 0, 1 <= top_k <= 64, y and out 16-byte aligned.
  */
-int mq_moe_combine(const void* y, const int32_t* inv, const float* w, void* out, int64_t rows,
-                   int64_t top_k, int64_t N, int dtype, void* hip_stream);
+int mq_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w, void* out,
+                   int64_t rows, int64_t top_k, int64_t N, int dtype, void* hip_stream);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,8 @@ hand-written HIP kernels behind a C ABI (``include/mlxturbo_amd.h``):
 
 * :func:`quantized_matmul` - decode (M=1), verify (M=2..16) and prefill widths
 * :func:`gather_qmm`       - MoE expert gather
-* :func:`dequantize`       - bit-exact MLX affine dequantization
+* :func:`dequantize`       - bit-exact MLX affine dequantization (every width)
+* :func:`quantize`         - MLX affine quantization (``mx.quantize``)
 * :func:`gather_glu`       - fused MoE gate+up+SiLU at decode widths
 * :func:`moe_combine`      - MoE unsort + router weight + top-k sum epilogue
 
@@ -13,16 +14,17 @@ Module level (:mod:`mlxturbo_amd.nn`, :mod:`mlxturbo_amd.dispatch`): torch
 ``QuantizedLinear`` / ``QuantizedSwitchLinear`` / ``SwitchGLU`` on MLX-format
 tensors, and the reference's shape-by-M route table with per-instance and
 class-level enabling.  :mod:`mlxturbo_amd.checkpoint` builds those modules
-from MLX safetensors checkpoints.
+from MLX safetensors checkpoints; :mod:`mlxturbo_amd.rebit` re-quantizes loaded
+layers to another width (dequantize + quantize on the GPU).
 """
 
-from . import checkpoint, dispatch, nn
-from .ops import (dequantize, gather_glu, gather_qmm, launch_count, moe_combine,
+from . import checkpoint, dispatch, nn, rebit
+from .ops import (dequantize, gather_glu, gather_qmm, launch_count, moe_combine, quantize,
                   quantized_matmul)
 
-__version__ = "0.1.0"
+__version__ = "0.2.0"
 
-__all__ = ["checkpoint", "dequantize", "dispatch", "gather_glu", "gather_qmm", "launch_count",
+__all__ = ["checkpoint", "rebit", "dequantize", "dispatch", "gather_glu", "gather_qmm", "launch_count",
            "moe_combine",
-           "nn", "quantized_matmul",
+           "nn", "quantize", "quantized_matmul",
            "__version__"]

@@ -27,6 +27,7 @@ EXPORTED = (
     "mq_last_error",
     "mq_launch_count",
     "mq_dequantize",
+    "mq_quantize",
     "mq_quantized_matmul",
     "mq_quantized_matmul_workspace_size",
     "mq_quantized_matmul_ws",
@@ -57,6 +58,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_launch_count.argtypes = []
     lib.mq_dequantize.restype = _int
     lib.mq_dequantize.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]
+    lib.mq_quantize.restype = _int
+    lib.mq_quantize.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]
     lib.mq_quantized_matmul.restype = _int
     lib.mq_quantized_matmul.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
                                         _int, _int, _vp]
@@ -75,7 +78,7 @@ def _bind(lib: ctypes.CDLL) -> None:
                                   _i64, _i64, _i64, _i64, _int, _int, _int, _vp, ctypes.c_size_t,
                                   _vp]
     lib.mq_moe_combine.restype = _int
-    lib.mq_moe_combine.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]
+    lib.mq_moe_combine.argtypes = [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]
 
 
 def lib() -> ctypes.CDLL:

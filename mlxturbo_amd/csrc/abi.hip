@@ -35,7 +35,8 @@ int check_launch(const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_common(const void* w, const void* scales, const void* biases, int64_t N, int64_t K,
+// Arguments every format shares: MLX's widths, group sizes and dtypes.
+int check_format(const void* w, const void* scales, const void* biases, int64_t N, int64_t K,
                  int group_size, int bits, int dtype) {
   if (!w || !scales) return fail(MQ_EINVAL, "w and scales must be non-null");
   if (!biases) return fail(MQ_EINVAL, "affine mode requires biases");
@@ -48,9 +49,17 @@ int check_common(const void* w, const void* scales, const void* biases, int64_t 
     return fail(MQ_EINVAL, "K=%lld is not a multiple of group_size=%d", (long long)K, group_size);
   if (dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16 && dtype != MQ_FLOAT32)
     return fail(MQ_EINVAL, "unknown dtype code %d", dtype);
-  if (bits != 4 && bits != 8)
-    return fail(MQ_EUNSUPPORTED, "bits=%d is not implemented (4 and 8 are)", bits);
   if (!aligned16(w)) return fail(MQ_EINVAL, "w must be 16-byte aligned");
+  return MQ_OK;
+}
+
+// check_format plus the widths the matmul kernels take (4 and 8 bits).
+int check_common(const void* w, const void* scales, const void* biases, int64_t N, int64_t K,
+                 int group_size, int bits, int dtype) {
+  const int rc = check_format(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (bits != 4 && bits != 8)
+    return fail(MQ_EUNSUPPORTED, "bits=%d has no matmul kernel (4 and 8 do)", bits);
   return MQ_OK;
 }
 
@@ -70,7 +79,7 @@ int dispatch_16(int dtype, int bits, int gs, Args... args) {
 
 extern "C" {
 
-int mq_version(void) { return 1; }
+int mq_version(void) { return 2; }
 
 const char* mq_last_error(void) { return g_last_error.c_str(); }
 
@@ -78,11 +87,17 @@ uint64_t mq_launch_count(void) { return g_launches.load(std::memory_order_relaxe
 
 int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, void* out,
                   int64_t N, int64_t K, int group_size, int bits, int dtype, void* hip_stream) {
-  int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
+  int rc = check_format(w, scales, biases, N, K, group_size, bits, dtype);
   if (rc) return rc;
   if (!out) return fail(MQ_EINVAL, "out must be non-null");
+  if (!aligned16(out)) return fail(MQ_EINVAL, "out must be 16-byte aligned");
   if (N == 0) return MQ_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  if (bits != 4 && bits != 8) {
+    rc = mq::launch_dequantize_bits(w, scales, biases, out, N, K, group_size, bits, dtype, st);
+    if (rc) return fail(rc, "dequantize: no kernel for bits=%d group_size=%d", bits, group_size);
+    return check_launch("dequantize");
+  }
   if (dtype == MQ_FLOAT32) {
     const int64_t words = N * (K * bits / 32);
 #define MQ_D32(B, G)                                                                         \
@@ -95,11 +110,25 @@ int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, voi
 #undef MQ_D32
     return fail(MQ_EUNSUPPORTED, "dequantize: unsupported float32 configuration");
   }
-  if (!aligned16(out)) return fail(MQ_EINVAL, "out must be 16-byte aligned");
   rc = dispatch_16<mq::DequantLaunch>(dtype, bits, group_size, w, scales, biases, out, N, K, st);
   if (rc) return fail(rc, "dequantize: no kernel for dtype=%d bits=%d group_size=%d", dtype, bits,
                       group_size);
   return check_launch("dequantize");
+}
+
+int mq_quantize(const void* w, uint32_t* wq, void* scales, void* biases, int64_t N, int64_t K,
+                int group_size, int bits, int dtype, void* hip_stream) {
+  int rc = check_format(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!wq) return fail(MQ_EINVAL, "wq must be non-null");
+  if (!aligned16(wq)) return fail(MQ_EINVAL, "wq must be 16-byte aligned");
+  if (dtype != MQ_FLOAT32 && (!aligned16(scales) || !aligned16(biases)))
+    return fail(MQ_EINVAL, "scales and biases must be 16-byte aligned");
+  if (N == 0) return MQ_OK;
+  rc = mq::launch_quantize(w, wq, scales, biases, N, K, group_size, bits, dtype,
+                           reinterpret_cast<hipStream_t>(hip_stream));
+  if (rc) return fail(rc, "quantize: no kernel for bits=%d group_size=%d", bits, group_size);
+  return check_launch("quantize");
 }
 
 size_t mq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size,
@@ -237,11 +266,12 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
   return MQ_OK;
 }
 
-int mq_moe_combine(const void* y, const int32_t* inv, const float* w, void* out, int64_t rows,
-                   int64_t top_k, int64_t N, int dtype, void* hip_stream) {
+int mq_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w, void* out,
+                   int64_t rows, int64_t top_k, int64_t N, int dtype, void* hip_stream) {
   if (!y || !w || !out) return fail(MQ_EINVAL, "y, w and out must be non-null");
-  if (rows < 0 || N <= 0) return fail(MQ_EINVAL, "invalid sizes rows=%lld N=%lld",
-                                      (long long)rows, (long long)N);
+  if (rows < 0 || N <= 0 || y_rows < 0) return fail(MQ_EINVAL, "invalid sizes rows=%lld N=%lld y_rows=%lld",
+                                      (long long)rows, (long long)N, (long long)y_rows);
+  if (y_rows > INT32_MAX) return fail(MQ_EUNSUPPORTED, "moe_combine supports y_rows < 2^31");
   if (top_k < 1 || top_k > mq::kCombineMaxTopK)
     return fail(MQ_EINVAL, "top_k must be in 1..%d (got %lld)", mq::kCombineMaxTopK,
                 (long long)top_k);
@@ -250,8 +280,11 @@ int mq_moe_combine(const void* y, const int32_t* inv, const float* w, void* out,
     return fail(MQ_EUNSUPPORTED, "moe_combine supports bf16 and fp16 (dtype %d)", dtype);
   if (!aligned16(y) || !aligned16(out)) return fail(MQ_EINVAL, "y and out must be 16-byte aligned");
   if (rows > 65535) return fail(MQ_EUNSUPPORTED, "moe_combine supports up to 65535 rows per call");
+  if (!inv && y_rows < rows * top_k)
+    return fail(MQ_EINVAL, "inv=NULL needs y_rows >= rows*top_k (%lld < %lld)", (long long)y_rows,
+                (long long)(rows * top_k));
   if (rows == 0) return MQ_OK;
-  int rc = mq::launch_moe_combine(y, inv, w, out, rows, top_k, N, dtype,
+  int rc = mq::launch_moe_combine(y, y_rows, inv, w, out, rows, top_k, N, dtype,
                                   reinterpret_cast<hipStream_t>(hip_stream));
   if (rc) return fail(rc, "moe_combine: no kernel for this configuration");
   return check_launch("moe_combine");

@@ -9,7 +9,9 @@
 // (inv, w).  One workgroup per token; each thread owns 8 columns (one 16-byte
 // load per expert row, one 16-byte store), so every read of y is a
 // contiguous 16-byte piece of a row and a wave reads 1 KiB per instruction.
-// The token's row numbers and weights are read once into LDS.
+// The token's row numbers and weights are read once into LDS; a row number
+// outside [0, y_rows) is dropped there (its term is skipped), so a bad index
+// never reads outside y.
 #pragma once
 #include "mq_common.h"
 
@@ -22,14 +24,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
                                                           const int32_t* __restrict__ inv,
                                                           const float* __restrict__ w,
                                                           uint16_t* __restrict__ out, int top_k,
-                                                          int N) {
+                                                          int N, int y_rows) {
   using T = T16<DT>;
   __shared__ int s_row[kCombineMaxTopK];
   __shared__ float s_w[kCombineMaxTopK];
   const int t = blockIdx.y;
   const int64_t base = (int64_t)t * top_k;
   for (int i = threadIdx.x; i < top_k; i += blockDim.x) {
-    s_row[i] = inv ? inv[base + i] : (int)(base + i);
+    const int r = inv ? inv[base + i] : (int)(base + i);
+    s_row[i] = (r >= 0 && r < y_rows) ? r : -1;
     s_w[i] = w[base + i];
   }
   __syncthreads();
@@ -39,6 +42,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 #pragma unroll
   for (int v = 0; v < 8; ++v) acc[v] = 0.f;
   for (int k = 0; k < top_k; ++k) {
+    if (s_row[k] < 0) continue;
     const float wk = s_w[k];
     const u32x4 p = *reinterpret_cast<const u32x4*>(y + (int64_t)s_row[k] * N + n);
 #pragma unroll
@@ -53,17 +57,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   *reinterpret_cast<u32x4*>(out + (int64_t)t * N + n) = o;
 }
 
-inline int launch_moe_combine(const void* y, const int32_t* inv, const float* w, void* out,
-                              int64_t rows, int64_t top_k, int64_t N, int dtype, hipStream_t st) {
+inline int launch_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w,
+                              void* out, int64_t rows, int64_t top_k, int64_t N, int dtype,
+                              hipStream_t st) {
   const int64_t cols = N / 8;
   const int tb = cols >= 256 ? 256 : cols >= 128 ? 128 : 64;
   const dim3 grid((unsigned)((cols + tb - 1) / tb), (unsigned)rows);
   if (dtype == kBF16)
     hipLaunchKernelGGL(moe_combine_kernel<kBF16>, grid, dim3(tb), 0, st, (const uint16_t*)y, inv,
-                       w, (uint16_t*)out, (int)top_k, (int)N);
+                       w, (uint16_t*)out, (int)top_k, (int)N, (int)y_rows);
   else if (dtype == kF16)
     hipLaunchKernelGGL(moe_combine_kernel<kF16>, grid, dim3(tb), 0, st, (const uint16_t*)y, inv,
-                       w, (uint16_t*)out, (int)top_k, (int)N);
+                       w, (uint16_t*)out, (int)top_k, (int)N, (int)y_rows);
   else
     return kStatusUnsupported;
   return 0;

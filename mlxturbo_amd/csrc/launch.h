@@ -56,6 +56,16 @@ struct GluLaunch {
                  int64_t K, int64_t E, void* ws, hipStream_t st, int* nlaunch);
 };
 
+// MLX affine quantize of N x K float values (dtype DT: weights, scales and
+// biases share it) into the bitstream format, and dequantize of any width
+// (formats.hip).  Both return 0 or kStatusUnsupported for a configuration
+// outside bits {2,3,4,5,6,8} x group {32,64,128} x dtype {bf16,f16,f32}.
+int launch_quantize(const void* w, uint32_t* wq, void* scales, void* biases, int64_t N,
+                    int64_t K, int group_size, int bits, int dtype, hipStream_t st);
+int launch_dequantize_bits(const uint32_t* wq, const void* scales, const void* biases, void* out,
+                           int64_t N, int64_t K, int group_size, int bits, int dtype,
+                           hipStream_t st);
+
 // ---- host-side routing and sizing ------------------------------------------
 
 // Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
@@ -202,6 +212,13 @@ constexpr int64_t kGroupedMinRows = 1024;
 // [header[1], header[2]), class 0 [header[2], header[3]) (header[3] = nseg).
 __host__ __device__ inline size_t gather_ws_header(int64_t P) { return 1 + 4 * (size_t)P; }
 __host__ __device__ inline size_t gather_ws_words(int64_t P) { return gather_ws_header(P) + 4; }
+
+// Builds gather_qmm's segment tables for P pairs into ws (prep.hip): pairs
+// sorted by expert (E for invalid ones), cut into segments of up to R pairs,
+// or by size class (R2 pairs from C2 pairs per expert, R1 from C1, R below).
+// Needs E <= kGatherPrepMaxE; returns 0 or a HIP error.
+int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, int64_t B, int R,
+                void* ws, hipStream_t st, int R1 = 0, int C1 = 0, int R2 = 0, int C2 = 0);
 
 inline size_t gather_workspace_bytes(int64_t P, int64_t M) {
   if (P <= kGatherFusedMaxP && P * M < kGroupedMinRows) return 0;

@@ -78,15 +78,18 @@ def select_route(k: int, n: int, m: int,
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: Optional[torch.Tensor], *, group_size: int, bits: int,
                      mode: str = "affine",
-                     table: Optional[dict[tuple[int, int], tuple[str, ...]]] = None
-                     ) -> torch.Tensor:
+                     table: Optional[dict[tuple[int, int], tuple[str, ...]]] = None,
+                     prepared: Optional[ops.PreparedWeights] = None) -> torch.Tensor:
     """Dispatch a QuantizedLinear matmul by ``(K, N, M)``.
 
     ``skinny`` runs the streaming kernel in launches of up to 16 rows even for
     wider inputs (a route-table override); ``wide`` and ``stock`` defer to
-    the library's width choice.
+    the library's width choice.  ``prepared`` (the layer's validated weights)
+    skips re-validating them on every call.
     """
     def stock():
+        if prepared is not None:
+            return ops.quantized_matmul_prepared(x, prepared)
         return ops.quantized_matmul(x, w, scales, biases, transpose=True,
                                     group_size=group_size, bits=bits, mode=mode)
 
@@ -116,7 +119,8 @@ class DispatchedQuantizedLinear(QuantizedLinear):
         if not active:
             return super().forward(x)
         out = quantized_matmul(x, self.weight, self.scales, self.biases,
-                               group_size=self.group_size, bits=self.bits, mode=self.mode)
+                               group_size=self.group_size, bits=self.bits, mode=self.mode,
+                               prepared=self.prepared_weights())
         if self.bias is not None:
             out = out + self.bias
         return out
@@ -167,7 +171,8 @@ def enable_class() -> None:
 
     def forward(self, x):
         out = quantized_matmul(x, self.weight, self.scales, self.biases,
-                               group_size=self.group_size, bits=self.bits, mode=self.mode)
+                               group_size=self.group_size, bits=self.bits, mode=self.mode,
+                               prepared=self.prepared_weights())
         if self.bias is not None:
             out = out + self.bias
         return out

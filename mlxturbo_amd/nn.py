@@ -59,19 +59,29 @@ class QuantizedLinear(torch.nn.Module):
         self.register_buffer("biases", biases)
         self.register_buffer("bias", bias)
 
+    def prepared_weights(self) -> Optional["ops.PreparedWeights"]:
+        """The layer's weights validated once (:class:`ops.PreparedWeights`),
+        rebuilt when a tensor is replaced or written in place; ``None`` for
+        configurations the full operator handles (non-affine modes, weights
+        off the GPU, missing biases)."""
+        if self.mode != "affine" or self.weight.device.type != "cuda" or self.biases is None:
+            return None
+        p = self.__dict__.get("_mq_prepared")
+        if p is None or not p.matches(self.weight, self.scales, self.biases, self.group_size,
+                                      self.bits):
+            p = ops.PreparedWeights(self.weight, self.scales, self.biases, self.group_size,
+                                    self.bits, self.mode)
+            self.__dict__["_mq_prepared"] = p
+        return p
+
     def quantized_forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.mode != "affine" or self.weight.device.type != "cuda":
+        p = self.prepared_weights()
+        if p is None:
             # the full operator raises the reference's errors
             out = ops.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                                        group_size=self.group_size, bits=self.bits,
                                        mode=self.mode)
         else:
-            p = self.__dict__.get("_mq_prepared")
-            if p is None or not p.matches(self.weight, self.scales, self.biases,
-                                          self.group_size, self.bits):
-                p = ops.PreparedWeights(self.weight, self.scales, self.biases, self.group_size,
-                                        self.bits, self.mode)
-                self.__dict__["_mq_prepared"] = p
             out = ops.quantized_matmul_prepared(x, p)
         if self.bias is not None:
             out = out + self.bias
@@ -79,6 +89,20 @@ class QuantizedLinear(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.quantized_forward(x)
+
+    @classmethod
+    def from_linear(cls, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                    group_size: int = 64, bits: int = 4) -> "QuantizedLinear":
+        """Quantize a float weight ``[N, K]`` (``mlx.nn.QuantizedLinear.
+        from_linear``): ``mx.quantize`` on the GPU; scales and biases keep
+        the weight's dtype."""
+        wq, s, b = ops.quantize(weight, group_size=group_size, bits=bits)
+        return cls(wq, s, b, bias=bias, group_size=group_size, bits=bits)
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """The layer's weight as ``mx.dequantize`` gives it, ``[N, K]``."""
+        return ops.dequantize(self.weight, self.scales, self.biases, self.group_size, self.bits,
+                              self.mode)
 
     def extra_repr(self) -> str:
         return (f"input_dims={self.input_dims}, output_dims={self.output_dims}, "

@@ -78,16 +78,20 @@ def _check_mode(mode: str, biases) -> None:
         raise ValueError("affine quantization requires biases")
 
 
-def _check_quant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
-                 group_size: int, bits: int) -> int:
-    if w.dtype not in (torch.uint32, torch.int32):
-        raise ValueError(f"w must be uint32 packed codes, got {w.dtype}")
+def _check_format(group_size: int, bits: int) -> None:
     if group_size not in _GROUP_SIZES:
         raise ValueError(f"group_size must be one of {_GROUP_SIZES}, got {group_size}")
     if bits not in _BITS:
         raise ValueError(f"bits must be one of {_BITS}, got {bits}")
-    if bits not in (4, 8):
-        raise NotImplementedError(f"bits={bits}: only 4- and 8-bit codes are on this path")
+
+
+def _check_quant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int, bits: int) -> int:
+    if w.dtype not in (torch.uint32, torch.int32):
+        raise ValueError(f"w must be uint32 packed codes, got {w.dtype}")
+    _check_format(group_size, bits)
+    if (w.shape[-1] * 32) % bits:
+        raise ValueError(f"w last dimension {w.shape[-1]} is not whole {bits}-bit codes")
     K = w.shape[-1] * 32 // bits
     if scales.shape != biases.shape:
         raise ValueError(f"scales {tuple(scales.shape)} and biases {tuple(biases.shape)} differ")
@@ -111,9 +115,44 @@ def _dtype_code(x_dtype: torch.dtype, s_dtype: torch.dtype) -> int:
     return _DTYPE_CODE[x_dtype]
 
 
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4, mode: str = "affine"):
+    """``mx.quantize(w, group_size, bits, mode="affine")``: returns
+    ``(w_q, scales, biases)`` with ``w_q`` uint32 ``[..., K*bits/32]`` and
+    scales/biases ``[..., K/group_size]`` in ``w``'s dtype, as the reference
+    calls it when it requantizes a layer (mlxturbo/rebit.py:119) or builds
+    test weights (kernels/moe_verify_gather.py:887).  One HIP kernel; the
+    per-group arithmetic is the C ABI's ``mq_quantize``."""
+    if mode != "affine":
+        raise NotImplementedError(f"mode={mode!r}: only affine quantization is on this path")
+    dev = _require_gpu(w)
+    _check_format(group_size, bits)
+    if w.dtype not in _DTYPE_CODE:
+        raise ValueError(f"w must be bfloat16, float16 or float32, got {w.dtype}")
+    if w.ndim < 1:
+        raise ValueError("w must have at least one dimension")
+    K = w.shape[-1]
+    if K == 0 or K % group_size:
+        raise ValueError(f"the last dimension {K} must be a positive multiple of "
+                         f"group_size={group_size}")
+    lead = tuple(w.shape[:-1])
+    N = math.prod(lead)
+    wq = torch.empty((*lead, K * bits // 32), dtype=torch.uint32, device=dev)
+    scales = torch.empty((*lead, K // group_size), dtype=w.dtype, device=dev)
+    biases = torch.empty_like(scales)
+    if N == 0:
+        return wq, scales, biases
+    w_ = _aligned(w.reshape(N, K))
+    rc = _lib.lib().mq_quantize(w_.data_ptr(), wq.data_ptr(), scales.data_ptr(),
+                                biases.data_ptr(), N, K, group_size, bits,
+                                _DTYPE_CODE[w.dtype], _stream_ptr(wq))
+    _lib.check(rc, "quantize")
+    return wq, scales, biases
+
+
 def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: Optional[torch.Tensor] = None,
                group_size: int = 64, bits: int = 4, mode: str = "affine") -> torch.Tensor:
-    """``mx.dequantize``: ``T(float(s)*q + float(b))`` bit-exact, dtype of ``scales``."""
+    """``mx.dequantize``: ``T(float(s)*q + float(b))`` bit-exact, dtype of
+    ``scales``, for every MLX width (2, 3, 4, 5, 6, 8 bits)."""
     _check_mode(mode, biases)
     dev = _require_gpu(w, scales, biases)
     K = _check_quant(w, scales, biases, group_size, bits)
@@ -131,28 +170,60 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: Optional[torch.Ten
     return out
 
 
+def _kernel_dtype(x_dtype: torch.dtype, s_dtype: torch.dtype) -> bool:
+    """Whether the matmul kernels compute in this (activation, scale) dtype pair."""
+    return x_dtype == s_dtype and x_dtype in (torch.bfloat16, torch.float16)
+
+
+def _result_dtype(x_dtype: torch.dtype, s_dtype: torch.dtype) -> torch.dtype:
+    """MLX's promotion of (x, scales, biases) for the quantized operators."""
+    dt = torch.promote_types(x_dtype, s_dtype)
+    if not dt.is_floating_point:
+        raise ValueError(f"quantized operators need floating activations, got {x_dtype}")
+    return dt
+
+
+def _composed_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                  transpose: bool, group_size: int, bits: int) -> torch.Tensor:
+    """Configurations the matmul kernels do not take (2/3/5/6-bit codes,
+    ``transpose=False``, float32 or mixed-dtype activations): this library's
+    bit-exact :func:`dequantize` in the promoted dtype, then one GPU GEMM.
+    It stands where the reference falls back to ``mx.quantized_matmul``
+    (fast_qmm.py:356-362; qmv_small_m.py:309-323; dispatch.py:317-327)."""
+    dt = _result_dtype(x.dtype, scales.dtype)
+    deq = dequantize(w, scales.to(dt), biases.to(dt), group_size, bits)
+    xx = x.to(dt)
+    if transpose:
+        return torch.nn.functional.linear(xx, deq)           # x @ deq^T, deq [N, K]
+    return torch.matmul(xx, deq)                              # deq [K, N]
+
+
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: Optional[torch.Tensor] = None, transpose: bool = True,
                      group_size: int = 64, bits: int = 4, mode: str = "affine") -> torch.Tensor:
-    """``mx.quantized_matmul``: ``x @ dequantize(w).T`` for ``x[..., K]``.
+    """``mx.quantized_matmul``: ``x @ dequantize(w).T`` for ``x[..., K]``
+    (``transpose=False``: ``x @ dequantize(w)`` with ``w`` quantized along N).
 
     Leading dimensions of ``x`` are flattened to M and restored on the output
     (as mlxturbo/kernels/dispatch.py:332-382 does around its kernels).
+    4- and 8-bit codes with bf16/fp16 activations in the scales' dtype run on
+    the matmul kernels; every other MLX configuration runs as the library's
+    dequantize plus one GPU GEMM (:func:`_composed_qmm`).
     """
     _check_mode(mode, biases)
     dev = _require_gpu(x, w, scales, biases)
     if w.ndim != 2:
         raise NotImplementedError("batched w: only 2-D weights are on this path")
-    if not transpose:
-        raise NotImplementedError("transpose=False is not on this path")
-    K = _check_quant(w, scales, biases, group_size, bits)
+    Kq = _check_quant(w, scales, biases, group_size, bits)
     if x.ndim < 1:
         raise ValueError("x must have at least one dimension")
+    K, N = (Kq, w.shape[0]) if transpose else (w.shape[0], Kq)
     if x.shape[-1] != K:
         raise ValueError(
             f"x last dimension {x.shape[-1]} does not match the quantized weight K={K}")
-    code = _dtype_code(x.dtype, scales.dtype)
-    N = w.shape[0]
+    if not (transpose and bits in (4, 8) and _kernel_dtype(x.dtype, scales.dtype)):
+        return _composed_qmm(x, w, scales, biases, transpose, group_size, bits)
+    code = _DTYPE_CODE[x.dtype]
     lead = tuple(x.shape[:-1])
     M = math.prod(lead)
     out = torch.empty((*lead, N), dtype=x.dtype, device=dev)
@@ -177,7 +248,9 @@ class PreparedWeights:
     """Weight-side arguments of :func:`quantized_matmul`, validated once
     (the per-call cost of a layer that reuses its weights is then the x
     checks and the launch).  ``matches`` tells whether the tensors are still
-    the ones validated."""
+    the ones validated: the same storage and no in-place write since (the
+    key holds each tensor's version counter, so a ``copy_`` into the layer's
+    weights, e.g. ``load_state_dict``, invalidates a cached aligned copy)."""
 
     __slots__ = ("w", "s", "b", "N", "K", "group_size", "bits", "dtype", "dev", "key")
 
@@ -191,10 +264,15 @@ class PreparedWeights:
         self.N = w.shape[0]
         self.w, self.s, self.b = _aligned(w), _aligned(scales), _aligned(biases)
         self.group_size, self.bits, self.dtype = group_size, bits, scales.dtype
-        self.key = (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits)
+        self.key = self._key(w, scales, biases, group_size, bits)
+
+    @staticmethod
+    def _key(w, scales, biases, group_size, bits):
+        return (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), w._version, scales._version,
+                biases._version, group_size, bits)
 
     def matches(self, w, scales, biases, group_size: int, bits: int) -> bool:
-        return self.key == (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits)
+        return self.key == self._key(w, scales, biases, group_size, bits)
 
 
 _QMM_WS_BYTES: dict = {}
@@ -202,7 +280,8 @@ _QMM_WS_BYTES: dict = {}
 
 def quantized_matmul_prepared(x: torch.Tensor, p: PreparedWeights) -> torch.Tensor:
     """:func:`quantized_matmul` with weights validated by :class:`PreparedWeights`."""
-    if x.device != p.dev or x.dtype != p.dtype or x.ndim < 1 or x.shape[-1] != p.K:
+    if (x.device != p.dev or x.dtype != p.dtype or x.ndim < 1 or x.shape[-1] != p.K
+            or p.bits not in (4, 8) or not _kernel_dtype(x.dtype, p.dtype)):
         return quantized_matmul(x, p.w, p.s, p.b, group_size=p.group_size, bits=p.bits)
     N, K = p.N, p.K
     M = x.numel() // K
@@ -283,25 +362,30 @@ def _as_index(t, dev) -> torch.Tensor:
 
 def _gather_prep(x, banks, lhs_indices, rhs_indices, transpose, group_size, bits, mode):
     """Validation and flattening shared by gather_qmm and gather_glu; ``banks``
-    is a list of (w, scales, biases) of one shape."""
+    is a list of (w, scales, biases) of one shape.  Returns ``(out, args)``:
+    ``args`` is None when there is nothing to compute, else the flattened
+    call (``route``: "kernel", "rows" (more than 16 rows per pair), "slices"
+    (more experts than the prep kernel's tables hold) or "composed" (no
+    kernel for the format or dtype))."""
     for _, _, b in banks:
         _check_mode(mode, b)
     dev = _require_gpu(x, *[t for bank in banks for t in bank])
-    if not transpose:
-        raise NotImplementedError("transpose=False is not on this path")
     w0 = banks[0][0]
     if x.ndim < 2 or w0.ndim < 3:
         raise ValueError("gather_qmm needs x (..., M, K) and w (..., N, K*bits/32) with a batch dim")
     for w, s, b in banks:
         if w.shape != w0.shape:
             raise ValueError(f"expert banks differ in shape: {tuple(w.shape)} and {tuple(w0.shape)}")
-        K = _check_quant(w, s, b, group_size, bits)
+        Kq = _check_quant(w, s, b, group_size, bits)
+        if s.dtype != banks[0][1].dtype:
+            raise ValueError("expert banks differ in scale dtype")
+    K, N = (Kq, w0.shape[-2]) if transpose else (w0.shape[-2], Kq)
     if x.shape[-1] != K:
         raise ValueError(
             f"x last dimension {x.shape[-1]} does not match the quantized weight K={K}")
-    code = _dtype_code(x.dtype, banks[0][1].dtype)
+    kernel_dtype = _kernel_dtype(x.dtype, banks[0][1].dtype)
+    out_dtype = x.dtype if kernel_dtype else _result_dtype(x.dtype, banks[0][1].dtype)
     M = x.shape[-2]
-    N = w0.shape[-2]
     bx = tuple(x.shape[:-2])
     bw = tuple(w0.shape[:-2])
     B = math.prod(bx)
@@ -316,30 +400,119 @@ def _gather_prep(x, banks, lhs_indices, rhs_indices, transpose, group_size, bits
         raise ValueError(f"lhs_indices {lshape} and rhs_indices "
                          f"{tuple(rhs.shape)} do not broadcast") from exc
     P = math.prod(shape)
-    out = torch.empty((*shape, M, N), dtype=x.dtype, device=dev)
+    out = torch.empty((*shape, M, N), dtype=out_dtype, device=dev)
     if P == 0 or M == 0 or N == 0:
         return out, None
-    if M > 16:
-        raise NotImplementedError(f"gather_qmm with M={M} rows per pair (> 16)")
     lhs_f = (_default_lhs(dev, bx, tuple(shape)) if lhs is None
              else lhs.expand(shape).reshape(-1).to(torch.int32).contiguous())
     rhs_f = rhs.expand(shape).reshape(-1).to(torch.int32).contiguous()
-    x_ = _aligned(x.reshape(B, M, K))
     flat = []
     for w, s, b in banks:
-        flat += [_aligned(w.reshape(E, N, w.shape[-1])),
-                 _aligned(s.reshape(E, N, s.shape[-1])),
-                 _aligned(b.reshape(E, N, b.shape[-1]))]
-    lib = _lib.lib()
-    nbytes = int(lib.mq_gather_qmm_workspace_size(P, M))
-    ws = _workspace(dev, nbytes) if nbytes else None
-    args = dict(x=x_, flat=flat, lhs=lhs_f, rhs=rhs_f, P=P, B=B, M=M, N=N, K=K, E=E, code=code,
-                ws=ws, lib=lib)
+        flat += [_aligned(w.reshape(E, *w.shape[-2:])),
+                 _aligned(s.reshape(E, *s.shape[-2:])),
+                 _aligned(b.reshape(E, *b.shape[-2:]))]
+    if not (transpose and bits in (4, 8) and kernel_dtype):
+        route = "composed"
+    elif M > 16:
+        route = "rows"
+    elif P > _GATHER_FUSED_MAX_P and E > _GATHER_PREP_MAX_E:
+        route = "slices"
+    else:
+        route = "kernel"
+    args = dict(x=x.reshape(B, M, K), flat=flat, lhs=lhs_f, rhs=rhs_f, P=P, B=B, M=M, N=N, K=K,
+                E=E, dev=dev, route=route, transpose=transpose, shape=tuple(shape),
+                dtype=out_dtype)
     return out, args
+
+
+# gather_qmm's kernels: up to this many pairs are grouped inside the matmul
+# kernel, more go through the prep kernel, whose tables hold this many experts
+_GATHER_FUSED_MAX_P = 256
+_GATHER_PREP_MAX_E = 2048
 
 
 def _ptr(t: Optional[torch.Tensor]):
     return t.data_ptr() if t is not None else None
+
+
+def _gather_launch(x3, flat, lhs, rhs, out, P, B, M, N, K, E, group_size, bits,
+                   sorted_indices) -> None:
+    """One mq_gather_qmm call on flattened, validated arguments."""
+    x_ = _aligned(x3)
+    lib = _lib.lib()
+    nbytes = int(lib.mq_gather_qmm_workspace_size(P, M))
+    ws = _workspace(out.device, nbytes) if nbytes else None
+    rc = lib.mq_gather_qmm(x_.data_ptr(), *[t.data_ptr() for t in flat], _ptr(lhs),
+                           rhs.data_ptr(), out.data_ptr(), P, B, M, N, K, E, group_size, bits,
+                           _DTYPE_CODE[x3.dtype], int(bool(sorted_indices)), _ptr(ws),
+                           ws.numel() if ws is not None else 0, _stream_ptr(out))
+    _lib.check(rc, "gather_qmm")
+
+
+def _gather_rows(a, out, group_size, bits, sorted_indices) -> torch.Tensor:
+    """More than 16 rows per pair: row m of pair p is the one-row pair
+    (lhs[p] * M + m, rhs[p]) of x viewed as B*M one-row batches, so the call
+    is one gather of P*M one-row pairs (prefill-sized, the grouped kernel)."""
+    P, B, M, N, K = a["P"], a["B"], a["M"], a["N"], a["K"]
+    dev = a["dev"]
+    rows = torch.arange(M, device=dev, dtype=torch.int32)
+    lhs = a["lhs"] if a["lhs"] is not None else torch.arange(P, device=dev, dtype=torch.int32)
+    lhs1 = (lhs[:, None] * M + rows[None, :]).reshape(-1).contiguous()
+    rhs1 = a["rhs"][:, None].expand(P, M).reshape(-1).contiguous()
+    o = out.reshape(P * M, 1, N)
+    _gather_launch(a["x"].reshape(B * M, 1, K), a["flat"], lhs1, rhs1, o, P * M, B * M, 1, N, K,
+                   a["E"], group_size, bits, sorted_indices)
+    return out
+
+
+def _gather_slices(a, out, group_size, bits, sorted_indices) -> torch.Tensor:
+    """More experts than the prep kernel's tables hold: the bank is run in
+    slices of that many experts (contiguous views), pairs of other slices
+    marked invalid (zero rows), and each pair's row kept from its slice."""
+    P, E = a["P"], a["E"]
+    rhs = a["rhs"]
+    res = None
+    for e0 in range(0, E, _GATHER_PREP_MAX_E):
+        e1 = min(E, e0 + _GATHER_PREP_MAX_E)
+        inside = (rhs >= e0) & (rhs < e1)
+        r = torch.where(inside, rhs - e0, torch.full_like(rhs, -1))
+        part = torch.empty_like(out) if res is not None else out
+        flat = [t[e0:e1] for t in a["flat"]]
+        _gather_launch(a["x"], flat, a["lhs"], r, part.reshape(P, a["M"], a["N"]), P, a["B"],
+                       a["M"], a["N"], a["K"], e1 - e0, group_size, bits, sorted_indices)
+        if res is None:
+            res = part
+        else:
+            res.copy_(torch.where(inside.reshape(*a["shape"], 1, 1), part, res))
+    return res
+
+
+def _gather_composed(a, out, bank, group_size, bits) -> torch.Tensor:
+    """Formats and dtypes without a gather kernel: each distinct expert's
+    weights dequantized by this library (bit-exact) in the promoted dtype
+    and applied to its pairs with one GPU GEMM; pairs with an out-of-range
+    index get zero rows, as in the kernels.  (The expert list is read on the
+    host, so this path synchronises the stream.)"""
+    w, s, b = bank
+    P, B, M, N, K, E = a["P"], a["B"], a["M"], a["N"], a["K"], a["E"]
+    dt = a["dtype"]
+    res = out.reshape(P, M, N)
+    res.zero_()
+    rhs = a["rhs"].long()
+    lhs = a["lhs"].long() if a["lhs"] is not None else torch.arange(P, device=a["dev"])
+    valid = (rhs >= 0) & (rhs < E) & (lhs >= 0) & (lhs < B)
+    rhs_h = torch.where(valid, rhs, torch.full_like(rhs, -1)).cpu()
+    xs = a["x"].to(dt)
+    for e in torch.unique(rhs_h).tolist():
+        if e < 0:
+            continue
+        sel = (rhs_h == e).nonzero().reshape(-1).to(a["dev"])
+        deq = dequantize(w[e], s[e].to(dt), b[e].to(dt), group_size, bits)
+        xe = xs[lhs[sel]]                                     # (n_e, M, K)
+        ye = (torch.nn.functional.linear(xe, deq) if a["transpose"]
+              else torch.matmul(xe, deq))
+        res[sel] = ye
+    return out
 
 
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
@@ -351,19 +524,23 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     ``x`` is ``(..., M, K)`` and ``w`` ``(..., N, K*bits/32)``; ``lhs_indices``
     index x's batch dims (default: all of them), ``rhs_indices`` index w's
     batch dims (default: all of them); the two broadcast together and the
-    output is ``broadcast_shape + (M, N)``.
+    output is ``broadcast_shape + (M, N)``.  4/8-bit codes with bf16/fp16
+    activations in the scales' dtype run on the gather kernels (more than 16
+    rows per pair as one-row pairs, banks beyond the prep tables in expert
+    slices); other formats and dtypes run as :func:`_gather_composed`.
     """
     out, a = _gather_prep(x, [(w, scales, biases)], lhs_indices, rhs_indices, transpose,
                           group_size, bits, mode)
     if a is None:
         return out
-    ws = a["ws"]
-    rc = a["lib"].mq_gather_qmm(a["x"].data_ptr(), *[t.data_ptr() for t in a["flat"]],
-                                _ptr(a["lhs"]), a["rhs"].data_ptr(), out.data_ptr(), a["P"],
-                                a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
-                                a["code"], int(bool(sorted_indices)), _ptr(ws),
-                                ws.numel() if ws is not None else 0, _stream_ptr(out))
-    _lib.check(rc, "gather_qmm")
+    if a["route"] == "composed":
+        return _gather_composed(a, out, a["flat"][:3], group_size, bits)
+    if a["route"] == "rows":
+        return _gather_rows(a, out, group_size, bits, sorted_indices)
+    if a["route"] == "slices":
+        return _gather_slices(a, out, group_size, bits, sorted_indices)
+    _gather_launch(a["x"], a["flat"], a["lhs"], a["rhs"], out, a["P"], a["B"], a["M"], a["N"],
+                   a["K"], a["E"], group_size, bits, sorted_indices)
     return out
 
 
@@ -380,25 +557,29 @@ def gather_glu(x: torch.Tensor, gate_w: torch.Tensor, gate_scales: torch.Tensor,
     ``moe_decode_fused.gate_up`` (kernels/moe_decode_fused.py:331-350).
 
     Fused in one kernel below 1024 output rows (decode / verify).  Above it
-    (prefill) the result is composed from two :func:`gather_qmm` calls and
-    a float SiLU-multiply of their rounded outputs, as the reference keeps
-    its stock path outside decode widths (fused.py:2476-2479)."""
+    (prefill), and for configurations the fused kernel does not take, the
+    result is composed from two :func:`gather_qmm` calls and a float
+    SiLU-multiply of their rounded outputs, as the reference keeps its stock
+    path outside decode widths (fused.py:2476-2479)."""
     out, a = _gather_prep(x, [(gate_w, gate_scales, gate_biases), (up_w, up_scales, up_biases)],
                           lhs_indices, rhs_indices, transpose, group_size, bits, mode)
     if a is None:
         return out
-    if a["P"] * a["M"] >= _GLU_FUSED_MAX_ROWS:
-        kw = dict(lhs_indices=lhs_indices, rhs_indices=rhs_indices, group_size=group_size,
-                  bits=bits, mode=mode, sorted_indices=sorted_indices)
+    if a["route"] != "kernel" or a["P"] * a["M"] >= _GLU_FUSED_MAX_ROWS:
+        kw = dict(lhs_indices=lhs_indices, rhs_indices=rhs_indices, transpose=transpose,
+                  group_size=group_size, bits=bits, mode=mode, sorted_indices=sorted_indices)
         g = gather_qmm(x, gate_w, gate_scales, gate_biases, **kw)
         u = gather_qmm(x, up_w, up_scales, up_biases, **kw)
-        return (torch.nn.functional.silu(g.float()) * u.float()).to(x.dtype)
-    ws = a["ws"]
-    rc = a["lib"].mq_gather_glu(a["x"].data_ptr(), *[t.data_ptr() for t in a["flat"]],
-                                _ptr(a["lhs"]), a["rhs"].data_ptr(), out.data_ptr(), a["P"],
-                                a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
-                                a["code"], _ptr(ws), ws.numel() if ws is not None else 0,
-                                _stream_ptr(out))
+        return (torch.nn.functional.silu(g.float()) * u.float()).to(g.dtype)
+    x_ = _aligned(a["x"])
+    lib = _lib.lib()
+    nbytes = int(lib.mq_gather_qmm_workspace_size(a["P"], a["M"]))
+    ws = _workspace(a["dev"], nbytes) if nbytes else None
+    rc = lib.mq_gather_glu(x_.data_ptr(), *[t.data_ptr() for t in a["flat"]],
+                           _ptr(a["lhs"]), a["rhs"].data_ptr(), out.data_ptr(), a["P"],
+                           a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
+                           _DTYPE_CODE[x.dtype], _ptr(ws), ws.numel() if ws is not None else 0,
+                           _stream_ptr(out))
     _lib.check(rc, "gather_glu")
     return out
 
@@ -438,7 +619,8 @@ def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, r
     out = torch.empty((rows, N), dtype=y.dtype, device=dev)
     if rows == 0:
         return out
-    rc = _lib.lib().mq_moe_combine(y_.data_ptr(), inv_.data_ptr() if inv_ is not None else None,
+    rc = _lib.lib().mq_moe_combine(y_.data_ptr(), M,
+                                   inv_.data_ptr() if inv_ is not None else None,
                                    w_.data_ptr(), out.data_ptr(), rows, top_k, N,
                                    _dtype_code(y.dtype, y.dtype), _stream_ptr(out))
     _lib.check(rc, "moe_combine")
@@ -450,6 +632,6 @@ def launch_count() -> int:
     return _lib.launch_count()
 
 
-__all__: Sequence[str] = ("dequantize", "quantized_matmul", "quantized_matmul_prepared",
+__all__: Sequence[str] = ("quantize", "dequantize", "quantized_matmul", "quantized_matmul_prepared",
                           "PreparedWeights", "gather_qmm", "gather_glu", "moe_combine",
                           "launch_count")

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version(lib):
-    assert lib.mq_version() == 1
+    assert lib.mq_version() == 2
 
 
 FAKE = 256  # aligned, never dereferenced: validation fails before any HIP call
@@ -66,7 +66,7 @@ def _qmm(lib, **kw):
     (dict(gs=48), -1, "group_size"),
     (dict(K=200), -1, "multiple of group_size"),
     (dict(bits=7), -1, "bits"),
-    (dict(bits=3), -2, "not implemented"),
+    (dict(bits=3), -2, "no matmul kernel"),
     (dict(transpose=0), -2, "transpose"),
     (dict(dtype=2), -2, "float32"),
     (dict(dtype=9), -1, "dtype"),
@@ -115,20 +115,45 @@ def test_dequant_argument_validation(lib):
     assert rc == -1
     rc = lib.mq_dequantize(FAKE, FAKE, FAKE, FAKE + 2, 4, 256, 64, 4, 0, None)
     assert rc == -1 and "aligned" in lib.mq_last_error().decode()
+    # every MLX width validates (no rows: nothing is launched)
+    for bits in (2, 3, 4, 5, 6, 8):
+        assert lib.mq_dequantize(FAKE, FAKE, FAKE, FAKE, 0, 256, 64, bits, 0, None) == 0
+    assert lib.mq_dequantize(FAKE, FAKE, FAKE, FAKE, 4, 256, 64, 7, 0, None) == -1
+
+
+def test_quantize_argument_validation(lib):
+    q = lib.mq_quantize
+    assert q(FAKE, FAKE, FAKE, FAKE, 0, 256, 64, 3, 0, None) == 0
+    assert q(FAKE, FAKE, FAKE, FAKE, 0, 256, 64, 6, 2, None) == 0
+    rc = q(FAKE, FAKE, FAKE, FAKE, 4, 256, 64, 7, 0, None)
+    assert rc == -1 and "bits" in lib.mq_last_error().decode()
+    rc = q(FAKE, FAKE, FAKE, FAKE, 4, 200, 64, 4, 0, None)
+    assert rc == -1 and "multiple of group_size" in lib.mq_last_error().decode()
+    rc = q(FAKE, FAKE + 4, FAKE, FAKE, 4, 256, 64, 4, 0, None)
+    assert rc == -1 and "aligned" in lib.mq_last_error().decode()
+    rc = q(FAKE, None, FAKE, FAKE, 4, 256, 64, 4, 0, None)
+    assert rc == -1
+    rc = q(FAKE, FAKE, FAKE, None, 4, 256, 64, 4, 0, None)
+    assert rc == -1 and "biases" in lib.mq_last_error().decode()
 
 
 def test_combine_argument_validation(lib):
-    rc = lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 4, 0, 64, 0, None)
+    rc = lib.mq_moe_combine(FAKE, 8, None, FAKE, FAKE, 4, 0, 64, 0, None)
     assert rc == -1 and "top_k" in lib.mq_last_error().decode()
-    rc = lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 4, 2, 60, 0, None)
+    rc = lib.mq_moe_combine(FAKE, 8, None, FAKE, FAKE, 4, 2, 60, 0, None)
     assert rc == -2 and "N % 8" in lib.mq_last_error().decode()
-    rc = lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 4, 2, 64, 2, None)
+    rc = lib.mq_moe_combine(FAKE, 8, None, FAKE, FAKE, 4, 2, 64, 2, None)
     assert rc == -2
-    rc = lib.mq_moe_combine(FAKE + 2, None, FAKE, FAKE, 4, 2, 64, 0, None)
+    rc = lib.mq_moe_combine(FAKE + 2, 8, None, FAKE, FAKE, 4, 2, 64, 0, None)
     assert rc == -1 and "aligned" in lib.mq_last_error().decode()
-    rc = lib.mq_moe_combine(None, None, FAKE, FAKE, 4, 2, 64, 0, None)
+    rc = lib.mq_moe_combine(None, 8, None, FAKE, FAKE, 4, 2, 64, 0, None)
     assert rc == -1
-    assert lib.mq_moe_combine(FAKE, None, FAKE, FAKE, 0, 2, 64, 0, None) == 0
+    # without inv, y must hold every (token, k) row
+    rc = lib.mq_moe_combine(FAKE, 7, None, FAKE, FAKE, 4, 2, 64, 0, None)
+    assert rc == -1 and "y_rows" in lib.mq_last_error().decode()
+    rc = lib.mq_moe_combine(FAKE, -1, FAKE, FAKE, FAKE, 4, 2, 64, 0, None)
+    assert rc == -1
+    assert lib.mq_moe_combine(FAKE, 8, None, FAKE, FAKE, 0, 2, 64, 0, None) == 0
 
 
 def test_ops_refuse_cpu_tensors():
@@ -187,13 +212,17 @@ class _FakeLib:
         self.calls.append(("deq", dict(N=N, K=K, gs=gs, bits=bits, dtype=dtype)))
         return 0
 
-    def mq_moe_combine(self, y, inv, w, out, rows, top_k, N, dtype, stream):
+    def mq_quantize(self, w, wq, s, b, N, K, gs, bits, dtype, stream):
+        self.calls.append(("quant", dict(N=N, K=K, gs=gs, bits=bits, dtype=dtype)))
+        return 0
+
+    def mq_moe_combine(self, y, y_rows, inv, w, out, rows, top_k, N, dtype, stream):
         n = rows * top_k
         read_i = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
                                                  shape=(n,)).copy()
         read_f = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)),
                                                  shape=(n,)).copy()
-        self.calls.append(("combine", dict(rows=rows, top_k=top_k, N=N, dtype=dtype,
+        self.calls.append(("combine", dict(rows=rows, top_k=top_k, N=N, dtype=dtype, y_rows=y_rows,
                                            inv=read_i(inv) if inv else None, w=read_f(w))))
         return 0
 
@@ -230,16 +259,94 @@ def test_qmm_contract_errors(fake):
     with pytest.raises(ValueError, match="requires biases"):
         mlxturbo_amd.quantized_matmul(x, w, s, None)
     with pytest.raises(NotImplementedError):
-        mlxturbo_amd.quantized_matmul(x, w, s, b, transpose=False)
-    with pytest.raises(NotImplementedError):
         mlxturbo_amd.quantized_matmul(x, w, s, b, mode="mxfp4")
     with pytest.raises(ValueError, match="does not match"):
         mlxturbo_amd.quantized_matmul(x[:, :256], w, s, b)
     with pytest.raises(ValueError, match="scales shape"):
         mlxturbo_amd.quantized_matmul(x, w, s, b, group_size=32)
-    with pytest.raises(NotImplementedError, match="differs"):
-        mlxturbo_amd.quantized_matmul(x.half(), w, s, b)
+    with pytest.raises(ValueError, match="bits"):
+        mlxturbo_amd.quantized_matmul(x, w, s, b, bits=7)
     assert fake.calls == []
+
+
+def test_qmm_without_kernel_composes_dequantize_and_gemm(fake):
+    """Configurations the matmul kernels do not take run as the library's
+    dequantize (in MLX's promoted dtype) plus one GEMM, never raising."""
+    w, s, b = _qweights(48, 512)
+    x = torch.zeros(4, 512, dtype=torch.bfloat16)
+    # fp16 activations over bf16 scales: promoted to float32
+    out = mlxturbo_amd.quantized_matmul(x.half(), w, s, b)
+    assert out.shape == (4, 48) and out.dtype == torch.float32
+    assert fake.calls[-1] == ("deq", dict(N=48, K=512, gs=64, bits=4, dtype=2))
+    # float32 activations
+    out = mlxturbo_amd.quantized_matmul(x.float(), w, s, b)
+    assert out.dtype == torch.float32
+    # transpose=False: w [K, N*bits/32] quantized along N
+    wt, st, bt = _qweights(512, 128)                      # K=512 rows, N=128
+    out = mlxturbo_amd.quantized_matmul(x, wt, st, bt, transpose=False)
+    assert out.shape == (4, 128) and out.dtype == torch.bfloat16
+    assert fake.calls[-1] == ("deq", dict(N=512, K=128, gs=64, bits=4, dtype=0))
+    # 3-bit codes
+    w3, s3, b3 = _qweights(48, 512, bits=3)
+    out = mlxturbo_amd.quantized_matmul(x, w3, s3, b3, bits=3)
+    assert out.shape == (4, 48)
+    assert fake.calls[-1] == ("deq", dict(N=48, K=512, gs=64, bits=3, dtype=0))
+    assert all(k == "deq" for k, _ in fake.calls)
+
+
+def test_quantize_shapes(fake):
+    w = torch.zeros(3, 48, 512, dtype=torch.bfloat16)
+    wq, s, b = mlxturbo_amd.quantize(w, group_size=64, bits=6)
+    assert wq.shape == (3, 48, 512 * 6 // 32) and wq.dtype == torch.uint32
+    assert s.shape == b.shape == (3, 48, 8) and s.dtype == torch.bfloat16
+    assert fake.calls[-1] == ("quant", dict(N=144, K=512, gs=64, bits=6, dtype=0))
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        mlxturbo_amd.quantize(w[..., :100])
+    with pytest.raises(ValueError, match="bfloat16, float16 or float32"):
+        mlxturbo_amd.quantize(w.to(torch.int32))
+
+
+def test_gather_more_than_16_rows_per_pair_is_one_row_pairs(fake):
+    T, top, E, N, K, M = 3, 2, 8, 32, 256, 20
+    w, s, b = _qweights(N, K, E=E)
+    x = torch.zeros(T, M, K, dtype=torch.bfloat16)
+    idx = torch.tensor([[1, 4], [0, 4], [7, 2]], dtype=torch.int32)
+    out = mlxturbo_amd.gather_qmm(x[:, None], w, s, b, rhs_indices=idx)
+    assert out.shape == (T, top, M, N)
+    kind, c = fake.calls[-1]
+    assert kind == "gather" and len(fake.calls) == 1
+    assert (c["P"], c["B"], c["M"]) == (T * top * M, T * M, 1)
+    pair_lhs = np.repeat(np.arange(T), top)
+    np.testing.assert_array_equal(c["lhs"], (pair_lhs[:, None] * M + np.arange(M)).reshape(-1))
+    np.testing.assert_array_equal(c["rhs"], np.repeat(idx.reshape(-1).numpy(), M))
+
+
+def test_gather_many_experts_runs_in_slices(fake):
+    P, E, N, K = 300, 4096 + 5, 32, 256
+    w, s, b = _qweights(N, K, E=E)
+    x = torch.zeros(P, 1, K, dtype=torch.bfloat16)
+    idx = torch.tensor(np.random.default_rng(0).integers(0, E, P), dtype=torch.int32)
+    mlxturbo_amd.gather_qmm(x, w, s, b, rhs_indices=idx)
+    assert [k for k, _ in fake.calls] == ["gather"] * 3
+    want = idx.numpy()
+    for (_, c), e0 in zip(fake.calls, (0, 2048, 4096)):
+        e1 = min(E, e0 + 2048)
+        assert c["E"] == e1 - e0
+        inside = (want >= e0) & (want < e1)
+        np.testing.assert_array_equal(c["rhs"], np.where(inside, want - e0, -1))
+
+
+def test_gather_without_kernel_composes_per_expert(fake):
+    E, N, K = 4, 32, 256
+    w, s, b = _qweights(N, K, E=E, bits=5)
+    x = torch.zeros(6, 1, K, dtype=torch.bfloat16)
+    idx = torch.tensor([2, 0, 2, 9, 3, -1], dtype=torch.int32)   # 9 and -1: zero rows
+    out = mlxturbo_amd.gather_qmm(x, w, s, b, rhs_indices=idx, bits=5)
+    assert out.shape == (6, 1, N)
+    kinds = [k for k, _ in fake.calls]
+    assert kinds == ["deq"] * 3                           # experts 0, 2, 3 once each
+    assert all(c["bits"] == 5 and (c["N"], c["K"]) == (N, K) for _, c in fake.calls)
+    assert torch.all(out[3] == 0) and torch.all(out[5] == 0)
 
 
 def test_gather_broadcasts_like_switchglu(fake):
@@ -299,6 +406,7 @@ def test_combine_passes_indices_and_weights(fake):
     _, c = fake.calls[-1]
     np.testing.assert_array_equal(c["inv"], inv.numpy())
     np.testing.assert_array_equal(c["w"], w.numpy().astype(np.float32))
+    assert c["y_rows"] == rows * top_k
     mlxturbo_amd.moe_combine(y, None, w, rows, top_k)
     assert fake.calls[-1][1]["inv"] is None
     with pytest.raises(ValueError):

@@ -243,6 +243,34 @@ def test_prepared_weights_follow_buffer_changes():
     layer.scales.copy_(to_dev(s1, "bfloat16"))
     layer.biases.copy_(to_dev(b1, "bfloat16"))
     np.testing.assert_array_equal(bits16(layer(x)), first)
-    # a wrong activation dtype still raises the operator's error
-    with pytest.raises(NotImplementedError):
-        layer(x.half())
+    # another activation dtype takes the operator's composed route (MLX
+    # promotes fp16 x over bf16 scales to float32)
+    out = layer(x.half())
+    assert out.dtype == torch.float32 and out.shape == (3, N)
+    ref = O.quantized_matmul_ref(O.to_f32(bits16(x.half()), "float16"), w1,
+                                 O.to_f32(s1, "bfloat16"), O.to_f32(b1, "bfloat16"), 64, 4,
+                                 "float32")
+    res = O.check_output(from_dev(out), ref, "float32")
+    assert res["ok"], res
+
+
+@pytest.mark.gpu
+def test_prepared_weights_see_in_place_writes_to_copied_buffers():
+    """A weight buffer the prepared path has to copy (misaligned view) and
+    that is then written in place: the next forward uses the new values."""
+    rng = np.random.default_rng(91)
+    N, K = 64, 256
+    w1, s1, b1 = quantized(rng, N, K)
+    w2, _, _ = quantized(rng, N, K)
+    base = torch.zeros(N * K // 8 + 1, dtype=torch.int32, device="cuda")
+    base[1:].copy_(to_dev(w1).view(torch.int32).reshape(-1))
+    wview = base[1:].view(N, K // 8).view(torch.uint32)        # 4 bytes off 16-byte alignment
+    assert wview.data_ptr() % 16
+    layer = QuantizedLinear(wview, to_dev(s1, "bfloat16"), to_dev(b1, "bfloat16"))
+    x = to_dev(act(rng, (2, K)), "bfloat16")
+    first = bits16(layer(x))
+    base[1:].copy_(to_dev(w2).view(torch.int32).reshape(-1))   # in place, same storage
+    second = bits16(layer(x))
+    want = bits16(mq.quantized_matmul(x, to_dev(w2), to_dev(s1, "bfloat16"), to_dev(b1, "bfloat16")))
+    np.testing.assert_array_equal(second, want)
+    assert not np.array_equal(first, second)

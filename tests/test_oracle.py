@@ -324,29 +324,7 @@ def test_gather_glu_zero_gate_and_up_linearity():
     assert np.all(np.sign(out) == np.sign(g * O.gather_qmm_ref(x, *up, lhs, rhs)))
 
 
-# ----------------------------------------------------------------- quantize
-
-def test_quantize_invariants():
-    """Parity with mx.quantize is unpinned (source absent); invariants only."""
-    rng = np.random.default_rng(7)
-    for bits in (4, 8):
-        w = (rng.standard_normal((8, 256)) * 0.02).astype(np.float32)
-        w[0, :64] = 0.0                                   # a constant-zero group
-        wq, s, b = O.quantize(w, 64, bits, "bfloat16")
-        codes = O.unpack(wq, bits)
-        qmax = (1 << bits) - 1
-        assert codes.max() <= qmax
-        deq = O.bf16_to_f32(O.dequantize(wq, s, b, 64, bits, "bfloat16"))
-        sf = np.repeat(np.abs(O.bf16_to_f32(s)), 64, axis=1)
-        bf = np.repeat(np.abs(O.bf16_to_f32(b)), 64, axis=1)
-        err = np.abs(deq - w)
-        # half a step, plus the bf16 rounding of s (times q), of b and of the result
-        tol = 0.5 * sf + qmax * sf * 2**-8 + bf * 2**-8 + np.abs(w) * 2**-7 + 1e-12
-        inner = (codes > 0) & (codes < qmax)
-        assert np.all(err[inner] <= tol[inner])
-        # the edge-exact scale may clip the far end by less than one more step
-        assert np.all(err <= tol + sf)
-        np.testing.assert_array_equal(deq[0, :64], 0.0)
+# quantize and the 3/5/6-bit packing are pinned in test_quantize_oracle.py
 
 
 # --------------------------------------------------------------- tolerance
@@ -361,6 +339,31 @@ def test_tolerance_accepts_reordered_fp32_sum():
     c = cref.qmm(x, wq, s, b, 64, 4)
     out = O.bf16_to_f32(O.bf16_bits(c))
     assert O.check_output(out, ref)["ok"]
+
+
+def test_float32_tolerance_accepts_reordered_sums_and_rejects_bf16():
+    """The composed routes' float32 outputs: a float32 GEMM summing in any
+    order passes; the same product rounded through bf16 (a route that
+    silently computed in 16 bits) fails; so does a dropped bias."""
+    rng = np.random.default_rng(31)
+    M, N, K, gs = 3, 96, 512, 64
+    wq, s, b = O.quantize((rng.standard_normal((N, K)) * 0.02).astype(np.float32), gs, 4,
+                          "float32")
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ref = O.quantized_matmul_ref(x, wq, s, b, gs, 4, "float32")
+    deq = O.dequantize(wq, s, b, gs, 4, "float32")
+    # float32 accumulation in two different orders
+    fwd = np.zeros((M, N), np.float32)
+    for k in range(K):
+        fwd += x[:, k:k + 1] * deq[:, k][None, :]
+    blocked = sum((x[:, i:i + 64] @ deq[:, i:i + 64].T).astype(np.float32)
+                  for i in range(K - 64, -1, -64))
+    assert O.check_output(fwd, ref, "float32")["ok"]
+    assert O.check_output(blocked, ref, "float32")["ok"]
+    through_bf16 = O.bf16_to_f32(O.bf16_bits(ref))
+    assert not O.check_output(through_bf16, ref, "float32")["ok"]
+    nob = O.quantized_matmul_ref(x, wq, s, np.zeros_like(b), gs, 4, "float32")
+    assert not O.check_output(nob, ref, "float32")["ok"]
 
 
 def test_tolerance_rejects_planted_mistakes():
