@@ -146,6 +146,25 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
                   void* hip_stream);
 
 /*
+ * mq_gather_qmm without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference (MLX
+ * allocates its own temporaries).  The workspace is a static device array of
+ * 4 MiB (MQ_GATHER_NOALLOC_SCRATCH_BYTES) that each GPU holds until the
+ * process ends; it takes calls whose mq_gather_qmm_workspace_size(P, M) fits,
+ * i.e. up to 262142 pairs, and larger ones return MQ_EINVAL.  The call
+ * allocates nothing.  Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other streams, other threads) race: order them,
+ * e.g. on one stream.  Arguments and results are those of mq_gather_qmm.
+ */
+#define MQ_GATHER_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+int mq_gather_qmm_noalloc(const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const int32_t* lhs_indices,
+                          const int32_t* rhs_indices, void* out, int64_t P, int64_t B, int64_t M,
+                          int64_t N, int64_t K, int64_t E, int group_size, int bits, int dtype,
+                          int sorted_indices, void* hip_stream);
+
+/*
  * Fused MoE gate+up+SiLU at decode / verify widths:
  *   out[p, M, N] = silu(x[lhs[p]] . dequantize(w_gate[rhs[p]])^T)
  *                * (x[lhs[p]] . dequantize(w_up[rhs[p]])^T)

@@ -33,6 +33,7 @@ EXPORTED = (
     "mq_quantized_matmul_ws",
     "mq_gather_qmm_workspace_size",
     "mq_gather_qmm",
+    "mq_gather_qmm_noalloc",
     "mq_gather_glu",
     "mq_moe_combine",
 )
@@ -73,6 +74,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_gather_qmm.restype = _int
     lib.mq_gather_qmm.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]
+    lib.mq_gather_qmm_noalloc.restype = _int
+    lib.mq_gather_qmm_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                          _i64, _i64, _i64, _int, _int, _int, _int, _vp]
     lib.mq_gather_glu.restype = _int
     lib.mq_gather_glu.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _int, _int, _int, _vp, ctypes.c_size_t,

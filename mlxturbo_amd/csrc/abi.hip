@@ -4,6 +4,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/mlxturbo_amd.h"
@@ -73,6 +74,41 @@ int dispatch_16(int dtype, int bits, int gs, Args... args) {
   MQ_CASE(mq::kF16, 8, 64) MQ_CASE(mq::kF16, 8, 32) MQ_CASE(mq::kF16, 8, 128)
 #undef MQ_CASE
   return mq::kStatusUnsupported;
+}
+
+// ---- scratch of mq_gather_qmm_noalloc --------------------------------------
+// A file-scope device array holds the gather workspace (the prep kernel's
+// segment tables) for callers that cannot allocate.  Each GPU holds its own
+// copy until the process ends.  In host code `scratch` is only a stand-in
+// for the symbol: its device address on the current device comes from
+// hipGetSymbolAddress, resolved once per device and kept in g_scratch.
+constexpr size_t kScratchBytes = MQ_GATHER_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+
+// Device address of the current device's scratch, or a status.
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MQ_EUNSUPPORTED, "device %d is beyond the %d devices with a scratch slot", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : MQ_EINVAL,
+                  "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return MQ_OK;
 }
 
 }  // namespace
@@ -223,6 +259,29 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
   if (e != hipSuccess) return fail((int)e, "gather_qmm: launch failed: %s", hipGetErrorString(e));
   g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
   return MQ_OK;
+}
+
+int mq_gather_qmm_noalloc(const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const int32_t* lhs_indices,
+                          const int32_t* rhs_indices, void* out, int64_t P, int64_t B, int64_t M,
+                          int64_t N, int64_t K, int64_t E, int group_size, int bits, int dtype,
+                          int sorted_indices, void* hip_stream) {
+  if (P < 0 || M < 0)
+    return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld", (long long)P, (long long)M);
+  const size_t need = mq::gather_workspace_bytes(P, M);
+  if (need > kScratchBytes)
+    return fail(MQ_EINVAL,
+                "gather_qmm_noalloc: %lld pairs need %zu bytes of workspace; the static scratch "
+                "holds %zu (use mq_gather_qmm with a workspace)",
+                (long long)P, need, kScratchBytes);
+  void* ws = nullptr;
+  if (need) {
+    const int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+  }
+  return mq_gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices, out, P, B, M, N, K, E,
+                       group_size, bits, dtype, sorted_indices, ws, need ? kScratchBytes : 0,
+                       hip_stream);
 }
 
 int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate,
