@@ -9,8 +9,10 @@
  *
  * Formats (MLX affine quantization, the format the reference's kernels read:
  * mlxturbo/fast_qmm.py:93-106, kernels/_steel_flat.py:1152-1256):
- *   w       uint32 [N, K*bits/32]   code j of word i = element i*(32/bits)+j,
- *                                   at bit bits*j (low bits first)
+ *   w       uint32 [N, K*bits/32]   a little-endian bitstream per row: code k
+ *                                   at bits [bits*k, bits*k + bits); for 4/8
+ *                                   bits, code j of word i = element
+ *                                   i*(32/bits)+j at bit bits*j
  *   scales  T [N, K/group_size]     T = the activation dtype
  *   biases  T [N, K/group_size]
  *   deq     T(float(s)*q + float(b)), rounded to nearest even
@@ -89,7 +91,9 @@ int mq_quantize(const void* w, uint32_t* wq, void* scales, void* biases, int64_t
  * qmv_wide_nocap.py:240-288) and qmm_wide (kernels/qmm_wide.py:456-502).
  * x and out are row-major with leading dimension K and N.
  * bits in {4, 8}; group_size in {32, 64, 128}; dtype bfloat16 or float16;
- * transpose = 0 returns MQ_EUNSUPPORTED (the reference never accelerates it).
+ * other widths, float32 and transpose = 0 return MQ_EUNSUPPORTED (the
+ * reference never accelerates them; the Python layer composes mq_dequantize
+ * and a GEMM for them, as the reference falls back to stock MLX).
  */
 int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
                         const void* biases, void* out, int64_t M, int64_t N, int64_t K,

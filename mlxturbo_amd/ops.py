@@ -10,15 +10,19 @@ MLX 0.32's operators as the reference calls them:
   QuantizedSwitchLinear (mlxturbo/fused.py:2389-2394, 3105-3116)
 * ``dequantize(w, scales, biases, group_size, bits, mode)`` - mx.dequantize
   (bench/test_qmm_wide_shapes.py:35-42)
+* ``quantize(w, group_size, bits, mode)`` - mx.quantize (rebit.py:119,
+  kernels/moe_verify_gather.py:887)
 * ``gather_glu`` - fused MoE gate+up+SiLU (kernels/moe_glu.py:145-168)
 * ``moe_combine`` - MoE unsort + router weight + top-k sum
   (kernels/moe_combine.py:160-195)
 
-Errors: genuinely invalid arguments raise ``ValueError`` as MLX does;
-configurations the reference never accelerates and this build does not
-implement (``transpose=False``, non-affine modes, bits other than 4/8,
-float32 activations) raise ``NotImplementedError``.  There is no CPU or
-PyTorch fallback: every result comes from a HIP kernel.
+Errors and coverage: genuinely invalid arguments raise ``ValueError`` as MLX
+does; non-affine modes raise ``NotImplementedError``.  Every affine
+configuration returns a result, as the reference's wrappers do by falling
+back to ``mx.quantized_matmul`` (fast_qmm.py:356-362): the kernels take 4/8
+bits with bf16/fp16 activations in the scales' dtype, and the rest (other
+widths, ``transpose=False``, float32 or mixed dtypes) runs as this library's
+bit-exact dequantize plus one GPU GEMM.  Nothing runs on the CPU.
 """
 
 from __future__ import annotations
