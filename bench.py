@@ -68,7 +68,8 @@ def parse():
                         "wide<M> (configs[2]), gather_<proj>_<routing>_T<T> (configs[3] decode), "
                         "gather_glu_<routing>_T<T> (fused gate+up+SiLU), qmv<M> / qmvdown<M> "
                         "(configs[1] skinny), combine (MoE combine, 2048 x top-8 x 2048), "
-                        "gather_prefill_<proj>_<routing> (2048 tokens)")
+                        "gather_prefill_<proj>_<routing> (2048 tokens), "
+                        "moe_layer_<routing>_T<T> (whole decode MoE layer)")
     return p.parse_args()
 
 
@@ -95,6 +96,9 @@ def run_case(torch, mq, case: str) -> dict:
         proj, routing = case[len("gather_prefill_"):].rsplit("_", 1)
         NN, KK = banks[proj]
         return {"case": case, **measure_gather_prefill(torch, mq, 2048, NN, KK, routing, 20, 3)}
+    if case.startswith("moe_layer_"):
+        routing, t = case[len("moe_layer_"):].rsplit("_T", 1)
+        return {"case": case, **measure_moe_layer(torch, mq, int(t), routing, 100, 5)}
     if case.startswith("gather_"):
         body, t = case[len("gather_"):].rsplit("_T", 1)
         proj, routing = body.rsplit("_", 1)
@@ -244,6 +248,49 @@ def measure_gather(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, n
             "distinct_experts": round(uniq, 1)}
 
 
+def measure_moe_layer(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidden=2048,
+                      inter=512, nroute=64, seed=8):
+    """One whole decode MoE layer of configs[3] (SwitchGLU with the fused
+    gate+up+SiLU route and router scores): gather_glu, the down gather_qmm
+    and the combine epilogue, three launches.  Algorithmic bytes: each
+    distinct expert's gate, up and down weights once, plus activations."""
+    from mlxturbo_amd import nn as mqnn
+    rng = np.random.default_rng(seed + T)
+    routes = [(zipf_routing(rng, T, top_k, E) if routing == "zipf" else
+               np.stack([rng.choice(E, size=top_k, replace=False) for _ in range(T)]).astype(np.int32))
+              for _ in range(nroute)]
+
+    def bank(N, K, s):
+        (w, sc, b), = make_weights(torch, E * N, K, 1, seed=s)
+        return mqnn.QuantizedSwitchLinear(w.view(E, N, -1), sc.view(E, N, -1), b.view(E, N, -1))
+
+    layer = mqnn.SwitchGLU(bank(inter, hidden, seed), bank(inter, hidden, seed + 1),
+                           bank(hidden, inter, seed + 2), fuse_gate_up=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((T, hidden), device="cuda", generator=g).to(torch.bfloat16)
+    scores = torch.softmax(torch.randn((T, top_k), device="cuda", generator=g), -1)
+    idx = [torch.from_numpy(r).cuda() for r in routes]
+
+    def per_expert(N, K):
+        return N * K // 2 + 4 * N * (K // 64)
+
+    pe = 2 * per_expert(inter, hidden) + per_expert(hidden, inter)
+    act = 2 * T * hidden * 2 + 2 * T * top_k * (inter + hidden) * 2 + 4 * T * top_k
+    nbytes = [len(np.unique(r)) * pe + act for r in routes]
+
+    def fn(i):
+        layer(x, idx[i % nroute], scores)
+
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    avg_bytes = sum(nbytes[i % nroute] for i in range(steps)) / steps
+    del layer
+    torch.cuda.empty_cache()
+    return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
+            "distinct_experts": round(sum(len(np.unique(r)) for r in routes) / nroute, 1),
+            "launches": 3}
+
+
 def measure_gather_prefill(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, seed=5):
     """The prefill form of configs[3]: T tokens x top_k experts as one
     gather_qmm (x (P, 1, K) sorted by expert, sorted_indices=True, as mlx-lm's
@@ -310,8 +357,9 @@ def measure_dequant(torch, mq, N, K, steps, warmup):
 
 def measure_stream_read(torch, nbytes, steps=200, warmup=10):
     """The second roofline denominator: a plain streaming read of `nbytes`
-    (mlxturbo_amd/csrc/read_probe.hip, contiguous 16-byte loads, eight
-    workgroups per CU) over rotated copies that exceed the MALL, timed the
+    (mlxturbo_amd/csrc/read_probe.hip, contiguous non-temporal 16-byte
+    loads, four workgroups per CU: the fastest of a sweep over cache
+    policies and grids) over rotated copies that exceed the MALL, timed the
     same way as the kernel (one HIP graph of `steps` launches).  What one
     MI355X reads per second at this size, launch and ramp included."""
     import ctypes
@@ -324,7 +372,7 @@ def measure_stream_read(torch, nbytes, steps=200, warmup=10):
     R = copies_for(nbytes)
     bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(R)]
     sink = torch.empty(1024, dtype=torch.uint8, device="cuda")
-    wgs = 8 * torch.cuda.get_device_properties(0).multi_processor_count
+    wgs = 4 * torch.cuda.get_device_properties(0).multi_processor_count
 
     def fn(i):
         rc = lib.mq_read_probe(bufs[i % R].data_ptr(), nbytes, sink.data_ptr(), wgs,
@@ -336,8 +384,9 @@ def measure_stream_read(torch, nbytes, steps=200, warmup=10):
     del bufs
     torch.cuda.empty_cache()
     return {"us": round(per_step * 1e6, 2), "GBps": round(nbytes / per_step / 1e9, 1),
-            "bytes": nbytes, "how": "plain 16-byte loads, 8 workgroups per CU, rotated copies, "
-                                    "one HIP graph (mlxturbo_amd/csrc/read_probe.hip)"}
+            "bytes": nbytes, "how": "plain non-temporal 16-byte loads, 4 workgroups per CU, "
+                                    "rotated copies, one HIP graph "
+                                    "(mlxturbo_amd/csrc/read_probe.hip)"}
 
 
 def copy_probe(torch, nbytes, reps=4):
@@ -352,41 +401,96 @@ def copy_probe(torch, nbytes, reps=4):
     torch.cuda.empty_cache()
 
 
+def cpu_threads() -> tuple:
+    """(threads used, cores the host's affinity mask shows).  The GPU box
+    grants one GPU's share of the host (OMP_NUM_THREADS, 16 there) whatever
+    the affinity mask shows, so the OpenMP legs use that share."""
+    affinity = len(os.sched_getaffinity(0))
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        share = 0
+    return (min(share, affinity) if share > 0 else affinity), affinity
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, seconds, max_reps=200):
+    fn()                                                  # warm-up (page faults, thread pool)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= max_reps:
+            return el / reps, reps
+
+
+def torch_cpu_qmm(torch, x, w, s, b, gs=64, bits=4):
+    """torch-CPU dequantize -> matmul over MLX-format tensors (the second
+    MLX-CPU substitute): codes unpacked with shifts and masks, s*q + b in
+    float32 rounded to bf16 per weight, then a float32 matmul."""
+    per = 32 // bits
+    shifts = torch.arange(per, dtype=torch.int64) * bits
+    codes = ((w.to(torch.int64).unsqueeze(-1) >> shifts) & ((1 << bits) - 1))
+    codes = codes.reshape(w.shape[0], -1).to(torch.float32)
+    deq = (codes.view(w.shape[0], -1, gs) * s.float().unsqueeze(-1)
+           + b.float().unsqueeze(-1)).reshape(w.shape[0], -1)
+    deq = deq.to(torch.bfloat16).float()
+    return (x.float() @ deq.T).to(torch.bfloat16)
+
+
 def cpu_baseline(N, K, seconds):
     """The C restatement of the oracle (bf16-exact dequant, fp32 accumulation,
-    OpenMP) on this host's cores, bounded to about `seconds`."""
+    OpenMP) on this host's cores, bounded to about `seconds`, with all of the
+    box's threads and with one; and a torch-CPU dequantize -> matmul of the
+    same call.  MLX's CPU quantized_matmul is not installable here."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import cref
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    import torch
+    threads, affinity = cpu_threads()
     rng = np.random.default_rng(3)
     w = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
     s = np.full((N, K // 64), 0x3B00, np.uint16)
     b = np.full((N, K // 64), 0xBC00, np.uint16)
     x = np.full((1, K), 0x3F80, np.uint16)
-    cref.qmm(x, w, s, b, 64, 4, threads=threads)            # warm-up (page faults, OpenMP pool)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        cref.qmm(x, w, s, b, 64, 4, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 200:
-            break
-    per = el / reps
-    cpu_model = ""
+    per, reps = _timed(lambda: cref.qmm(x, w, s, b, 64, 4, threads=threads), seconds)
+    per1, reps1 = _timed(lambda: cref.qmm(x, w, s, b, 64, 4, threads=1), seconds / 2, 20)
+    tw = torch.from_numpy(w.view(np.int32))
+    ts = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16)
+    tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    tx = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    nt0 = torch.get_num_threads()
+    torch.set_num_threads(threads)
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+        per_t, reps_t = _timed(lambda: torch_cpu_qmm(torch, tx, tw, ts, tb), seconds / 2, 50)
+    finally:
+        torch.set_num_threads(nt0)
+    nbytes = algo_bytes(1, N, K)
+    model = cpu_model()
     return {
-        "value": round(algo_bytes(1, N, K) / per / 1e9, 3),
+        "value": round(nbytes / per / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": model,
+        "host_affinity_cores": affinity,
+        "one_thread": {"value": round(nbytes / per1 / 1e9, 3), "unit": "GB/s",
+                       "ms_per_call": round(per1 * 1e3, 2), "reps": reps1},
+        "torch_cpu": {"value": round(nbytes / per_t / 1e9, 3), "unit": "GB/s",
+                      "ms_per_call": round(per_t * 1e3, 2), "reps": reps_t, "threads": threads,
+                      "what": "torch-CPU dequantize (bf16-rounded per weight) -> fp32 matmul"},
         "sample": (f"{reps} full M=1 calls K={K} N={N} (C oracle oracle/qmm_oracle.c, OpenMP "
-                   f"{threads} threads, {per * 1e3:.1f} ms/call) on {cpu_model or 'host CPU'}; "
+                   f"{threads} threads = the box's CPU share, {per * 1e3:.1f} ms/call); "
+                   f"1 thread {per1 * 1e3:.1f} ms/call; torch-CPU {per_t * 1e3:.1f} ms/call; "
                    "MLX's CPU quantized_matmul is not installable here"),
     }
 
@@ -397,7 +501,7 @@ def cpu_rows(seconds):
     `seconds` and scaled to the whole call; units as in the GPU sweep."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import cref
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads, _ = cpu_threads()
     rng = np.random.default_rng(5)
 
     def timed(fn):
@@ -523,6 +627,9 @@ def main():
                 # the same gate/up bytes through the fused gate+up+SiLU kernel
                 sweep[f"gather_glu_{routing}_T{T}"] = measure_gather(
                     torch, mq, T, 1024, 2048, routing, 100, 5, glu=True)
+                # the whole layer: gate+up+SiLU, down, router-weighted combine
+                sweep[f"moe_layer_{routing}_T{T}"] = measure_moe_layer(
+                    torch, mq, T, routing, 100, 5)
         # config 4 banks at prefill width (2048 tokens): expert-grouped MFMA tiles
         for routing in ("zipf", "uniform"):
             for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):

@@ -137,8 +137,11 @@ size_t mq_gather_qmm_workspace_size(int64_t P, int64_t M);
  * (kernels/moe_decode_fused.py:331-397, kernels/moe_verify_gather.py:453-875)
  * and prefill grouped GEMM (kernels/moe_grouped_gemm.py:913-1066).
  * x is [B, M, K]; w is [E, N, K*bits/32]; scales/biases [E, N, K/group_size];
- * lhs_indices may be NULL (then lhs[p] = p, requiring B == P); indices are
- * int32 device arrays of length P (the caller broadcasts them).  Pairs that
+ * lhs_indices may be NULL: then pair p reads x batch p / (P / B), which
+ * requires B to divide P (B == P: the identity; B == P / top_k: tokens
+ * (T, 1) broadcast against their expert indices (T, top_k), mlx-lm's
+ * SwitchGLU call, with no index table); indices are int32 device arrays of
+ * length P (the caller broadcasts them).  Pairs that
  * share an expert are computed together so each expert's weights are read
  * once per call.  sorted_indices = 1 promises rhs is non-decreasing.
  * workspace must hold mq_gather_qmm_workspace_size(P, M) bytes.

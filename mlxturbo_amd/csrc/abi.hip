@@ -236,9 +236,11 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
   if (P < 0 || M < 0 || E <= 0 || B < 0)
     return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
                 (long long)M, (long long)E, (long long)B);
-  if (!lhs_indices && B != P)
-    return fail(MQ_EINVAL, "lhs_indices=NULL requires B == P (B=%lld P=%lld)", (long long)B,
-                (long long)P);
+  if (!lhs_indices && P > 0 && (B <= 0 || P % B))
+    return fail(MQ_EINVAL,
+                "lhs_indices=NULL requires B to divide P (pair p reads x batch p / (P / B); "
+                "B=%lld P=%lld)",
+                (long long)B, (long long)P);
   if (dtype == MQ_FLOAT32)
     return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
   if (N > INT32_MAX || K > INT32_MAX || P > INT32_MAX || E > INT32_MAX || M > 16)
@@ -298,9 +300,11 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
   if (P < 0 || M < 0 || E <= 0 || B < 0)
     return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
                 (long long)M, (long long)E, (long long)B);
-  if (!lhs_indices && B != P)
-    return fail(MQ_EINVAL, "lhs_indices=NULL requires B == P (B=%lld P=%lld)", (long long)B,
-                (long long)P);
+  if (!lhs_indices && P > 0 && (B <= 0 || P % B))
+    return fail(MQ_EINVAL,
+                "lhs_indices=NULL requires B to divide P (pair p reads x batch p / (P / B); "
+                "B=%lld P=%lld)",
+                (long long)B, (long long)P);
   if (dtype == MQ_FLOAT32)
     return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
   if (N > INT32_MAX || K > INT32_MAX || P > INT32_MAX || E > INT32_MAX || M > 16)

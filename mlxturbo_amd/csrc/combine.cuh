@@ -18,6 +18,7 @@
 namespace mq {
 
 constexpr int kCombineMaxTopK = 64;
+constexpr int kCombineBatch = 8;
 
 template <int DT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y,
@@ -41,14 +42,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   float acc[8];
 #pragma unroll
   for (int v = 0; v < 8; ++v) acc[v] = 0.f;
-  for (int k = 0; k < top_k; ++k) {
-    if (s_row[k] < 0) continue;
-    const float wk = s_w[k];
-    const u32x4 p = *reinterpret_cast<const u32x4*>(y + (int64_t)s_row[k] * N + n);
+  // kCombineBatch rows in flight at once (a decode token's whole top-k): all
+  // loads of a batch are issued before the first is used, then the terms
+  // are added in k order
+  for (int k0 = 0; k0 < top_k; k0 += kCombineBatch) {
+    u32x4 p[kCombineBatch];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      acc[2 * v] = __builtin_fmaf(wk, T::to_f32((uint16_t)p[v]), acc[2 * v]);
-      acc[2 * v + 1] = __builtin_fmaf(wk, T::to_f32((uint16_t)(p[v] >> 16)), acc[2 * v + 1]);
+    for (int j = 0; j < kCombineBatch; ++j) {
+      const int r = k0 + j < top_k ? s_row[k0 + j] : -1;
+      p[j] = r >= 0 ? *reinterpret_cast<const u32x4*>(y + (int64_t)r * N + n)
+                    : (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) {
+      if (k0 + j >= top_k || s_row[k0 + j] < 0) continue;
+      const float wk = s_w[k0 + j];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        acc[2 * v] = __builtin_fmaf(wk, T::to_f32((uint16_t)p[j][v]), acc[2 * v]);
+        acc[2 * v + 1] = __builtin_fmaf(wk, T::to_f32((uint16_t)(p[j][v] >> 16)),
+                                        acc[2 * v + 1]);
+      }
     }
   }
   u32x4 o;

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   // key of a pair: its expert, or E when the expert or the x index is invalid
   auto key_of = [&](int p) {
     const int e = rhs[p];
-    const int xb = lhs ? lhs[p] : p;
+    const int xb = x_batch(lhs, p, P, B);
     return (e >= 0 && e < E && xb >= 0 && xb < B) ? e : E;
   };
 
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     __builtin_amdgcn_wave_barrier();
     if (lane < P && key == e && d >= 0 && d < R) {
       s_members[d] = lane;
-      s_xbase[d] = lhs ? lhs[lane] : lane;       // loaded with rhs by key_of: cache hit
+      s_xbase[d] = x_batch(lhs, lane, P, B);       // loaded with rhs by key_of: cache hit
     }
     if (t == 0) s_expert = e;
     __syncthreads();
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   if (!(ws == nullptr && P <= 64)) {
     if (t < 16) {
       const int p = s_members[t];
-      s_xbase[t] = p >= 0 ? (lhs ? lhs[p] : p) : 0;
+      s_xbase[t] = p >= 0 ? x_batch(lhs, p, P, B) : 0;
     }
     __syncthreads();
   }

@@ -36,7 +36,7 @@ constexpr int kThinBM = 64, kThinNT = 256;
 // 1-D grid of ceil(N / 256) x segment bound workgroups (tiles placed by
 // grouped_tile), 256 threads; segments of size class cls of the prep
 // tables in ws hold up to 64 / Mi pairs of one expert; pair p contributes
-// rows p*Mi .. p*Mi+Mi-1 and reads x batch lhs[p] (or p).  Segments of
+// rows p*Mi .. p*Mi+Mi-1 and reads x batch x_batch(lhs, p, P, B).  Segments of
 // out-of-range experts write zeros.  K % 64 == 0, B * Mi * K * 2 < 2^31.
 template <int DT, int BITS, int GS, int PS>
 __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
   if (t < BM) {
     if (t < rows) {
       const int p = perm[st0 + t / Mi], mi = t % Mi;
-      const int xb = lhs ? lhs[p] : p;
+      const int xb = x_batch(lhs, p, P, B);
       s_xoff[t] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
       s_orow[t] = p * Mi + mi;
     } else {

@@ -82,6 +82,14 @@ template <> struct T16<kF16> {
 __device__ __forceinline__ float half_lo(uint32_t v) { return (float)bitcast<f16x2>(v).x; }
 __device__ __forceinline__ float half_hi(uint32_t v) { return (float)bitcast<f16x2>(v).y; }
 
+// The x batch that gather pair p reads: lhs[p], or with no table p / (P / B)
+// (B divides P: each x batch serves P / B consecutive pairs, as when tokens
+// (T, 1) broadcast against their top-k expert indices (T, k); B == P is the
+// identity).
+__device__ __forceinline__ int x_batch(const int32_t* lhs, int p, int P, int B) {
+  return lhs ? lhs[p] : (B == P ? p : p / (P / B));
+}
+
 // Per-group dequant parameters for the fast path.
 struct GroupScale {
   float s24, s20;  // s * 2^24, s * 2^20

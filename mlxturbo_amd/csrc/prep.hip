@@ -54,7 +54,7 @@ __global__ __launch_bounds__(1024) void gather_prep_kernel(
   const bool staged = P <= kPrepLdsKeys;
   auto key_of = [&](int p) {
     const int e = rhs[p];
-    const int xb = lhs ? lhs[p] : p;
+    const int xb = x_batch(lhs, p, P, B);
     return (e >= 0 && e < E && xb >= 0 && xb < B) ? e : E;
   };
   if (staged) {

@@ -406,8 +406,8 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restric
 // One expert-grouped tile (prefill gather_qmm, reference moe_grouped_gemm.py:
 // 913-1066): segment seg of the prep tables in ws (up to BM / Mi pairs of one
 // expert, pairs sorted by expert) times the 256 columns from n0.  Pair p
-// contributes rows p*Mi .. p*Mi+Mi-1 of the output and reads x batch lhs[p]
-// (or p).  Segments of out-of-range experts write zeros.  s_xoff / s_orow
+// contributes rows p*Mi .. p*Mi+Mi-1 of the output and reads x batch
+// x_batch(lhs, p, P, B).  Segments of out-of-range experts write zeros.  s_xoff / s_orow
 // hold BM entries of LDS; B * Mi * K * 2 < 2^31.
 template <int DT, int BITS, int GS, int BM>
 __device__ __forceinline__ void grouped_body(
@@ -423,7 +423,7 @@ __device__ __forceinline__ void grouped_body(
   for (int r = t; r < BM; r += kWideNT) {
     if (r < rows) {
       const int p = perm[st0 + r / Mi], mi = r % Mi;
-      const int xb = lhs ? lhs[p] : p;
+      const int xb = x_batch(lhs, p, P, B);
       s_xoff[r] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
       s_orow[r] = p * Mi + mi;
     } else {

@@ -5,10 +5,12 @@
 // and ramp included, at the kernel's own byte count).
 //
 // Layout: workgroup g reads the contiguous chunk [g * chunk, (g + 1) * chunk)
-// with 16-byte loads, each lane keeping U loads in flight; the data are
-// folded into a register and written only if they equal a magic value, so
-// the loads cannot be dropped.  A grid of 8 workgroups per CU and U = 2 ran
-// fastest among contiguous and tiled patterns over 44-50 MB (8.0-8.7 us).
+// with 16-byte non-temporal loads, each lane keeping U loads in flight; the
+// data are folded into a register and written only if they equal a magic
+// value, so the loads cannot be dropped.  Swept over 50 MB-4.3 GB (default,
+// sc0, sc1 and nt cache policies; 4, 8 and 16 workgroups per CU; U = 2, 4):
+// nt with 4 workgroups per CU and U = 2 read fastest at every size (50 MB in
+// 8.85 us, 4.3 GB at 6.99 TB/s), 7-10% ahead of the default policy.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -17,6 +19,7 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256, kUnroll = 2;
+constexpr int kNonTemporal = 2;  // cache-policy bits of the buffer load: nt
 
 __global__ __launch_bounds__(kThreads) void read_probe_kernel(const char* __restrict__ p,
                                                               uint64_t bytes, uint64_t chunk,
@@ -32,7 +35,7 @@ __global__ __launch_bounds__(kThreads) void read_probe_kernel(const char* __rest
     u32x4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
-      v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + u * kThreads * 16u, 0, 0);
+      v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + u * kThreads * 16u, 0, kNonTemporal);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
   }

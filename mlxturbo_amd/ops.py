@@ -319,16 +319,37 @@ def _stream_of(dev: torch.device) -> int:
 
 
 _WS_CACHE: dict = {}
+# Buffers dropped from the caches after this process has captured a HIP
+# graph: a captured kernel may still point at them (its graph can replay any
+# time later), so they are kept alive instead of returned to the allocator.
+_RETIRED: list = []
+_SEEN_CAPTURE = False
+
+
+def _capturing() -> bool:
+    global _SEEN_CAPTURE
+    c = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+    _SEEN_CAPTURE = _SEEN_CAPTURE or c
+    return c
+
+
+def _retire(bufs) -> None:
+    if _SEEN_CAPTURE:
+        _RETIRED.extend(bufs)
 
 
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     """The gather workspace of the current stream (kernels on one stream run
     in order, so consecutive calls can share it; calls on other streams get
-    their own, as concurrent calls must not share one)."""
+    their own, as concurrent calls must not share one).  A buffer outgrown
+    after a graph capture is kept alive (captured kernels may use it)."""
     key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device(),
            _stream_of(dev))
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
+        _capturing()
+        if buf is not None:
+            _retire([buf])
         buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
         _WS_CACHE[key] = buf
     return buf
@@ -337,12 +358,24 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
 _LHS_CACHE: dict = {}
 
 
+def _repeat_broadcast(bx: tuple, shape: tuple) -> bool:
+    """True when x's batch dims ``bx`` broadcast to ``shape`` by repeating
+    each batch over consecutive pairs (leading dims equal, trailing dims 1),
+    e.g. tokens (T, 1) against expert indices (T, top_k): the C ABI's NULL
+    lhs, pair p reading batch p / (P / B), needs no index table then."""
+    bx = (1,) * (len(shape) - len(bx)) + tuple(bx)
+    j = 0
+    while j < len(shape) and bx[j] == shape[j]:
+        j += 1
+    return all(d == 1 for d in bx[j:])
+
+
 def _default_lhs(dev: torch.device, bx: tuple, shape: tuple) -> Optional[torch.Tensor]:
     """x's own batch index per pair (lhs_indices=None), flattened over the
-    broadcast shape; None when that is the identity (the C ABI's NULL lhs).
-    Cached per shape and stream (the table is written by kernels on the
-    stream that built it): building it costs two small kernels per call."""
-    if tuple(bx) == tuple(shape):
+    broadcast shape; None when the C ABI's NULL lhs expresses it (identity
+    or repeated batches).  Other broadcasts build a table, cached per shape
+    and stream (it is written by kernels on the stream that built it)."""
+    if _repeat_broadcast(bx, shape):
         return None
     key = (dev.type, dev.index, _stream_of(dev), tuple(bx), tuple(shape))
     t = _LHS_CACHE.get(key)
@@ -350,9 +383,13 @@ def _default_lhs(dev: torch.device, bx: tuple, shape: tuple) -> Optional[torch.T
         B = math.prod(bx)
         t = (torch.arange(B, device=dev, dtype=torch.int32).reshape(bx).expand(shape)
              .reshape(-1).contiguous())
-        if len(_LHS_CACHE) > 64:
-            _LHS_CACHE.clear()
-        _LHS_CACHE[key] = t
+        # a table built under graph capture holds data only once the graph
+        # replays, so it is not offered to later eager calls
+        if not _capturing():
+            if len(_LHS_CACHE) > 64:
+                _retire(_LHS_CACHE.values())
+                _LHS_CACHE.clear()
+            _LHS_CACHE[key] = t
     return t
 
 
@@ -453,6 +490,11 @@ def _gather_launch(x3, flat, lhs, rhs, out, P, B, M, N, K, E, group_size, bits,
     _lib.check(rc, "gather_qmm")
 
 
+def _lhs_table(P: int, B: int, dev) -> torch.Tensor:
+    """The table the C ABI's NULL lhs stands for: pair p reads batch p / (P / B)."""
+    return torch.arange(P, device=dev, dtype=torch.int32) // (P // B)
+
+
 def _gather_rows(a, out, group_size, bits, sorted_indices) -> torch.Tensor:
     """More than 16 rows per pair: row m of pair p is the one-row pair
     (lhs[p] * M + m, rhs[p]) of x viewed as B*M one-row batches, so the call
@@ -460,7 +502,7 @@ def _gather_rows(a, out, group_size, bits, sorted_indices) -> torch.Tensor:
     P, B, M, N, K = a["P"], a["B"], a["M"], a["N"], a["K"]
     dev = a["dev"]
     rows = torch.arange(M, device=dev, dtype=torch.int32)
-    lhs = a["lhs"] if a["lhs"] is not None else torch.arange(P, device=dev, dtype=torch.int32)
+    lhs = a["lhs"] if a["lhs"] is not None else _lhs_table(P, B, dev)
     lhs1 = (lhs[:, None] * M + rows[None, :]).reshape(-1).contiguous()
     rhs1 = a["rhs"][:, None].expand(P, M).reshape(-1).contiguous()
     o = out.reshape(P * M, 1, N)
@@ -503,7 +545,7 @@ def _gather_composed(a, out, bank, group_size, bits) -> torch.Tensor:
     res = out.reshape(P, M, N)
     res.zero_()
     rhs = a["rhs"].long()
-    lhs = a["lhs"].long() if a["lhs"] is not None else torch.arange(P, device=a["dev"])
+    lhs = (a["lhs"] if a["lhs"] is not None else _lhs_table(P, B, a["dev"])).long()
     valid = (rhs >= 0) & (rhs < E) & (lhs >= 0) & (lhs < B)
     rhs_h = torch.where(valid, rhs, torch.full_like(rhs, -1)).cpu()
     xs = a["x"].to(dt)

@@ -100,9 +100,11 @@ def test_empty_problem_is_a_noop(lib):
 
 def test_gather_argument_validation(lib):
     f = lib.mq_gather_qmm
-    # lhs NULL needs B == P
-    rc = f(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, 4, 3, 1, 16, 256, 8, 64, 4, 0, 0, None, 0, None)
-    assert rc == -1 and "B == P" in lib.mq_last_error().decode()
+    # lhs NULL needs B to divide P (pair p reads x batch p / (P / B))
+    for P, B in ((4, 3), (4, 0), (6, 4), (4, 8)):
+        rc = f(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, P, B, 1, 16, 256, 8, 64, 4, 0, 0, None,
+               0, None)
+        assert rc == -1 and "B to divide P" in lib.mq_last_error().decode(), (P, B)
     # more than 16 rows per pair
     rc = f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, 17, 16, 256, 8, 64, 4, 0, 0, None, 0, None)
     assert rc == -2
@@ -192,10 +194,10 @@ class _FakeLib:
                       sorted_, ws, wsb, stream):
         read = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
                                                shape=(P,)).copy()
-        # a NULL lhs means pair p reads x batch p (the C ABI requires B == P then)
-        assert lhs or B == P
+        # a NULL lhs means pair p reads x batch p / (P / B) (B divides P)
+        assert lhs or (B > 0 and P % B == 0)
         self.calls.append(("gather", dict(P=P, B=B, M=M, N=N, K=K, E=E,
-                                          lhs=read(lhs) if lhs else np.arange(P),
+                                          lhs=read(lhs) if lhs else np.arange(P) // (P // B),
                                           lhs_null=not lhs, rhs=read(rhs), sorted=sorted_)))
         return 0
 
@@ -205,7 +207,7 @@ class _FakeLib:
                                                shape=(P,)).copy()
         self.calls.append(("glu", dict(P=P, B=B, M=M, N=N, K=K, E=E, gate=(wg, sg, bg),
                                        up=(wu, su, bu), rhs=read(rhs),
-                                       lhs=read(lhs) if lhs else np.arange(P))))
+                                       lhs=read(lhs) if lhs else np.arange(P) // (P // B))))
         return 0
 
     def mq_dequantize(self, w, s, b, out, N, K, gs, bits, dtype, stream):
@@ -361,6 +363,25 @@ def test_gather_broadcasts_like_switchglu(fake):
     assert kind == "gather" and c["P"] == T * top and c["B"] == T and c["M"] == 1 and c["E"] == E
     np.testing.assert_array_equal(c["rhs"], idx.reshape(-1).numpy())
     np.testing.assert_array_equal(c["lhs"], np.repeat(np.arange(T), top))
+    assert c["lhs_null"]                  # repeated batches need no index table
+
+
+@pytest.mark.parametrize("bx,ishape,null", [((3, 1), (3, 4), True), ((1, 1), (3, 4), True),
+                                            ((), (5,), True), ((2, 3, 1), (2, 3, 4), True),
+                                            ((1, 4), (3, 4), False), ((2, 1, 3), (2, 4, 3), False)])
+def test_gather_default_lhs_broadcasts(fake, bx, ishape, null):
+    # x's batch dims broadcast against the indices: NULL lhs exactly when
+    # each x batch covers consecutive pairs, else an explicit table; either
+    # way the pair -> batch map is numpy's broadcast of x's batch index
+    E, N, K = 8, 32, 256
+    w, s, b = _qweights(N, K, E=E)
+    x = torch.zeros(*bx, 1, K, dtype=torch.bfloat16)
+    idx = torch.arange(int(np.prod(ishape)), dtype=torch.int32).reshape(ishape) % E
+    mlxturbo_amd.gather_qmm(x, w, s, b, rhs_indices=idx)
+    _, c = fake.calls[-1]
+    want = np.broadcast_to(np.arange(int(np.prod(bx))).reshape(bx), ishape).reshape(-1)
+    np.testing.assert_array_equal(c["lhs"], want)
+    assert c["lhs_null"] == null and c["B"] == int(np.prod(bx))
 
 
 def test_gather_sorted_layout(fake):
