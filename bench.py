@@ -137,15 +137,17 @@ def make_weights(torch, N, K, copies, seed=1, bits=4, gs=64):
 def time_graph(torch, fn, steps, warmup):
     """Warm up eagerly, capture `steps` calls in one graph, time one replay.
 
-    Returns (elapsed seconds of the replay, per-step seconds).  Events are
-    recorded on the capture stream, the stream every launch in the graph runs
-    on.
+    Returns (elapsed seconds of the replay, per-step seconds).  The warm-up
+    runs on the capture stream (so per-stream caches built there serve the
+    capture), and events are recorded on that stream, the stream every
+    launch in the graph runs on.
     """
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):          # warm-up on the capture stream
+        for i in range(warmup):
+            fn(i)
+    torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):

@@ -42,7 +42,7 @@ extern "C" {
 #define MQ_FLOAT16 1
 #define MQ_FLOAT32 2
 
-/* ABI version; bumped on any signature change. */
+/* ABI version; bumped on any signature or contract change. */
 int mq_version(void);
 
 /* Message for the last non-zero status returned on this thread. */

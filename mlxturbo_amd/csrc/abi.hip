@@ -115,7 +115,7 @@ int scratch_for_current_device(void** out) {
 
 extern "C" {
 
-int mq_version(void) { return 2; }
+int mq_version(void) { return 3; }
 
 const char* mq_last_error(void) { return g_last_error.c_str(); }
 

@@ -338,13 +338,18 @@ def _retire(bufs) -> None:
         _RETIRED.extend(bufs)
 
 
+def _dev_index(dev: torch.device) -> int:
+    if dev.index is not None:
+        return dev.index
+    return torch.cuda.current_device() if dev.type == "cuda" else 0
+
+
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     """The gather workspace of the current stream (kernels on one stream run
     in order, so consecutive calls can share it; calls on other streams get
     their own, as concurrent calls must not share one).  A buffer outgrown
     after a graph capture is kept alive (captured kernels may use it)."""
-    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device(),
-           _stream_of(dev))
+    key = (dev.type, _dev_index(dev), _stream_of(dev))
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
         _capturing()
@@ -632,7 +637,6 @@ def gather_glu(x: torch.Tensor, gate_w: torch.Tensor, gate_scales: torch.Tensor,
 
 # mq_gather_glu fuses below this many output rows (P * M)
 _GLU_FUSED_MAX_ROWS = 1024
-
 
 def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, rows: int,
                 top_k: int) -> torch.Tensor:
