@@ -27,8 +27,10 @@
 //  * x, W, scales and biases are read with buffer loads; rows past M (or past
 //    N) are past the buffer range and read zeros, so no row clamping.
 //  * Each weight is dequantized once per BM output rows; a whole tile whose
-//    scales include |s| >= 2^100 (never in real checkpoints) takes the plain
-//    float dequantization route, chosen once per tile by a scan of its scales.
+//    scales include |s| >= 2^100 (never in real checkpoints) is recomputed on
+//    the plain float dequantization route: the fast route checks each scale
+//    as it uses it, so no tile waits for a scan of its scales before its
+//    first weight load.
 #pragma once
 #include <type_traits>
 
@@ -136,6 +138,7 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
     uint16_t s[WPT], b[WPT];
   };
   Set S0, S1;
+  bool big = false;   // a scale with |s| >= 2^100 met on the fast route
   // Scales and biases, 64- and 128-row tiles of weights that no other tile
   // reads through L2 (on dense tiles it cost 1.5-4%), K / GS a multiple of 8,
   // both arrays 16-byte aligned and whose k range is whole blocks of SPB
@@ -212,6 +215,7 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
         b16 = st.b[i];
       }
       const GroupScale g = make_group(T::to_f32(s16), T::to_f32(b16));
+      if constexpr (!PLAIN) big |= needs_plain(g.s);
       uint32_t o[CPC / 8];
       if constexpr (PLAIN) deq_word_plain<DT, BITS>(st.wv[i][j], g, o);
       else deq_word<DT, BITS>(st.wv[i][j], g, o);
@@ -222,12 +226,14 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
   };
 
   f32x16 acc[TM][TN];
+  auto clear = [&]() {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  };
 
   const int lr = lane & 31, lk = 8 * (lane >> 5);
   auto mma = [&](int buf) {
@@ -247,18 +253,8 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
     }
   };
 
-  bool big = false;
-  {
-    const uint32_t nbytes = (uint32_t)nrows * G * 2;
-    const auto rs = wide_rsrc(scales, nbytes);
-    for (uint32_t off = t * 16u; off < nbytes; off += NT * 16u) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        big |= needs_plain(T::to_f32((uint16_t)v[e])) || needs_plain(T::to_f32((uint16_t)(v[e] >> 16)));
-    }
-  }
   auto run = [&](auto plainc) {
+    clear();
     auto stage_store = [&](const Set& st, int buf) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) spart(st, buf, ks, plainc, std::integral_constant<int, -1>{});
@@ -325,8 +321,12 @@ __device__ __forceinline__ void wide_tile(__amdgpu_buffer_rsrc_t xrsrc, XRowOff 
       }
     }
   };
+  // Optimistic fast dequantization: every scale a thread uses on the fast
+  // path is checked as it is used; a tile that met |s| >= 2^100 (never in
+  // real checkpoints) is recomputed from scratch on the plain float route
+  // before anything is stored.
+  run(std::integral_constant<bool, false>{});
   if (__syncthreads_or(big)) run(std::integral_constant<bool, true>{});
-  else run(std::integral_constant<bool, false>{});
 
   // D[row][col] of a 32x32 tile: col = lane & 31, row = 8*(e/4) + 4*(lane>>5) + e%4
 #pragma unroll
