@@ -69,7 +69,8 @@ def parse():
                         "gather_glu_<routing>_T<T> (fused gate+up+SiLU), qmv<M> / qmvdown<M> "
                         "(configs[1] skinny), combine (MoE combine, 2048 x top-8 x 2048), "
                         "gather_prefill_<proj>_<routing> (2048 tokens), "
-                        "moe_layer_<routing>_T<T> (whole decode MoE layer)")
+                        "moe_layer_<routing>_T<T> (whole decode MoE layer), "
+                        "route<T> (MoE routing + shared gate)")
     return p.parse_args()
 
 
@@ -96,6 +97,8 @@ def run_case(torch, mq, case: str) -> dict:
         proj, routing = case[len("gather_prefill_"):].rsplit("_", 1)
         NN, KK = banks[proj]
         return {"case": case, **measure_gather_prefill(torch, mq, 2048, NN, KK, routing, 20, 3)}
+    if case.startswith("route"):
+        return {"case": case, **measure_route(torch, mq, int(case[len("route"):] or 1), 100, 5)}
     if case.startswith("moe_layer_"):
         routing, t = case[len("moe_layer_"):].rsplit("_T", 1)
         return {"case": case, **measure_moe_layer(torch, mq, int(t), routing, 100, 5)}
@@ -340,6 +343,22 @@ def measure_combine(torch, mq, rows, top_k, N, steps, warmup, seed=6):
     _, per_step = time_graph(torch, fn, steps, warmup)
     nbytes = 2 * rows * top_k * N + 2 * rows * N + 8 * rows * top_k
     return {"us": round(per_step * 1e6, 2), "GBps": round(nbytes / per_step / 1e9, 1)}
+
+
+def measure_route(torch, mq, T, steps, warmup, E=512, top_k=8, H=2048, seed=9):
+    """MoE routing of T tokens (config-4 router: 512 experts, top-8) with the
+    shared-expert gate over the hidden size: one launch, latency-bound."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    logits = torch.randn((T, E), device="cuda", generator=g)
+    x = torch.randn((T, H), device="cuda", generator=g).to(torch.bfloat16)
+    sgw = (torch.randn((H,), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+
+    def fn(i):
+        mq.moe_route(logits, top_k, x, sgw)
+
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    return {"us": round(per_step * 1e6, 2), "bytes": T * (4 * E + 2 * H) + 2 * H + T * 8 * top_k}
 
 
 def measure_dequant(torch, mq, N, K, steps, warmup):
@@ -632,6 +651,8 @@ def main():
                 # the whole layer: gate+up+SiLU, down, router-weighted combine
                 sweep[f"moe_layer_{routing}_T{T}"] = measure_moe_layer(
                     torch, mq, T, routing, 100, 5)
+        for T in (1, 4, 8):
+            sweep[f"moe_route_T{T}_E512_k8"] = measure_route(torch, mq, T, 100, 5)
         # config 4 banks at prefill width (2048 tokens): expert-grouped MFMA tiles
         for routing in ("zipf", "uniform"):
             for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):

@@ -208,6 +208,40 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
 int mq_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w, void* out,
                    int64_t rows, int64_t top_k, int64_t N, int dtype, void* hip_stream);
 
+/*
+ * mq_moe_combine with the shared expert merged in, as the reference's decode
+ * combine does (kernels/moe_route_decode.py:353-398 `combine`, kept off by
+ * default there): out[t, n] = T(float(T(sum_k w[t*top_k + k] * y[inv[..], n]))
+ * + float(T(sgate[t] * shared[t, n]))), with sgate (dtype [rows]) the
+ * already-sigmoided shared-expert gate (mq_moe_route writes it) and shared
+ * (dtype [rows, N], 16-byte aligned) the shared expert's output.  Other
+ * arguments and limits as mq_moe_combine.
+ */
+int mq_moe_combine_shared(const void* y, int64_t y_rows, const int32_t* inv, const float* w,
+                          const void* sgate, const void* shared, void* out, int64_t rows,
+                          int64_t top_k, int64_t N, int dtype, void* hip_stream);
+
+/*
+ * MoE routing at decode / verify widths.  Replaces the reference's
+ * kernels/moe_route_decode.py:269-327 (`route(logits, top_k, x, sgw)`, kept
+ * off by default there; the stock path is argpartition + take_along_axis +
+ * softmax(precise) + the shared-expert gate of _vendor/qwen4_exp.py).  For
+ * each of `rows` rows of float32 logits [rows, E]: the top_k experts by value
+ * in descending order (equal values: the smaller expert index first, as
+ * torch.topk decides) into idx (int32 [rows, top_k]), and their softmax
+ * weights into weights (float32 [rows, top_k]):
+ *   w_j = exp(v_j - v_0) / sum_i exp(v_i - v_0),  summed in float in order.
+ * With x (dtype [rows, H]), sgw (dtype [H]) and sgate (dtype [rows]) given,
+ * also the shared expert's gate sgate[r] = sigmoid(T(sum_h x[r,h] sgw[h]))
+ * (dot in float; sigmoid as MLX evaluates it in T: y = 1 / (1 + exp(|s|)),
+ * s < 0 ? y : 1 - y, every operation rounded to T); pass all three NULL to
+ * skip it.  E <= 1024 and top_k <= 64 (else MQ_EUNSUPPORTED); dtype bf16 or
+ * fp16 when the gate is asked for.
+ */
+int mq_moe_route(const float* logits, int32_t* idx, float* weights, int64_t rows, int64_t E,
+                 int64_t top_k, const void* x, const void* sgw, void* sgate, int64_t H, int dtype,
+                 void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

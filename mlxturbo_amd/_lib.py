@@ -36,6 +36,8 @@ EXPORTED = (
     "mq_gather_qmm_noalloc",
     "mq_gather_glu",
     "mq_moe_combine",
+    "mq_moe_combine_shared",
+    "mq_moe_route",
 )
 
 _lock = threading.Lock()
@@ -77,6 +79,11 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_gather_qmm_noalloc.restype = _int
     lib.mq_gather_qmm_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _int, _int, _int, _int, _vp]
+    lib.mq_moe_combine_shared.restype = _int
+    lib.mq_moe_combine_shared.argtypes = [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                          _int, _vp]
+    lib.mq_moe_route.restype = _int
+    lib.mq_moe_route.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _int, _vp]
     lib.mq_gather_glu.restype = _int
     lib.mq_gather_glu.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _int, _int, _int, _vp, ctypes.c_size_t,

@@ -113,6 +113,36 @@ int scratch_for_current_device(void** out) {
 
 }  // namespace
 
+namespace {
+
+int moe_combine_checked(const void* y, int64_t y_rows, const int32_t* inv, const float* w,
+                        const void* sgate, const void* shared, void* out, int64_t rows,
+                        int64_t top_k, int64_t N, int dtype, void* hip_stream, const char* what) {
+  if (!y || !w || !out) return fail(MQ_EINVAL, "y, w and out must be non-null");
+  if (rows < 0 || N <= 0 || y_rows < 0) return fail(MQ_EINVAL, "invalid sizes rows=%lld N=%lld y_rows=%lld",
+                                      (long long)rows, (long long)N, (long long)y_rows);
+  if (y_rows > INT32_MAX) return fail(MQ_EUNSUPPORTED, "%s supports y_rows < 2^31", what);
+  if (top_k < 1 || top_k > mq::kCombineMaxTopK)
+    return fail(MQ_EINVAL, "top_k must be in 1..%d (got %lld)", mq::kCombineMaxTopK,
+                (long long)top_k);
+  if (N % 8) return fail(MQ_EUNSUPPORTED, "%s needs N %% 8 == 0 (got %lld)", what, (long long)N);
+  if (dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16)
+    return fail(MQ_EUNSUPPORTED, "%s supports bf16 and fp16 (dtype %d)", what, dtype);
+  if (!aligned16(y) || !aligned16(out)) return fail(MQ_EINVAL, "y and out must be 16-byte aligned");
+  if (shared && !aligned16(shared)) return fail(MQ_EINVAL, "shared must be 16-byte aligned");
+  if (rows > 65535) return fail(MQ_EUNSUPPORTED, "%s supports up to 65535 rows per call", what);
+  if (!inv && y_rows < rows * top_k)
+    return fail(MQ_EINVAL, "inv=NULL needs y_rows >= rows*top_k (%lld < %lld)", (long long)y_rows,
+                (long long)(rows * top_k));
+  if (rows == 0) return MQ_OK;
+  int rc = mq::launch_moe_combine(y, y_rows, inv, w, out, rows, top_k, N, dtype,
+                                  reinterpret_cast<hipStream_t>(hip_stream), sgate, shared);
+  if (rc) return fail(rc, "%s: no kernel for this configuration", what);
+  return check_launch(what);
+}
+
+}  // namespace
+
 extern "C" {
 
 int mq_version(void) { return 3; }
@@ -329,28 +359,43 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
   return MQ_OK;
 }
 
+
 int mq_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w, void* out,
                    int64_t rows, int64_t top_k, int64_t N, int dtype, void* hip_stream) {
-  if (!y || !w || !out) return fail(MQ_EINVAL, "y, w and out must be non-null");
-  if (rows < 0 || N <= 0 || y_rows < 0) return fail(MQ_EINVAL, "invalid sizes rows=%lld N=%lld y_rows=%lld",
-                                      (long long)rows, (long long)N, (long long)y_rows);
-  if (y_rows > INT32_MAX) return fail(MQ_EUNSUPPORTED, "moe_combine supports y_rows < 2^31");
-  if (top_k < 1 || top_k > mq::kCombineMaxTopK)
-    return fail(MQ_EINVAL, "top_k must be in 1..%d (got %lld)", mq::kCombineMaxTopK,
-                (long long)top_k);
-  if (N % 8) return fail(MQ_EUNSUPPORTED, "moe_combine needs N %% 8 == 0 (got %lld)", (long long)N);
-  if (dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16)
-    return fail(MQ_EUNSUPPORTED, "moe_combine supports bf16 and fp16 (dtype %d)", dtype);
-  if (!aligned16(y) || !aligned16(out)) return fail(MQ_EINVAL, "y and out must be 16-byte aligned");
-  if (rows > 65535) return fail(MQ_EUNSUPPORTED, "moe_combine supports up to 65535 rows per call");
-  if (!inv && y_rows < rows * top_k)
-    return fail(MQ_EINVAL, "inv=NULL needs y_rows >= rows*top_k (%lld < %lld)", (long long)y_rows,
-                (long long)(rows * top_k));
+  return moe_combine_checked(y, y_rows, inv, w, nullptr, nullptr, out, rows, top_k, N, dtype,
+                             hip_stream, "moe_combine");
+}
+
+int mq_moe_combine_shared(const void* y, int64_t y_rows, const int32_t* inv, const float* w,
+                          const void* sgate, const void* shared, void* out, int64_t rows,
+                          int64_t top_k, int64_t N, int dtype, void* hip_stream) {
+  if (!sgate || !shared) return fail(MQ_EINVAL, "sgate and shared must be non-null");
+  return moe_combine_checked(y, y_rows, inv, w, sgate, shared, out, rows, top_k, N, dtype,
+                             hip_stream, "moe_combine_shared");
+}
+
+int mq_moe_route(const float* logits, int32_t* idx, float* weights, int64_t rows, int64_t E,
+                 int64_t top_k, const void* x, const void* sgw, void* sgate, int64_t H, int dtype,
+                 void* hip_stream) {
+  if (!logits || !idx || !weights) return fail(MQ_EINVAL, "logits, idx and weights must be non-null");
+  if (rows < 0 || E < 1 || top_k < 1)
+    return fail(MQ_EINVAL, "invalid sizes rows=%lld E=%lld top_k=%lld", (long long)rows,
+                (long long)E, (long long)top_k);
+  if (top_k > E) return fail(MQ_EINVAL, "top_k=%lld exceeds E=%lld", (long long)top_k, (long long)E);
+  const bool sg = x || sgw || sgate;
+  if (sg && (!x || !sgw || !sgate))
+    return fail(MQ_EINVAL, "x, sgw and sgate are given together or not at all");
+  if (sg && H < 1) return fail(MQ_EINVAL, "invalid hidden size H=%lld", (long long)H);
+  if (sg && dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16)
+    return fail(MQ_EUNSUPPORTED, "moe_route's shared gate supports bf16 and fp16 (dtype %d)", dtype);
+  if (E > 1024 || top_k > 64 || rows > INT32_MAX || H > INT32_MAX)
+    return fail(MQ_EUNSUPPORTED, "moe_route takes E <= 1024 and top_k <= 64 (E=%lld top_k=%lld)",
+                (long long)E, (long long)top_k);
   if (rows == 0) return MQ_OK;
-  int rc = mq::launch_moe_combine(y, y_rows, inv, w, out, rows, top_k, N, dtype,
-                                  reinterpret_cast<hipStream_t>(hip_stream));
-  if (rc) return fail(rc, "moe_combine: no kernel for this configuration");
-  return check_launch("moe_combine");
+  int rc = mq::launch_moe_route(logits, idx, weights, rows, E, top_k, x, sgw, sgate, H,
+                                sg ? dtype : MQ_BFLOAT16, reinterpret_cast<hipStream_t>(hip_stream));
+  if (rc) return fail(rc, "moe_route: no kernel for this configuration");
+  return check_launch("moe_route");
 }
 
 }  // extern "C"

@@ -20,12 +20,17 @@ namespace mq {
 constexpr int kCombineMaxTopK = 64;
 constexpr int kCombineBatch = 8;
 
-template <int DT>
+// SH: the shared expert merged in as the reference's decode combine does
+// (kernels/moe_route_decode.py:392-398): out = T(float(T(sum)) +
+// float(T(sgate[t] * shared[t, n]))), sgate the already-sigmoided gate.
+template <int DT, bool SH = false>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y,
                                                           const int32_t* __restrict__ inv,
                                                           const float* __restrict__ w,
                                                           uint16_t* __restrict__ out, int top_k,
-                                                          int N, int y_rows) {
+                                                          int N, int y_rows,
+                                                          const uint16_t* __restrict__ sgate = nullptr,
+                                                          const uint16_t* __restrict__ shared = nullptr) {
   using T = T16<DT>;
   __shared__ int s_row[kCombineMaxTopK];
   __shared__ float s_w[kCombineMaxTopK];
@@ -68,23 +73,43 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   u32x4 o;
 #pragma unroll
   for (int v = 0; v < 4; ++v) o[v] = T::pack2(acc[2 * v], acc[2 * v + 1]);
+  if constexpr (SH) {
+    const float sg = T::to_f32(sgate[t]);
+    const u32x4 sh = *reinterpret_cast<const u32x4*>(shared + (int64_t)t * N + n);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint32_t m = T::pack2(sg * T::to_f32((uint16_t)sh[v]), sg * T::to_f32((uint16_t)(sh[v] >> 16)));
+      o[v] = T::pack2(T::to_f32((uint16_t)o[v]) + T::to_f32((uint16_t)m),
+                      T::to_f32((uint16_t)(o[v] >> 16)) + T::to_f32((uint16_t)(m >> 16)));
+    }
+  }
   *reinterpret_cast<u32x4*>(out + (int64_t)t * N + n) = o;
 }
 
+// sgate / shared: both null, or the shared expert's gate (T [rows]) and
+// output (T [rows, N]) to merge in.
 inline int launch_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w,
                               void* out, int64_t rows, int64_t top_k, int64_t N, int dtype,
-                              hipStream_t st) {
+                              hipStream_t st, const void* sgate = nullptr,
+                              const void* shared = nullptr) {
   const int64_t cols = N / 8;
   const int tb = cols >= 256 ? 256 : cols >= 128 ? 128 : 64;
   const dim3 grid((unsigned)((cols + tb - 1) / tb), (unsigned)rows);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(moe_combine_kernel<kBF16>, grid, dim3(tb), 0, st, (const uint16_t*)y, inv,
-                       w, (uint16_t*)out, (int)top_k, (int)N, (int)y_rows);
-  else if (dtype == kF16)
-    hipLaunchKernelGGL(moe_combine_kernel<kF16>, grid, dim3(tb), 0, st, (const uint16_t*)y, inv,
-                       w, (uint16_t*)out, (int)top_k, (int)N, (int)y_rows);
-  else
+  const auto* sg = static_cast<const uint16_t*>(sgate);
+  const auto* sh = static_cast<const uint16_t*>(shared);
+#define MQ_COMBINE(DT, SH)                                                                        \
+  hipLaunchKernelGGL((moe_combine_kernel<DT, SH>), grid, dim3(tb), 0, st, (const uint16_t*)y, inv, \
+                     w, (uint16_t*)out, (int)top_k, (int)N, (int)y_rows, sg, sh)
+  if (dtype == kBF16) {
+    if (sh) MQ_COMBINE(kBF16, true);
+    else MQ_COMBINE(kBF16, false);
+  } else if (dtype == kF16) {
+    if (sh) MQ_COMBINE(kF16, true);
+    else MQ_COMBINE(kF16, false);
+  } else {
     return kStatusUnsupported;
+  }
+#undef MQ_COMBINE
   return 0;
 }
 

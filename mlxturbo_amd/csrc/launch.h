@@ -56,6 +56,15 @@ struct GluLaunch {
                  int64_t K, int64_t E, void* ws, hipStream_t st, int* nlaunch);
 };
 
+// MoE routing (route.hip): per row of float logits [rows, E] the top_k
+// experts (descending, equal values by smaller index) into idx and their
+// softmax weights into w; with x ([rows, H]) and sgw ([H]) non-null (dtype
+// DT) also sgate[r] = sigmoid(T(x[r] . sgw)).  kStatusUnsupported outside
+// E <= 1024, 1 <= top_k <= min(64, E), dtype bf16 / f16.
+int launch_moe_route(const float* logits, int32_t* idx, float* w, int64_t rows, int64_t E,
+                     int64_t top_k, const void* x, const void* sgw, void* sgate, int64_t H,
+                     int dtype, hipStream_t st);
+
 // MLX affine quantize of N x K float values (dtype DT: weights, scales and
 // biases share it) into the bitstream format, and dequantize of any width
 // (formats.hip).  Both return 0 or kStatusUnsupported for a configuration

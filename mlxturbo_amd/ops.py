@@ -639,15 +639,23 @@ def gather_glu(x: torch.Tensor, gate_w: torch.Tensor, gate_scales: torch.Tensor,
 _GLU_FUSED_MAX_ROWS = 1024
 
 def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, rows: int,
-                top_k: int) -> torch.Tensor:
+                top_k: int, sgate: Optional[torch.Tensor] = None,
+                shared: Optional[torch.Tensor] = None) -> torch.Tensor:
     """MoE combine epilogue (kernels/moe_combine.py:160-195): from the down
     projection's expert-ordered output ``y`` ``(M, N)`` build ``(rows, N)``
     with ``out[t] = sum_k w[t*top_k + k] * y[inv[t*top_k + k]]``, float
     accumulation in k order, one rounding.  ``inv`` (int, ``(rows*top_k,)``)
     is the sorted row of each (token, k) -- ``argsort(order)``; ``None``
     when ``y`` is already in (token, k) order.  ``w`` is the router weight
-    per (token, k), cast to float32 as the reference does."""
-    dev = _require_gpu(y, w, inv)
+    per (token, k), cast to float32 as the reference does.
+
+    With the shared expert's sigmoided gate ``sgate`` (``(rows,)`` or
+    ``(rows, 1)``, as :func:`moe_route` returns it) and its output
+    ``shared`` ``(rows, N)``, both in y's dtype, the shared expert is merged
+    in as the reference's decode combine rounds it
+    (kernels/moe_route_decode.py:353-398): ``T(float(T(sum)) +
+    float(T(sgate * shared)))``."""
+    dev = _require_gpu(y, w, inv, sgate, shared)
     if y.ndim != 2:
         raise ValueError("y must be (M, N)")
     if y.dtype not in (torch.bfloat16, torch.float16):
@@ -664,17 +672,81 @@ def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, r
         if inv.numel() != rows * top_k:
             raise ValueError(f"inv has {inv.numel()} entries, expected {rows * top_k}")
         inv_ = inv.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+    if (sgate is None) != (shared is None):
+        raise ValueError("sgate and shared are given together")
+    if shared is not None:
+        if sgate.numel() != rows or tuple(shared.shape) != (rows, N):
+            raise ValueError(f"sgate must hold {rows} gates and shared be ({rows}, {N})")
+        if sgate.dtype != y.dtype or shared.dtype != y.dtype:
+            raise ValueError("sgate and shared must have y's dtype")
     w_ = w.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
     y_ = _aligned(y)
     out = torch.empty((rows, N), dtype=y.dtype, device=dev)
     if rows == 0:
         return out
-    rc = _lib.lib().mq_moe_combine(y_.data_ptr(), M,
-                                   inv_.data_ptr() if inv_ is not None else None,
-                                   w_.data_ptr(), out.data_ptr(), rows, top_k, N,
-                                   _dtype_code(y.dtype, y.dtype), _stream_ptr(out))
-    _lib.check(rc, "moe_combine")
+    lib = _lib.lib()
+    code = _dtype_code(y.dtype, y.dtype)
+    if shared is None:
+        rc = lib.mq_moe_combine(y_.data_ptr(), M, inv_.data_ptr() if inv_ is not None else None,
+                                w_.data_ptr(), out.data_ptr(), rows, top_k, N, code,
+                                _stream_ptr(out))
+        _lib.check(rc, "moe_combine")
+    else:
+        sg_ = sgate.reshape(-1).contiguous()
+        sh_ = _aligned(shared)
+        rc = lib.mq_moe_combine_shared(y_.data_ptr(), M,
+                                       inv_.data_ptr() if inv_ is not None else None,
+                                       w_.data_ptr(), sg_.data_ptr(), sh_.data_ptr(),
+                                       out.data_ptr(), rows, top_k, N, code, _stream_ptr(out))
+        _lib.check(rc, "moe_combine_shared")
     return out
+
+
+def moe_route(logits: torch.Tensor, top_k: int, x: Optional[torch.Tensor] = None,
+              sgw: Optional[torch.Tensor] = None):
+    """MoE routing (kernels/moe_route_decode.py:269-327 ``route``): for
+    float32 router ``logits`` ``(..., E)`` the ``top_k`` experts in
+    descending order (equal values: the smaller index first, as torch.topk),
+    as int32 ``(..., top_k)``, and their softmax weights (float32, the
+    largest logit subtracted, summed in float in that order).  With ``x``
+    ``(..., H)`` and the shared expert's gate weight ``sgw`` ``(H,)`` (bf16 or
+    fp16) also ``sigmoid(T(x . sgw))`` ``(..., 1)`` evaluated as MLX does in
+    T; else None.  Returns ``(idx, weights, sgate)``."""
+    dev = _require_gpu(logits, x, sgw)
+    if logits.dtype != torch.float32:
+        raise ValueError(f"moe_route takes float32 logits, got {logits.dtype}")
+    if logits.ndim < 1:
+        raise ValueError("logits must have an expert dimension")
+    E = logits.shape[-1]
+    lead = tuple(logits.shape[:-1])
+    rows = math.prod(lead)
+    top_k = int(top_k)
+    if not 1 <= top_k <= E:
+        raise ValueError(f"top_k={top_k} must be in 1..E={E}")
+    if (x is None) != (sgw is None):
+        raise ValueError("x and sgw are given together")
+    idx = torch.empty((*lead, top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((*lead, top_k), dtype=torch.float32, device=dev)
+    sg = None
+    H, code = 0, 0
+    if x is not None:
+        if x.dtype not in (torch.bfloat16, torch.float16) or sgw.dtype != x.dtype:
+            raise ValueError("x and sgw must share a bf16 / fp16 dtype")
+        H = x.shape[-1]
+        if tuple(x.shape[:-1]) != lead or sgw.numel() != H:
+            raise ValueError(f"x must be {lead} + (H,) and sgw (H,), got {tuple(x.shape)}, "
+                             f"{tuple(sgw.shape)}")
+        sg = torch.empty((*lead, 1), dtype=x.dtype, device=dev)
+        code = _DTYPE_CODE[x.dtype]
+    if rows == 0:
+        return idx, wts, sg
+    l_ = logits.reshape(rows, E).contiguous()
+    x_ = x.reshape(rows, H).contiguous() if x is not None else None
+    g_ = sgw.reshape(-1).contiguous() if sgw is not None else None
+    rc = _lib.lib().mq_moe_route(l_.data_ptr(), idx.data_ptr(), wts.data_ptr(), rows, E, top_k,
+                                 _ptr(x_), _ptr(g_), _ptr(sg), H, code, _stream_ptr(idx))
+    _lib.check(rc, "moe_route")
+    return idx, wts, sg
 
 
 def launch_count() -> int:

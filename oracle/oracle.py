@@ -32,7 +32,16 @@ gather_glu_ref         closed-form SiLU values (silu(0) = 0, silu(1) =
                        gate and up changes it, linearity in the up bank
 moe_combine_ref        pure-Python loop on tiny shapes, one-hot weights copy
                        rows, identity inv equals the unsorted layout, linearity
-                       in w
+                       in w; the shared-expert merge: gate 0 / shared 0 leave
+                       the sum's rounding alone, gate 1 adds shared exactly
+                       where the sum is exact
+moe_route_ref          brute force over all expert subsets on tiny E (the
+                       chosen set maximises the sum of logits), torch.topk's
+                       indices and softmax on distinct logits, ties broken
+                       by the smaller index, weights summing to one
+sigmoid_t              closed-form points (sigmoid(0) = 1/2, large |s|
+                       saturating to 0 / 1), symmetry s(-x) = 1 - s(x) up to
+                       T's rounding, and a float64 sigmoid within two T ulps
 quantize               exact affine grids round-trip bit for bit for every
                        width, group size, dtype and both scale signs; known
                        codes for points off the grid (half-to-even); a
@@ -258,13 +267,20 @@ def gather_glu_ref(x, gate, up, lhs_indices, rhs_indices, group_size: int = 64,
 
 # ------------------------------------------------------------- moe combine
 
-def moe_combine_ref(y, inv, w, rows: int, top_k: int, dtype: str = "bfloat16") -> np.ndarray:
+def moe_combine_ref(y, inv, w, rows: int, top_k: int, dtype: str = "bfloat16",
+                    sgate=None, shared=None) -> np.ndarray:
     """``out[t] = sum_k w[t*top_k + k] * y[inv[t*top_k + k]]`` accumulated in
     float32 in k order (each step rounded once, as an fma), returned
     un-rounded float32 ``[rows, N]``.  ``inv`` ``None`` means rows of ``y``
     are in (token, k) order.  Restates kernels/moe_combine.py:63-97 (the
     per-thread loop ``acc += wk * (float)p[v]``) and its caller contract
     (moe_combine.py:160-195: inv = argsort(order), w cast to float32).
+
+    With ``sgate`` ([rows], the sigmoided shared-expert gate) and ``shared``
+    ([rows, N]) in ``dtype``: the shared expert merged in as the reference's
+    decode combine rounds it (kernels/moe_route_decode.py:392-398): the sum
+    rounded to T, ``T(sgate * shared)``, their float32 sum returned (the
+    caller's final rounding to T is the kernel's last one).
     """
     yf = to_f32(y, dtype).astype(np.float64)
     w = np.asarray(w, dtype=np.float32).reshape(-1).astype(np.float64)
@@ -276,7 +292,64 @@ def moe_combine_ref(y, inv, w, rows: int, top_k: int, dtype: str = "bfloat16") -
         # float32 accumulator rounds once to float32
         out = (w[np.arange(rows) * top_k + k][:, None] * yf[sel] + out.astype(np.float64)
                ).astype(np.float32)
+    if shared is not None:
+        s1 = to_f32(from_f32(out, dtype), dtype)
+        sg = to_f32(np.asarray(sgate).reshape(-1), dtype).astype(np.float64)[:, None]
+        sh = to_f32(np.asarray(shared).reshape(rows, -1), dtype).astype(np.float64)
+        # a 16-bit by 16-bit product is exact in float32: one rounding to T
+        m1 = to_f32(from_f32((sg * sh).astype(np.float32), dtype), dtype)
+        out = (s1 + m1).astype(np.float32)
     return out
+
+
+# ----------------------------------------------------------------- routing
+
+def sigmoid_t(s, dtype: str = "bfloat16") -> np.ndarray:
+    """MLX's Sigmoid evaluated in T one operation at a time, as the reference
+    writes it (kernels/moe_route_decode.py:141-146: ``y = 1 / (1 + exp(|x|));
+    x < 0 ? y : 1 - y`` on T values): every intermediate rounded to T.  ``s``
+    holds T values; returns the T results as float32."""
+    r = lambda a: to_f32(from_f32(np.asarray(a, np.float32), dtype), dtype)
+    x = np.asarray(s, np.float32)
+    e = r(np.exp(np.abs(x).astype(np.float64)))
+    d = r(1.0 + e.astype(np.float64))
+    y = r(1.0 / d.astype(np.float64))
+    return np.where(x < 0, y, r(1.0 - y.astype(np.float64)))
+
+
+def moe_route_ref(logits, top_k: int, x=None, sgw=None, dtype: str = "bfloat16"):
+    """Top-k routing with softmax weights, restating the reference's decode
+    route (kernels/moe_route_decode.py:205-244 and 269-327): per row, the
+    top_k experts in descending order of logit (equal values: the smaller
+    expert index first; -0 equals +0), ``ex_j = exp(v_j - v_0)`` in float32,
+    ``w_j = ex_j / sum`` with the sum accumulated in float32 in selection
+    order.  Returns ``(idx int32 [rows, k], w float32 [rows, k], sgate)``;
+    with ``x`` ([rows, H], T values) and ``sgw`` ([H]) ``sgate`` is
+    ``sigmoid_t(T(x . sgw))`` as float32 (the dot exact in float64, then
+    rounded to float32 and to T: a kernel summing in float32 in another
+    order may differ from it by one T ulp), else None."""
+    L = np.asarray(logits, np.float32)
+    rows, E = L.shape
+    idx = np.zeros((rows, top_k), np.int32)
+    w = np.zeros((rows, top_k), np.float32)
+    for r in range(rows):
+        order = sorted(range(E), key=lambda e: (-float(L[r, e]), e))[:top_k]
+        v = L[r, order]
+        # the difference rounded in float32 (as the reference's float code),
+        # its exp correctly rounded
+        ex = np.exp((v - v[0]).astype(np.float64)).astype(np.float32)
+        tot = np.float32(0.0)
+        for e in ex:
+            tot = np.float32(tot + e)
+        idx[r] = order
+        w[r] = ex / tot
+    sg = None
+    if x is not None:
+        xs = to_f32(np.asarray(x), dtype).astype(np.float64).reshape(rows, -1)
+        gw = to_f32(np.asarray(sgw), dtype).astype(np.float64).reshape(-1)
+        dot = (xs @ gw).astype(np.float32)
+        sg = sigmoid_t(to_f32(from_f32(dot, dtype), dtype), dtype)
+    return idx, w, sg
 
 
 # ----------------------------------------------------------------- quantize

@@ -98,6 +98,28 @@ def test_empty_problem_is_a_noop(lib):
     assert _qmm(lib, N=0) == 0
 
 
+def test_route_and_shared_combine_validation(lib):
+    r = lib.mq_moe_route
+    def route(rows=2, E=64, k=8, x=None, g=None, sg=None, H=0, dtype=0, lg=FAKE):
+        return r(lg, FAKE, FAKE, rows, E, k, x, g, sg, H, dtype, None)
+    assert route(lg=None) == -1 and "non-null" in lib.mq_last_error().decode()
+    assert route(k=65, E=64) == -1 and "exceeds" in lib.mq_last_error().decode()
+    assert route(k=0) == -1
+    assert route(E=2048) == -2 and "E <= 1024" in lib.mq_last_error().decode()
+    assert route(E=1024, k=65) == -2
+    assert route(x=FAKE) == -1 and "together" in lib.mq_last_error().decode()
+    assert route(x=FAKE, g=FAKE, sg=FAKE, H=0) == -1 and "hidden size" in lib.mq_last_error().decode()
+    assert route(x=FAKE, g=FAKE, sg=FAKE, H=64, dtype=2) == -2
+    assert route(rows=0) == 0
+    c = lib.mq_moe_combine_shared
+    assert c(FAKE, 8, None, FAKE, None, FAKE, FAKE, 4, 2, 64, 0, None) == -1
+    assert "sgate and shared" in lib.mq_last_error().decode()
+    assert c(FAKE, 8, None, FAKE, FAKE, FAKE + 2, FAKE, 4, 2, 64, 0, None) == -1
+    assert "shared must be 16-byte aligned" in lib.mq_last_error().decode()
+    assert c(FAKE, 8, None, FAKE, FAKE, FAKE, FAKE, 4, 2, 60, 0, None) == -2
+    assert c(FAKE, 8, None, FAKE, FAKE, FAKE, FAKE, 0, 2, 64, 0, None) == 0
+
+
 def test_gather_argument_validation(lib):
     f = lib.mq_gather_qmm
     # lhs NULL needs B to divide P (pair p reads x batch p / (P / B))
@@ -208,6 +230,17 @@ class _FakeLib:
         self.calls.append(("glu", dict(P=P, B=B, M=M, N=N, K=K, E=E, gate=(wg, sg, bg),
                                        up=(wu, su, bu), rhs=read(rhs),
                                        lhs=read(lhs) if lhs else np.arange(P) // (P // B))))
+        return 0
+
+    def mq_moe_route(self, lg, idx, wts, rows, E, k, x, g, sg, H, dtype, stream):
+        self.calls.append(("route", dict(rows=rows, E=E, k=k, H=H, dtype=dtype, x=bool(x),
+                                         g=bool(g), sg=bool(sg))))
+        return 0
+
+    def mq_moe_combine_shared(self, y, y_rows, inv, w, sg, sh, out, rows, top_k, N, dtype,
+                              stream):
+        self.calls.append(("combine_shared", dict(rows=rows, top_k=top_k, N=N, y_rows=y_rows,
+                                                  sg=bool(sg), sh=bool(sh), inv=bool(inv))))
         return 0
 
     def mq_dequantize(self, w, s, b, out, N, K, gs, bits, dtype, stream):
@@ -382,6 +415,41 @@ def test_gather_default_lhs_broadcasts(fake, bx, ishape, null):
     want = np.broadcast_to(np.arange(int(np.prod(bx))).reshape(bx), ishape).reshape(-1)
     np.testing.assert_array_equal(c["lhs"], want)
     assert c["lhs_null"] == null and c["B"] == int(np.prod(bx))
+
+
+def test_route_shapes_and_arguments(fake):
+    logits = torch.zeros(2, 3, 64, dtype=torch.float32)
+    idx, w, sg = mlxturbo_amd.moe_route(logits, 8)
+    assert idx.shape == (2, 3, 8) and idx.dtype == torch.int32 and w.dtype == torch.float32
+    assert sg is None
+    assert fake.calls[-1] == ("route", dict(rows=6, E=64, k=8, H=0, dtype=0, x=False, g=False,
+                                            sg=False))
+    x = torch.zeros(2, 3, 128, dtype=torch.bfloat16)
+    idx, w, sg = mlxturbo_amd.moe_route(logits, 4, x, torch.zeros(128, dtype=torch.bfloat16))
+    assert sg.shape == (2, 3, 1) and sg.dtype == torch.bfloat16
+    assert fake.calls[-1][1]["H"] == 128 and fake.calls[-1][1]["sg"]
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_route(logits.double(), 4)
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_route(logits, 65)
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_route(logits, 4, x)
+
+
+def test_combine_shared_arguments(fake):
+    rows, top_k, N = 3, 2, 64
+    y = torch.zeros(rows * top_k, N, dtype=torch.bfloat16)
+    w = torch.ones(rows * top_k)
+    sg = torch.zeros(rows, 1, dtype=torch.bfloat16)
+    sh = torch.zeros(rows, N, dtype=torch.bfloat16)
+    out = mlxturbo_amd.moe_combine(y, None, w, rows, top_k, sgate=sg, shared=sh)
+    assert out.shape == (rows, N)
+    assert fake.calls[-1] == ("combine_shared", dict(rows=rows, top_k=top_k, N=N, y_rows=6,
+                                                     sg=True, sh=True, inv=False))
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_combine(y, None, w, rows, top_k, sgate=sg)
+    with pytest.raises(ValueError):
+        mlxturbo_amd.moe_combine(y, None, w, rows, top_k, sgate=sg, shared=sh[:2])
 
 
 def test_gather_sorted_layout(fake):

@@ -1,0 +1,128 @@
+"""Pins the oracle's MoE routing and shared-expert merge (CPU only).
+
+``moe_route_ref`` is checked by brute force over expert subsets, against
+torch.topk / torch.softmax on distinct logits, on ties, on large logits (the
+max subtraction), and by planted mistakes; ``sigmoid_t`` by closed-form
+points and a float64 sigmoid; the shared merge of ``moe_combine_ref`` by the
+cases where its roundings are known exactly.
+"""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+def _distinct_logits(rng, rows, E):
+    return rng.permutation(rows * E).reshape(rows, E).astype(np.float32) / 7.0 - 3.0
+
+
+def test_route_brute_force_subsets():
+    rng = np.random.default_rng(1)
+    E, k = 7, 3
+    L = _distinct_logits(rng, 5, E)
+    idx, w, _ = O.moe_route_ref(L, k)
+    for r in range(L.shape[0]):
+        best = max(itertools.combinations(range(E), k), key=lambda c: sum(L[r, list(c)]))
+        assert set(idx[r]) == set(best)
+        assert np.all(np.diff(L[r, idx[r]]) < 0)             # descending
+
+
+def test_route_matches_torch_topk_softmax():
+    rng = np.random.default_rng(2)
+    L = _distinct_logits(rng, 4, 64)
+    idx, w, _ = O.moe_route_ref(L, 8)
+    tv, ti = torch.topk(torch.from_numpy(L), 8, dim=-1)
+    np.testing.assert_array_equal(idx, ti.numpy())
+    np.testing.assert_allclose(w, torch.softmax(tv.double(), -1).numpy(), rtol=2e-7, atol=0)
+    np.testing.assert_allclose(w.sum(-1), 1.0, rtol=1e-6)
+
+
+def test_route_ties_take_the_smaller_index():
+    L = np.array([[1.0, 2.0, 2.0, 0.0, 2.0], [0.0, -0.0, 0.0, -1.0, 5.0]], np.float32)
+    idx, w, _ = O.moe_route_ref(L, 3)
+    np.testing.assert_array_equal(idx[0], [1, 2, 4])
+    np.testing.assert_array_equal(idx[1], [4, 0, 1])
+    np.testing.assert_array_equal(w[0], np.float32(1.0) / np.float32(3.0))
+
+
+def test_route_large_logits_stay_finite():
+    L = np.array([[200.0, 199.0, -50.0, 198.5]], np.float32)
+    idx, w, _ = O.moe_route_ref(L, 3)
+    np.testing.assert_array_equal(idx[0], [0, 1, 3])
+    assert np.all(np.isfinite(w))
+    np.testing.assert_allclose(w[0], np.exp([0.0, -1.0, -1.5]) / np.exp([0.0, -1.0, -1.5]).sum(),
+                               rtol=1e-6)
+
+
+def _planted_route(L, k, mistake):
+    rows, E = L.shape
+    idx = np.zeros((rows, k), np.int32)
+    w = np.zeros((rows, k), np.float32)
+    for r in range(rows):
+        if mistake == "ties_larger":
+            order = sorted(range(E), key=lambda e: (-float(L[r, e]), -e))[:k]
+        else:
+            order = sorted(range(E), key=lambda e: (-float(L[r, e]), e))[:k]
+        v = L[r, order].astype(np.float32)
+        ex = np.exp(v) if mistake == "no_max" else np.exp(v - v[0])
+        w[r] = ex / ex.sum()
+        idx[r] = order
+    return idx, w
+
+
+@pytest.mark.parametrize("mistake", ["ties_larger", "no_max"])
+def test_route_checks_reject_planted_mistakes(mistake):
+    L = np.array([[1.0, 2.0, 2.0, 0.0, 2.0]], np.float32)
+    big = np.array([[200.0, 199.0, -50.0, 198.5]], np.float32)
+    ref_t, _, _ = O.moe_route_ref(L, 3)
+    ref_b, ref_wb, _ = O.moe_route_ref(big, 3)
+    got_t, _ = _planted_route(L, 3, mistake)
+    got_b, got_wb = _planted_route(big, 3, mistake)
+    with np.errstate(all="ignore"):
+        same = (np.array_equal(got_t, ref_t) and np.array_equal(got_b, ref_b)
+                and np.allclose(got_wb, ref_wb, rtol=1e-6))
+    assert not same
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_sigmoid_t_points(dtype):
+    s = O.sigmoid_t(np.array([0.0, 30.0, -30.0], np.float32), dtype)
+    assert s[0] == 0.5 and s[1] == 1.0 and s[2] < 1e-10
+    x = O.to_f32(O.from_f32(np.linspace(-8, 8, 257).astype(np.float32), dtype), dtype)
+    got = O.sigmoid_t(x, dtype)
+    exact = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    ulp = O.ulp_bf16(exact.astype(np.float32)) if dtype == "bfloat16" else O.ulp_f16(exact.astype(np.float32))
+    assert np.all(np.abs(got - exact) <= 2 * ulp)
+    sym = O.sigmoid_t(-x, dtype)
+    big = np.maximum(sym, got).astype(np.float32)   # the one >= 1/2 sets the rounding
+    ulp2 = O.ulp_bf16(big) if dtype == "bfloat16" else O.ulp_f16(big)
+    assert np.all(np.abs(sym - (1.0 - got)) <= 2 * ulp2)
+
+
+def test_route_shared_gate_is_sigmoid_of_rounded_dot():
+    rng = np.random.default_rng(3)
+    H = 64
+    x = O.from_f32((rng.integers(-4, 5, (2, H)) / 8.0).astype(np.float32), "bfloat16")
+    g = O.from_f32((rng.integers(-4, 5, H) / 4.0).astype(np.float32), "bfloat16")
+    _, _, sg = O.moe_route_ref(np.zeros((2, 4), np.float32), 1, x, g)
+    dot = O.to_f32(x, "bfloat16").astype(np.float64) @ O.to_f32(g, "bfloat16").astype(np.float64)
+    np.testing.assert_array_equal(sg, O.sigmoid_t(dot.astype(np.float32), "bfloat16"))
+
+
+def test_combine_shared_merge_known_roundings():
+    rng = np.random.default_rng(4)
+    rows, k, N = 3, 2, 16
+    y = O.from_f32((rng.integers(-8, 8, (rows * k, N)) / 4.0).astype(np.float32), "bfloat16")
+    w = np.array([0.5, 0.25, 1.0, 0.0, 2.0, -1.0], np.float32)
+    base = O.moe_combine_ref(y, None, w, rows, k)                # exact sums of quarters
+    zero = O.moe_combine_ref(y, None, w, rows, k, sgate=O.from_f32(np.zeros(rows, np.float32), "bfloat16"),
+                             shared=O.from_f32(rng.standard_normal((rows, N)).astype(np.float32), "bfloat16"))
+    np.testing.assert_array_equal(zero, O.to_f32(O.from_f32(base, "bfloat16"), "bfloat16"))
+    sh = (rng.integers(-8, 8, (rows, N)) / 2.0).astype(np.float32)
+    one = O.moe_combine_ref(y, None, w, rows, k, sgate=O.from_f32(np.ones(rows, np.float32), "bfloat16"),
+                            shared=O.from_f32(sh, "bfloat16"))
+    np.testing.assert_array_equal(one, base + sh)
