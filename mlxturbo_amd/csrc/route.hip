@@ -11,8 +11,8 @@
 // y = 1 / (1 + exp(|s|)), s < 0 ? y : 1 - y, each step rounded to T).
 //
 // CDNA4 design: one workgroup of 256 threads per row.  All four waves share
-// the shared-gate dot product (strided loads, DPP wave sums, four partials
-// in LDS); wave 0 then runs the top-k alone: lane l holds experts l, l + 64,
+// the shared-gate dot product (16-byte loads, all of a thread's in flight at
+// once, DPP wave sums, four partials in LDS); wave 0 then runs the top-k alone: lane l holds experts l, l + 64,
 // ... (up to 16 per lane for E <= 1024) as order-preserving integer keys,
 // and each round is a lane-local maximum plus two DPP wave reductions (the
 // largest key, then the smallest expert index holding it), no barrier.
@@ -113,7 +113,41 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     using T = T16<DT>;
     const uint16_t* xr = x + (int64_t)row * H;
     float acc = 0.0f;
-    for (int h = t; h < H; h += kRouteThreads) acc += T::to_f32(xr[h]) * T::to_f32(sgw[h]);
+    // 16-byte pieces of x and the gate weight (eight values each), four per
+    // thread in flight; a ragged or unaligned row goes element by element
+    const bool vec = H % 8 == 0 && (((uintptr_t)xr | (uintptr_t)sgw) & 15u) == 0;
+    if (vec) {
+      const u32x4* xv = reinterpret_cast<const u32x4*>(xr);
+      const u32x4* gv = reinterpret_cast<const u32x4*>(sgw);
+      for (int c0 = t; c0 < H / 8; c0 += 4 * kRouteThreads) {
+        u32x4 a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = c0 + i * kRouteThreads;
+          a[i] = c < H / 8 ? xv[c] : (u32x4){0u, 0u, 0u, 0u};
+          b[i] = c < H / 8 ? gv[c] : (u32x4){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            acc += T::to_f32((uint16_t)a[i][v]) * T::to_f32((uint16_t)b[i][v]);
+            acc += T::to_f32((uint16_t)(a[i][v] >> 16)) * T::to_f32((uint16_t)(b[i][v] >> 16));
+          }
+      }
+    } else {
+      for (int h0 = t; h0 < H; h0 += 8 * kRouteThreads) {
+        float a[8], b[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int h = h0 + i * kRouteThreads;
+          a[i] = h < H ? T::to_f32(xr[h]) : 0.0f;
+          b[i] = h < H ? T::to_f32(sgw[h]) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += a[i] * b[i];
+      }
+    }
     acc = wave_sum_f32(acc);
     if (lane == 0) s_part[wv] = acc;
     __syncthreads();

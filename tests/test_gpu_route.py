@@ -63,12 +63,13 @@ def test_route_batched_shape():
                  w.cpu().numpy().reshape(6, 8))
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-def test_route_shared_gate_exact_dot(dtype):
+@pytest.mark.parametrize("dtype,H", [("bfloat16", 2560), ("float16", 2560), ("bfloat16", 1001)])
+def test_route_shared_gate_exact_dot(dtype, H):
     # small dyadic values: every partial sum is exact in float32, so the
     # kernel's T(dot) is the oracle's and the sigmoid must match bit for bit
+    # (H = 1001: rows neither a multiple of 8 long nor 16-byte aligned)
     rng = np.random.default_rng(11)
-    rows, E, H = 8, 512, 2560
+    rows, E = 8, 512
     x = O.from_f32((rng.integers(-8, 9, (rows, H)) / 64.0).astype(np.float32), dtype)
     g = O.from_f32((rng.integers(-8, 9, H) / 256.0).astype(np.float32), dtype)
     logits = rng.standard_normal((rows, E)).astype(np.float32)
