@@ -730,7 +730,8 @@ def test_gather_glu_formats_and_paths(M, bits, gs, dtype, T):
 
 def test_gather_glu_prefill_composition():
     """1024+ output rows: two grouped gather_qmm calls, then SiLU-multiply in
-    float of their rounded outputs."""
+    float of their rounded outputs.  Each gather against the oracle at the
+    full contract; the composition bit for bit from the gathers' outputs."""
     rng = np.random.default_rng(91)
     E, N, K, T, top = 8, 96, 512, 300, 4
     def bank():
@@ -740,17 +741,25 @@ def test_gather_glu_prefill_composition():
     dev = lambda bk: (to_dev(bk[0]), to_dev(bk[1], "bfloat16"), to_dev(bk[2], "bfloat16"))  # noqa: E731
     idx = zipf_routing(rng, T, top, E)
     x = act(rng, (T, 1, 1, K))
-    out = mq.gather_glu(to_dev(x, "bfloat16"), *dev(gate), *dev(up),
-                        rhs_indices=torch.from_numpy(idx).cuda())
-    lhs, rhs = np.repeat(np.arange(T), top), idx.reshape(-1)
+    xd, rhs = to_dev(x, "bfloat16"), torch.from_numpy(idx).cuda()
+    out = mq.gather_glu(xd, *dev(gate), *dev(up), rhs_indices=rhs)
+    g = mq.gather_qmm(xd, *dev(gate), rhs_indices=rhs)
+    u = mq.gather_qmm(xd, *dev(up), rhs_indices=rhs)
+    lhs, flat = np.repeat(np.arange(T), top), idx.reshape(-1)
+    for got, bk in ((g, gate), (u, up)):
+        res = O.check_output(from_dev(got).reshape(T * top, 1, N),
+                             O.gather_qmm_ref(x.reshape(T, 1, K), *bk, lhs, flat))
+        assert res["ok"], res
+    want = (torch.nn.functional.silu(g.float()) * u.float()).to(g.dtype)
+    np.testing.assert_array_equal(bits16(out), bits16(want))
+    # and the whole chain against the oracle's own gathers, rounded to bf16,
+    # through a float64 SiLU-multiply: the full contract holds
     rb = lambda v: O.to_f32(O.from_f32(v, "bfloat16"), "bfloat16").astype(np.float64)  # noqa: E731
-    g = rb(O.gather_qmm_ref(x.reshape(T, 1, K), *gate, lhs, rhs))
-    u = rb(O.gather_qmm_ref(x.reshape(T, 1, K), *up, lhs, rhs))
-    ref = (g / (1 + np.exp(-g)) * u).astype(np.float32)
-    # g and u each carry one bf16 rounding that the fused kernel avoids; the
-    # reference models them, the sums' order remains
+    gr = rb(O.gather_qmm_ref(x.reshape(T, 1, K), *gate, lhs, flat))
+    ur = rb(O.gather_qmm_ref(x.reshape(T, 1, K), *up, lhs, flat))
+    ref = (gr / (1 + np.exp(-gr)) * ur).astype(np.float32)
     res = O.check_output(from_dev(out).reshape(T * top, 1, N), ref)
-    assert res["rel_l2"] < 2e-3, res
+    assert res["ok"], res
 
 
 @pytest.mark.parametrize("rows,top_k,N,sorted_", [(1, 8, 2048, False), (7, 8, 2048, True),
