@@ -159,7 +159,7 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
  * allocates its own temporaries).  The workspace is a static device array of
  * 4 MiB (MQ_GATHER_NOALLOC_SCRATCH_BYTES) that each GPU holds until the
  * process ends; it takes calls whose mq_gather_qmm_workspace_size(P, M) fits,
- * i.e. up to 262142 pairs, and larger ones return MQ_EINVAL.  The call
+ * i.e. up to 261375 pairs, and larger ones return MQ_EINVAL.  The call
  * allocates nothing.  Every call on one GPU shares that GPU's array, so calls
  * that overlap on one GPU (other streams, other threads) race: order them,
  * e.g. on one stream.  Arguments and results are those of mq_gather_qmm.

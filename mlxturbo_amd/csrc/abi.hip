@@ -145,7 +145,7 @@ int moe_combine_checked(const void* y, int64_t y_rows, const int32_t* inv, const
 
 extern "C" {
 
-int mq_version(void) { return 3; }
+int mq_version(void) { return 4; }
 
 const char* mq_last_error(void) { return g_last_error.c_str(); }
 

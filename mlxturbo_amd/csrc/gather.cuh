@@ -320,7 +320,7 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
   if (ncol * (P + E + 1) > INT32_MAX - 8) return kStatusUnsupported;
   if (!classes || M > 64) {
     if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
-    *nlaunch += 1;
+    *nlaunch += kPrepLaunches;
     return launch_grouped_class<DT, BITS, GS, BM>(x, w, s, b, lhs, out, P, B, M, N, K, E, ws, 0,
                                                   class_seg_bound(P, R, 0, E), st, nlaunch);
   }
@@ -343,7 +343,7 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
                      dim3(kWideNT), wide_lds_bytes<256>(), st, (const uint16_t*)x, w,
                      (const uint16_t*)s, (const uint16_t*)b, lhs, (uint16_t*)out,
                      (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K, (int)E);
-  *nlaunch += 2;
+  *nlaunch += kPrepLaunches + 1;
   return 0;
 }
 
@@ -364,7 +364,7 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
                      (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,
                      (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K,
                      (int)E, 0);
-  *nlaunch += 2;
+  *nlaunch += kPrepLaunches + 1;
   return 0;
 }
 
@@ -437,7 +437,7 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
   if (P > kGatherFusedMaxP) {
     if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
     wsp = (const int32_t*)ws;
-    *nlaunch += 1;
+    *nlaunch += kPrepLaunches;
   }
   // One workgroup per (segment bound, column slot); the kernel gives each
   // busy workgroup 1, 2, 4 or 8 slots in turn so that at most ~3 per CU are

@@ -218,14 +218,25 @@ constexpr int64_t kGroupedMinRows = 1024;
 
 // Workspace (int32): [0] nseg | perm[P] | seg_start[P] | seg_len[P] | seg_expert[P] |
 // header[4]: segments of size class 2 are [header[0], header[1]), class 1
-// [header[1], header[2]), class 0 [header[2], header[3]) (header[3] = nseg).
+// [header[1], header[2]), class 0 [header[2], header[3]) (header[3] = nseg) |
+// lower[kGatherPrepMaxE + 2]: for keys in order, lower[e] = first pair whose
+// key is >= e | order[ceil(P / kPrepChunk)]: 1 where chunk i of kPrepChunk
+// pairs is in key order (its first pair compared with the pair before).
+constexpr int kPrepChunk = 256;
 __host__ __device__ inline size_t gather_ws_header(int64_t P) { return 1 + 4 * (size_t)P; }
-__host__ __device__ inline size_t gather_ws_words(int64_t P) { return gather_ws_header(P) + 4; }
+__host__ __device__ inline size_t gather_ws_lower(int64_t P) { return gather_ws_header(P) + 4; }
+__host__ __device__ inline size_t gather_ws_order(int64_t P) {
+  return gather_ws_lower(P) + kGatherPrepMaxE + 2;
+}
+__host__ __device__ inline size_t gather_ws_words(int64_t P) {
+  return gather_ws_order(P) + (size_t)((P + kPrepChunk - 1) / kPrepChunk);
+}
 
 // Builds gather_qmm's segment tables for P pairs into ws (prep.hip): pairs
 // sorted by expert (E for invalid ones), cut into segments of up to R pairs,
 // or by size class (R2 pairs from C2 pairs per expert, R1 from C1, R below).
-// Needs E <= kGatherPrepMaxE; returns 0 or a HIP error.
+// kPrepLaunches kernels; needs E <= kGatherPrepMaxE; returns 0 or a HIP error.
+constexpr int kPrepLaunches = 2;
 int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, int64_t B, int R,
                 void* ws, hipStream_t st, int R1 = 0, int C1 = 0, int R2 = 0, int C2 = 0);
 

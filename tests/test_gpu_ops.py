@@ -552,7 +552,7 @@ def test_gather_prefill_size_classes(M, bits, gs, sort):
                         to_dev(b, "bfloat16"), lhs_indices=torch.from_numpy(lhs.astype(np.int32)).cuda(),
                         rhs_indices=torch.from_numpy(rhs).cuda(), group_size=gs, bits=bits,
                         sorted_indices=sort)
-    assert mq.launch_count() - n0 == 2                 # prep + the grouped kernel
+    assert mq.launch_count() - n0 == 3                 # two prep kernels + the grouped kernel
     ref = O.gather_qmm_ref(x.reshape(T, M, K), w, s, b, lhs, rhs, gs, bits)
     _check(out.reshape(idx.size, M, N), ref)
 
@@ -577,7 +577,7 @@ def test_gather_prefill_scale_blocks(bits, gs, dtype, K):
     n0 = mq.launch_count()
     out = mq.gather_qmm(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
                         rhs_indices=torch.from_numpy(idx).cuda(), group_size=gs, bits=bits)
-    assert mq.launch_count() - n0 == 2                 # prep + the grouped kernel
+    assert mq.launch_count() - n0 == 3                 # two prep kernels + the grouped kernel
     ref = O.gather_qmm_ref(x.reshape(T, 1, K), w, s, b, np.repeat(np.arange(T), top),
                            idx.reshape(-1), gs, bits, dtype)
     res = O.check_output(from_dev(out).reshape(T * top, 1, N), ref, dtype)
@@ -603,7 +603,7 @@ def test_gather_prefill_thin_experts(M, bits, gs, dtype):
     n0 = mq.launch_count()
     out = mq.gather_qmm(to_dev(x, dtype), to_dev(w), to_dev(s, dtype), to_dev(b, dtype),
                         rhs_indices=torch.from_numpy(idx).cuda(), group_size=gs, bits=bits)
-    assert mq.launch_count() - n0 == 2                 # prep + grouped kernel
+    assert mq.launch_count() - n0 == 3                 # two prep kernels + grouped kernel
     o = from_dev(out).reshape(T * top, M, N)
     flat = idx.reshape(-1)
     bad = (flat < 0) | (flat >= E)
@@ -641,6 +641,57 @@ def test_gather_sorted_prep_matches_counting_sort(T, top, M, K):
     rows = rng.choice(P, 64, replace=False)
     ref = O.gather_qmm_ref(x, w, s, b, rows, flat[rows])
     res = O.check_output(O.to_f32(out_sorted[rows].view(np.uint16), "bfloat16"), ref)
+    assert res["ok"], res
+
+
+def _sorted_cases(rng, E):
+    """Expert lists for the prep kernels' chunk logic (chunks of 256 pairs)."""
+    z = np.sort(rng.integers(0, E, 3000)).astype(np.int32)          # runs cross chunks
+    halves = np.concatenate([np.sort(rng.integers(0, E, 2048)),
+                             np.sort(rng.integers(0, E, 2048))]).astype(np.int32)
+    one = np.concatenate([np.full(2000, 3), np.full(5, E - 1)]).astype(np.int32)
+    tail = np.concatenate([np.sort(rng.integers(0, E, 1022)), [E, E + 7, 99]]).astype(np.int32)
+    return {"sorted": (z, True), "two_sorted_halves": (halves, False),
+            "one_hot_expert": (one, True), "invalid_tail_1025": (tail, True)}
+
+
+@pytest.mark.parametrize("case", ["sorted", "two_sorted_halves", "one_hot_expert",
+                                  "invalid_tail_1025"])
+def test_gather_prep_chunks(case):
+    """The prep's run kernel checks key order per chunk of 256 pairs (the
+    first pair of a chunk against the pair before it) and, where every chunk
+    is in order, writes each expert's first pair once: sorted runs crossing
+    chunks, two sorted halves (a descent exactly at a chunk boundary: the
+    counting sort must take over), one expert holding almost every pair
+    (long gaps of absent experts), out-of-range experts sorting last (key E)
+    with a one-pair last chunk.  Rows must equal the same pairs shuffled
+    (counting sort) bit for bit, zero where the expert is invalid, and the
+    oracle on sampled rows."""
+    rng = np.random.default_rng(["sorted", "two_sorted_halves", "one_hot_expert",
+                                 "invalid_tail_1025"].index(case) + 700)
+    E, N, K = 24, 160, 512
+    banks = [quantized(rng, N, K) for _ in range(E)]
+    w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
+    b = np.stack([t[2] for t in banks])
+    dev = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    flat, in_order = _sorted_cases(rng, E)[case]
+    assert in_order == bool(np.all(np.diff(np.where((flat >= 0) & (flat < E), flat, E)) >= 0))
+    P = flat.size
+    x = act(rng, (P, 1, K))
+    xd = to_dev(x, "bfloat16")
+    print(f"prep chunks case={case} P={P}", flush=True)
+    out = bits16(mq.gather_qmm(xd, *dev, rhs_indices=torch.from_numpy(flat).cuda(),
+                               sorted_indices=in_order))
+    shuf = rng.permutation(P)
+    out_shuf = bits16(mq.gather_qmm(xd[torch.from_numpy(shuf).cuda()], *dev,
+                                    rhs_indices=torch.from_numpy(flat[shuf]).cuda()))
+    np.testing.assert_array_equal(out_shuf, out[shuf])
+    bad = (flat < 0) | (flat >= E)
+    assert np.all(out.reshape(P, N)[bad] == 0)
+    ok = np.nonzero(~bad)[0]
+    rows = rng.choice(ok, 64, replace=False)
+    ref = O.gather_qmm_ref(x, w, s, b, rows, flat[rows])
+    res = O.check_output(O.to_f32(out[rows].view(np.uint16), "bfloat16"), ref)
     assert res["ok"], res
 
 

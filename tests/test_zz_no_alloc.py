@@ -67,7 +67,12 @@ def test_noalloc_gather_matches_workspace_entry():
 
 def test_noalloc_gather_refuses_oversize_calls():
     lib = _lib.lib()
-    P = 262143                                   # one pair past what 4 MiB of tables hold
+    lo, hi = 1024, 1 << 22                       # the first P whose tables pass 4 MiB
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        lo, hi = (mid, hi) if lib.mq_gather_qmm_workspace_size(mid, 1) <= SCRATCH else (lo, mid)
+    P = hi
+    assert 200000 < P < 262144                   # ~16 bytes of tables per pair
     assert lib.mq_gather_qmm_workspace_size(P, 1) > SCRATCH
     assert lib.mq_gather_qmm_workspace_size(P - 1, 1) <= SCRATCH
     fake = 256
