@@ -256,9 +256,11 @@ def measure_gather(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, n
 def measure_moe_layer(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidden=2048,
                       inter=512, nroute=64, seed=8):
     """One whole decode MoE layer of configs[3] (SwitchGLU with the fused
-    gate+up+SiLU route and router scores): gather_glu, the down gather_qmm
-    and the combine epilogue, three launches.  Algorithmic bytes: each
-    distinct expert's gate, up and down weights once, plus activations."""
+    gate+up+SiLU route and router scores): gather_glu, then the down
+    projection with the combine folded in (one or two tokens) or the down
+    gather_qmm and the combine epilogue; "launches" counts them.
+    Algorithmic bytes: each distinct expert's gate, up and down weights
+    once, plus activations."""
     from mlxturbo_amd import nn as mqnn
     rng = np.random.default_rng(seed + T)
     routes = [(zipf_routing(rng, T, top_k, E) if routing == "zipf" else
@@ -287,13 +289,16 @@ def measure_moe_layer(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidd
     def fn(i):
         layer(x, idx[i % nroute], scores)
 
+    n0 = mq.launch_count()
+    fn(0)
+    launches = mq.launch_count() - n0
     _, per_step = time_graph(torch, fn, steps, warmup)
     avg_bytes = sum(nbytes[i % nroute] for i in range(steps)) / steps
     del layer
     torch.cuda.empty_cache()
     return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
             "distinct_experts": round(sum(len(np.unique(r)) for r in routes) / nroute, 1),
-            "launches": 3}
+            "launches": int(launches)}
 
 
 def measure_gather_prefill(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, seed=5):

@@ -193,6 +193,30 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
                   void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /*
+ * MoE down projection with the combine folded in, at decode widths:
+ *   out[t, n] = T( sum_k weights[t*top_k + k] * y[t*top_k + k, n] ),
+ *   y[p, n]   = T( x[p] . dequantize(w[rhs[p]])[n]^T )
+ * i.e. mq_gather_qmm (x [T*top_k, K], one row per pair, lhs_indices NULL,
+ * M = 1) followed by mq_moe_combine (inv NULL), bit for bit, in one launch;
+ * with sgate and shared (dtype [T] and [T, N], both or neither) the shared
+ * expert is merged as mq_moe_combine_shared does.  The reference runs the two
+ * passes (kernels/moe_decode_fused.py:378-397 `down`, then
+ * kernels/moe_combine.py:160-195 or moe_route_decode.py:353-398 `combine`);
+ * its prefill path folds the router weight into the down projection's store
+ * instead (fused.py:3304-3315).  weights float32 [T*top_k], out [T, N].
+ * Up to 16 pairs (T * top_k <= 16), fewer where the gather tile splits K
+ * over 2 or 4 waves (8 or 4 pairs: each workgroup takes the call's segments
+ * in at most two rounds); other calls, and tile configurations this kernel
+ * does not cover, return MQ_EUNSUPPORTED, and the caller runs mq_gather_qmm
+ * + mq_moe_combine, which is faster there.  Out-of-range experts give y = 0.
+ */
+int mq_gather_qmm_combine(const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const int32_t* rhs_indices, const float* weights,
+                          const void* sgate, const void* shared, void* out, int64_t T,
+                          int64_t top_k, int64_t N, int64_t K, int64_t E, int group_size,
+                          int bits, int dtype, void* hip_stream);
+
+/*
  * MoE combine epilogue: out[t, n] = sum_k w[t*top_k + k] * y[inv[t*top_k + k], n]
  * for t < rows, accumulated in float in k order and rounded once to dtype.
  * Replaces kernels/moe_combine.py:160-195 (`combine(y, inv, w, rows, top_k)`,

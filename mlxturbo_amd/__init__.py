@@ -10,6 +10,8 @@ hand-written HIP kernels behind a C ABI (``include/mlxturbo_amd.h``):
 * :func:`gather_glu`       - fused MoE gate+up+SiLU at decode widths
 * :func:`moe_combine`      - MoE unsort + router weight + top-k sum epilogue
   (optionally merging the shared expert)
+* :func:`gather_qmm_combine` - MoE down projection with the combine folded in
+  (one kernel at decode widths)
 * :func:`moe_route`        - MoE top-k routing with softmax weights and the
   shared-expert gate
 
@@ -22,12 +24,13 @@ layers to another width (dequantize + quantize on the GPU).
 """
 
 from . import checkpoint, dispatch, nn, rebit
-from .ops import (dequantize, gather_glu, gather_qmm, launch_count, moe_combine, moe_route,
-                  quantize, quantized_matmul)
+from .ops import (dequantize, gather_glu, gather_qmm, gather_qmm_combine, launch_count,
+                  moe_combine, moe_route, quantize, quantized_matmul)
 
 __version__ = "0.2.0"
 
-__all__ = ["checkpoint", "rebit", "dequantize", "dispatch", "gather_glu", "gather_qmm", "launch_count",
+__all__ = ["checkpoint", "rebit", "dequantize", "dispatch", "gather_glu", "gather_qmm",
+           "gather_qmm_combine", "launch_count",
            "moe_combine", "moe_route",
            "nn", "quantize", "quantized_matmul",
            "__version__"]

@@ -35,6 +35,7 @@ EXPORTED = (
     "mq_gather_qmm",
     "mq_gather_qmm_noalloc",
     "mq_gather_glu",
+    "mq_gather_qmm_combine",
     "mq_moe_combine",
     "mq_moe_combine_shared",
     "mq_moe_route",
@@ -88,6 +89,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_gather_glu.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _int, _int, _int, _vp, ctypes.c_size_t,
                                   _vp]
+    lib.mq_gather_qmm_combine.restype = _int
+    lib.mq_gather_qmm_combine.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                          _i64, _i64, _i64, _i64, _int, _int, _int, _vp]
     lib.mq_moe_combine.restype = _int
     lib.mq_moe_combine.argtypes = [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]
 

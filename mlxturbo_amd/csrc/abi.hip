@@ -359,6 +359,39 @@ int mq_gather_glu(const void* x, const uint32_t* w_gate, const void* scales_gate
   return MQ_OK;
 }
 
+int mq_gather_qmm_combine(const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const int32_t* rhs_indices, const float* weights,
+                          const void* sgate, const void* shared, void* out, int64_t T,
+                          int64_t top_k, int64_t N, int64_t K, int64_t E, int group_size,
+                          int bits, int dtype, void* hip_stream) {
+  int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !out || !rhs_indices || !weights)
+    return fail(MQ_EINVAL, "x, out, rhs_indices and weights must be non-null");
+  if (T < 0 || top_k < 1 || E <= 0)
+    return fail(MQ_EINVAL, "invalid sizes T=%lld top_k=%lld E=%lld", (long long)T,
+                (long long)top_k, (long long)E);
+  if ((sgate != nullptr) != (shared != nullptr))
+    return fail(MQ_EINVAL, "sgate and shared are given together or not at all");
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (N > INT32_MAX || K > INT32_MAX || E > INT32_MAX || T * top_k > mq::kFoldMaxP)
+    return fail(MQ_EUNSUPPORTED, "gather_qmm_combine folds up to %d pairs per call (got %lld)",
+                mq::kFoldMaxP, (long long)(T * top_k));
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (T == 0 || N == 0) return MQ_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  int nl = 0;
+  rc = dispatch_16<mq::GatherFoldLaunch>(dtype, bits, group_size, x, w, scales, biases,
+                                         rhs_indices, weights, sgate, shared, out, T, top_k, N, K,
+                                         E, st, &nl);
+  if (rc) return fail(rc, "gather_qmm_combine: no folded kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "gather_qmm_combine: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
 
 int mq_moe_combine(const void* y, int64_t y_rows, const int32_t* inv, const float* w, void* out,
                    int64_t rows, int64_t top_k, int64_t N, int dtype, void* hip_stream) {

@@ -74,6 +74,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 #pragma unroll
   for (int v = 0; v < 4; ++v) o[v] = T::pack2(acc[2 * v], acc[2 * v + 1]);
   if constexpr (SH) {
+    // no contraction of the product into the sum (each is rounded to T)
+#pragma clang fp contract(off)
     const float sg = T::to_f32(sgate[t]);
     const u32x4 sh = *reinterpret_cast<const u32x4*>(shared + (int64_t)t * N + n);
 #pragma unroll

@@ -274,6 +274,152 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
   }
 }
 
+// ---- down projection with the MoE combine folded in (decode widths) -------
+// out[t, n] = T( sum_k w[t*top_k + k] * y[t*top_k + k, n] ) with
+// y[p] = T(x[p] . deq(W[rhs[p]])^T): mq_gather_qmm (one x row per pair)
+// followed by mq_moe_combine (inv = NULL), in one launch and bit for bit the
+// same, since every y is computed by the same tile code with the same K
+// split (gather_tile_waves) and the same segments, rounded to T, and summed
+// in k order with fma as the combine kernel does.  Optionally the shared
+// expert is merged as mq_moe_combine_shared does.
+//
+// Each workgroup owns 16 output columns for every token, so no sum crosses
+// workgroups (a cross-workgroup fold needs a device-scope release per
+// workgroup, which on MI355X writes back the XCD's L2 and cost more than the
+// launch it saves).  Its kFoldNW / NWT wave groups take the segments of the
+// call (pairs sharing an expert, up to 8) in rounds; each tile's y values go
+// to LDS, and after the last round the workgroup sums them per token.  With
+// only N / 16 workgroups, each round is a serial memory round trip: the
+// launcher takes calls of at most two rounds (config-4 down bank, zipf
+// routing, whole decode layer: T=1 15.3 us folded against 18.0 with the two
+// kernels; at T=4 / 8, three or more rounds, 31.4 / 48.4 against 28.5 /
+// 39.1, so those run the two kernels).
+constexpr int kFoldNW = 8;
+
+// A rows of a folded segment (one x row per pair): outputs go to the
+// workgroup's LDS copy of y, row = pair.
+struct FoldRows {
+  static constexpr bool kCombine = false;
+  const uint16_t* x;
+  uint32_t x_nrec;
+  uint16_t (*ys)[16];
+  const int* members;      // LDS
+  int K;
+  __device__ __forceinline__ int64_t xoff(int m) const { return (int64_t)members[m] * K; }
+  __device__ __forceinline__ void store(int m, int nn, uint16_t v) const { ys[members[m]][nn] = v; }
+};
+
+template <int DT, int BITS, int GS, int GPL, int NWT, int PF, bool SBL, bool SH>
+__global__ __launch_bounds__(64 * kFoldNW) void gather_fold_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const int32_t* __restrict__ rhs, const float* __restrict__ cw,
+    const uint16_t* __restrict__ sgate, const uint16_t* __restrict__ shared,
+    uint16_t* __restrict__ out, int P, int top_k, int N, int K, int E, int R) {
+  extern __shared__ __align__(16) unsigned char qmv_smem[];
+  constexpr int NW = kFoldNW, NG = NW / NWT, XM = kQmvMaxXM;
+  using T = T16<DT>;
+  __shared__ f32x4 red[NW][64];
+  __shared__ uint16_t s_y[kFoldMaxP][16];
+  __shared__ uint16_t s_sh[SH ? kFoldMaxP : 1][16];
+  __shared__ float s_w[kFoldMaxP];
+  __shared__ uint16_t s_sg[SH ? kFoldMaxP : 1];
+  __shared__ int s_members[NG][16];
+  const int t = threadIdx.x, lane = t & 63;
+  const int n0 = blockIdx.x * 16;
+  const int rows = min(16, N - n0);
+  const int ntok = P / top_k;
+  // router weights and the shared expert's columns load with the indices
+  if (t < P) s_w[t] = cw[t];
+  if constexpr (SH) {
+    for (int i = t; i < ntok * 16; i += 64 * NW) {
+      const int tok = i >> 4, nn = i & 15;
+      s_sh[tok][nn] = nn < rows ? shared[(int64_t)tok * N + n0 + nn] : (uint16_t)0;
+    }
+    if (t < ntok) s_sg[t] = sgate[t];
+  }
+  // every wave ranks the pairs itself (as the gather kernel does for P <= 64):
+  // lane p holds pair p's key (its expert, E when out of range) and cb = the
+  // number of earlier pairs with that key; pair p leads a segment when cb is
+  // a multiple of R, and segments are numbered by leader position
+  const int key = lane < P ? ((unsigned)rhs[lane] < (unsigned)E ? rhs[lane] : E) : -1;
+  int cb = 0;
+  for (int q = 0; q < P; ++q) {
+    const int kq = __builtin_amdgcn_readlane(key, q);
+    cb += (q < lane && kq == key) ? 1 : 0;
+  }
+  const bool lead = lane < P && (cb % R) == 0;
+  const uint64_t lmask = __builtin_amdgcn_ballot_w64(lead);
+  const int nseg = __builtin_popcountll(lmask);
+  const int rank = __builtin_popcountll(lmask & ((1ull << lane) - 1ull));
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int g = wave / NWT, kw = wave - g * NWT;
+  unsigned char* gsm = qmv_smem + g * gather_group_lds<BITS, GS, GPL>(NWT, XM, SBL, K / GS, 1);
+  const uint32_t rowB = (uint32_t)K * BITS / 8;
+  const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  const uint32_t x_nrec = (uint32_t)((int64_t)P * K * 2);
+  const int rounds = (nseg + NG - 1) / NG;
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int seg = rd * NG + g;                 // wave-uniform
+    int e = E, nmem = 1;
+    if (seg < nseg) {
+      const uint64_t mine = __builtin_amdgcn_ballot_w64(lead && rank == seg);
+      const int leader = __builtin_ctzll(mine);
+      e = __builtin_amdgcn_readlane(key, leader);
+      const int d = cb - __builtin_amdgcn_readlane(cb, leader);
+      const bool mem = lane < P && key == e && d >= 0 && d < R;
+      nmem = __builtin_popcountll(__builtin_amdgcn_ballot_w64(mem));
+      if (kw == 0 && mem) {
+        s_members[g][d] = lane;
+        if (e >= E) {                            // invalid pairs: y = 0
+          *reinterpret_cast<u32x4*>(&s_y[lane][0]) = (u32x4){0u, 0u, 0u, 0u};
+          *reinterpret_cast<u32x4*>(&s_y[lane][8]) = (u32x4){0u, 0u, 0u, 0u};
+        }
+      }
+    } else if (kw == 0 && lane == 0) {
+      s_members[g][0] = 0;                       // empty tile: a valid x row
+    }
+    __syncthreads();
+    const bool live = seg < nseg && e < E && rows > 0;
+    const int64_t row0 = (int64_t)(live ? e : 0) * N + (live ? n0 : 0);
+    QmvTiles<1> tl;
+    tl.w[0] = reinterpret_cast<const char*>(w) + row0 * rowB;
+    tl.s[0] = reinterpret_cast<const char*>(scales) + row0 * sRowB;
+    tl.b[0] = reinterpret_cast<const char*>(biases) + row0 * sRowB;
+    tl.rows[0] = live ? rows : 0;
+    const FoldRows src{x, x_nrec, s_y, s_members[g], K};
+    const int M = live ? nmem : 1;
+    if (M == 1)
+      qmv_tile<DT, BITS, GS, GPL, NWT, PF, 1, SBL, 1>(tl, M, K, src, gsm, red + g * NWT, kw,
+                                                     t - 64 * NWT * g);
+    else
+      qmv_tile<DT, BITS, GS, GPL, NWT, PF, XM, SBL, 1>(tl, M, K, src, gsm, red + g * NWT, kw,
+                                                      t - 64 * NWT * g);
+    __syncthreads();                             // s_members is rewritten next round
+  }
+  // the combine: per token, the router-weighted sum over its top_k pairs in
+  // k order, rounded once (then the shared expert's term, rounded, added)
+  for (int i = t; i < ntok * 16; i += 64 * NW) {
+    const int tok = i >> 4, nn = i & 15;
+    if (nn >= rows) continue;
+    float acc = 0.f;
+    for (int k = 0; k < top_k; ++k) {
+      const int p = tok * top_k + k;
+      acc = __builtin_fmaf(s_w[p], T::to_f32(s_y[p][nn]), acc);
+    }
+    uint16_t o = T::round1(acc);
+    if constexpr (SH) {
+      // no contraction: for fp16 the compiler narrows the product and the sum
+      // to half operations (exact) and would then fuse them into one fma_f16,
+      // skipping the product's rounding
+#pragma clang fp contract(off)
+      const uint16_t m = T::round1(T::to_f32(s_sg[tok]) * T::to_f32(s_sh[tok][nn]));
+      o = T::round1(T::to_f32(o) + T::to_f32(m));
+    }
+    out[(int64_t)tok * N + n0 + nn] = o;
+  }
+}
+
 // One launch of the expert-grouped wide tile (BM rows) over the prep
 // tables' size class cls, whose segments number at most seg_bound.
 template <int DT, int BITS, int GS, int BM>
@@ -392,6 +538,24 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
                                              nlaunch, true);
 }
 
+// Waves per 16-row tile of the streaming gather kernel (its K split): 4 or 2
+// only while the tiles are few (about 2048 waves in all) and each wave gets
+// a step, and none for one or two steps.  Config-4 banks, zipf routing:
+// gate/up T=1 6.9 us split 4 ways against 8.8 unsplit, T=8 22 unsplit
+// against 30 split 4 ways; down T=4 10.0 unsplit against 12.2, T=1 (two
+// steps) the same either way.  A tile's float sum depends on it, so the
+// folded down projection below takes the same count.
+template <int BITS, int GS>
+inline int gather_tile_waves(int64_t max_seg, int64_t N, int64_t K) {
+  using Gm = QmvGeom<BITS, GS, QmvConf<BITS, GS>::GPL>;
+  const int64_t nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
+  const int64_t tiles = max_seg * ((N + 15) / 16);
+  if (nsteps <= 2) return 1;
+  int nwt = 4;
+  while (nwt > 1 && (nwt > nsteps || tiles * nwt > 2048)) nwt /= 2;
+  return nwt;
+}
+
 // The streaming gather kernel over segments (GLU: fused gate+up+SiLU with the
 // up bank in w2 / s2 / b2).
 template <int DT, int BITS, int GS, bool GLU>
@@ -401,7 +565,6 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
                              int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
                              hipStream_t st, int* nlaunch) {
   using C = QmvConf<BITS, GS>;
-  using Gm = QmvGeom<BITS, GS, C::GPL>;
   // Segments of up to R pairs; R * M <= 8 A rows stream x through LDS, one
   // pair of more than 8 rows reads x fragments from global memory.  A segment
   // holds at most one pair per x batch in the usual MoE call (each token
@@ -415,14 +578,7 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
     const int64_t bound = (P + R - 1) / R + E + 1;
     if (bound < max_seg) max_seg = bound;
   }
-  // waves per tile: split K over 4 or 2 waves only while the tiles are few
-  // (about 2048 waves in all) and each wave gets a step.  Config-4 banks,
-  // zipf routing: gate/up T=1 6.9 us split 4 ways against 8.8 unsplit, T=8
-  // 22 unsplit against 30 split 4 ways; down T=4 10.0 unsplit against 12.2.
-  const int64_t nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
-  const int64_t tiles = max_seg * ((N + 15) / 16);
-  int nwt = 4;
-  while (nwt > 1 && (nwt > nsteps || tiles * nwt > 2048)) nwt /= 2;
+  const int nwt = gather_tile_waves<BITS, GS>(max_seg, N, K);
   const int ng = C::NW / nwt;
   constexpr int TJ = GLU ? 2 : 1;
   const bool sbl =
@@ -502,6 +658,55 @@ int GluLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const void* 
   if ((N + 15) / 16 > 65535 || P * M >= kGroupedMinRows) return kStatusUnsupported;
   return gather_qmv_launch<DT, BITS, GS, true>(x, wg, sg, bg, wu, su, bu, lhs, rhs, out, P, B, M,
                                                N, K, E, ws, st, nlaunch);
+}
+
+
+template <int DT, int BITS, int GS>
+int GatherFoldLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
+                                        const void* b, const int32_t* rhs, const float* cw,
+                                        const void* sgate, const void* shared, void* out,
+                                        int64_t T, int64_t top_k, int64_t N, int64_t K, int64_t E,
+                                        hipStream_t st, int* nlaunch) {
+  using C = QmvConf<BITS, GS>;
+  const int64_t P = T * top_k;
+  if (P < 1 || P > kFoldMaxP || P * K * 2 >= ((int64_t)1 << 31) || N > INT32_MAX)
+    return kStatusUnsupported;
+  const int R = (int)(P < kQmvMaxXM ? P : kQmvMaxXM);
+  const int nwt = gather_tile_waves<BITS, GS>(P, N, K);
+  if (P > 2 * (kFoldNW / nwt)) return kStatusUnsupported;   // more than two rounds
+  // scales copied to LDS where the gather kernel copies them (the same tile
+  // code either way)
+  const bool sbl = qmv_sb_fits(K / GS, nwt, 1, s, b);
+  const size_t lds = (size_t)(kFoldNW / nwt) *
+                     gather_group_lds<BITS, GS, C::GPL>(nwt, kQmvMaxXM, sbl, (int)(K / GS), 1);
+  // group-size-128 steps are 512 codes: eight streamed x rows per wave take
+  // 8 KiB, so the limit is raised past the default 64 KiB once per kernel
+  constexpr size_t kFoldMaxLds = 128 * 1024;
+  if (lds > kFoldMaxLds) return kStatusUnsupported;
+  const dim3 grid((unsigned)((N + 15) / 16));
+  const bool sh = shared != nullptr;
+#define MQ_FOLD(WT, SB, SH)                                                                     \
+  if (nwt == WT && sbl == SB && sh == SH) {                                                      \
+    static std::atomic<uint64_t> lds_set{0};                                                     \
+    if (hipError_t e = ensure_lds_limit(                                                         \
+            reinterpret_cast<const void*>(                                                       \
+                &gather_fold_kernel<DT, BITS, GS, C::GPL, WT, C::PF, SB, SH>),                   \
+            (int)kFoldMaxLds, lds_set))                                                          \
+      return (int)e;                                                                             \
+    hipLaunchKernelGGL((gather_fold_kernel<DT, BITS, GS, C::GPL, WT, C::PF, SB, SH>), grid,      \
+                       dim3(64 * kFoldNW), lds, st, (const uint16_t*)x, w, (const uint16_t*)s,   \
+                       (const uint16_t*)b, rhs, cw, (const uint16_t*)sgate,                      \
+                       (const uint16_t*)shared, (uint16_t*)out, (int)P, (int)top_k, (int)N,      \
+                       (int)K, (int)E, R);                                                       \
+    *nlaunch += 1;                                                                               \
+    return 0;                                                                                    \
+  }
+  MQ_FOLD(1, true, false) MQ_FOLD(2, true, false) MQ_FOLD(4, true, false)
+  MQ_FOLD(1, true, true) MQ_FOLD(2, true, true) MQ_FOLD(4, true, true)
+  MQ_FOLD(1, false, false) MQ_FOLD(2, false, false) MQ_FOLD(4, false, false)
+  MQ_FOLD(1, false, true) MQ_FOLD(2, false, true) MQ_FOLD(4, false, true)
+#undef MQ_FOLD
+  return kStatusUnsupported;
 }
 
 }  // namespace mq

@@ -1,7 +1,8 @@
 // Kernel instantiations of one (dtype, bits) pair for every group size.  The
 // build compiles this file once per pair with -DMQ_INST_DT=<0|1> and
 // -DMQ_INST_BITS=<4|8>, and once more per pair with -DMQ_INST_GLU for the
-// fused gate+up kernels; abi.hip calls the launchers through launch.h.
+// fused gate+up and folded down + combine kernels; abi.hip calls the
+// launchers through launch.h.
 #include "launch.h"
 #include "dequant.cuh"
 #include "gather.cuh"
@@ -15,7 +16,9 @@
 namespace mq {
 
 #ifdef MQ_INST_GLU
-#define MQ_INST(GS) template struct GluLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
+#define MQ_INST(GS)                                                  \
+  template struct GluLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;           \
+  template struct GatherFoldLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
 #else
 #define MQ_INST(GS)                                                  \
   template struct DequantLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;       \

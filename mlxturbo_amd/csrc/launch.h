@@ -56,6 +56,23 @@ struct GluLaunch {
                  int64_t K, int64_t E, void* ws, hipStream_t st, int* nlaunch);
 };
 
+// Down projection with the MoE combine folded in (gather.cuh), decode widths:
+// x [T * top_k, K] (one row per pair), rhs and cw (float router weights)
+// [T * top_k], out [T, N] = the combine of mq_moe_combine (inv = NULL) over
+// mq_gather_qmm's output, bit for bit; sgate / shared (both or neither) merge
+// the shared expert.  kStatusUnsupported beyond kFoldMaxP pairs, beyond two
+// rounds of segments per workgroup (8 / 4 pairs where the tile splits K over
+// 2 / 4 waves) or where the tile configuration does not fit: the caller then
+// runs the two kernels, which are faster there.
+constexpr int kFoldMaxP = 16;
+template <int DT, int BITS, int GS>
+struct GatherFoldLaunch {
+  static int run(const void* x, const uint32_t* w, const void* s, const void* b,
+                 const int32_t* rhs, const float* cw, const void* sgate, const void* shared,
+                 void* out, int64_t T, int64_t top_k, int64_t N, int64_t K, int64_t E,
+                 hipStream_t st, int* nlaunch);
+};
+
 // MoE routing (route.hip): per row of float logits [rows, E] the top_k
 // experts (descending, equal values by smaller index) into idx and their
 // softmax weights into w; with x ([rows, H]) and sgw ([H]) non-null (dtype

@@ -171,6 +171,16 @@ class SwitchGLU(torch.nn.Module):
                 and u.bias is None and g.weight.shape == u.weight.shape
                 and (g.group_size, g.bits, g.mode) == (u.group_size, u.bits, u.mode))
 
+    def _down_combine(self, h: torch.Tensor, idx: torch.Tensor,
+                      scores: torch.Tensor) -> torch.Tensor:
+        """Down projection of h (one row per pair, pairs in (token, k)
+        order) and the router-weighted top-k sum: one kernel at decode widths
+        (:func:`ops.gather_qmm_combine`), identical to the two passes."""
+        d = self.down_proj
+        return ops.gather_qmm_combine(h, d.weight, d.scales, d.biases, idx,
+                                      scores.reshape(idx.shape), group_size=d.group_size,
+                                      bits=d.bits, mode=d.mode)
+
     def forward(self, x: torch.Tensor, indices: torch.Tensor,
                 scores: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x: (..., K), indices: (..., top_k) -> (..., top_k, K_out); with
@@ -187,6 +197,9 @@ class SwitchGLU(torch.nn.Module):
             h = ops.gather_glu(xe, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases,
                                rhs_indices=idx, group_size=g.group_size, bits=g.bits,
                                mode=g.mode)                        # (T, k, 1, I)
+            if scores is not None and self.down_proj.bias is None:
+                out = self._down_combine(h, idx, scores)
+                return out.reshape(*lead, out.shape[-1])
             y = self.down_proj(h, idx)                             # (T, k, 1, N)
             if scores is not None:
                 out = ops.moe_combine(y.reshape(-1, y.shape[-1]), None, scores.reshape(-1),
@@ -207,6 +220,9 @@ class SwitchGLU(torch.nn.Module):
         # SwiGLU in T as MLX evaluates it: each op in float, rounded to T
         act = torch.nn.functional.silu(g.float()).to(g.dtype)
         h = (act.float() * u.float()).to(g.dtype)
+        if scores is not None and not do_sort and self.down_proj.bias is None:
+            out = self._down_combine(h, idx, scores)
+            return out.reshape(*lead, out.shape[-1])
         y = self.down_proj(h, idx_use, sorted_indices=do_sort)  # (T or P, k, 1, N)
         if scores is not None:
             rows = idx.shape[0]

@@ -638,6 +638,78 @@ def gather_glu(x: torch.Tensor, gate_w: torch.Tensor, gate_scales: torch.Tensor,
 # mq_gather_glu fuses below this many output rows (P * M)
 _GLU_FUSED_MAX_ROWS = 1024
 
+# mq_gather_qmm_combine folds up to this many (token, expert) pairs
+_FOLD_MAX_P = 16
+_EUNSUPPORTED = -2
+
+
+def gather_qmm_combine(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                       biases: Optional[torch.Tensor], rhs_indices: torch.Tensor,
+                       weights: torch.Tensor, transpose: bool = True, group_size: int = 64,
+                       bits: int = 4, mode: str = "affine", sgate: Optional[torch.Tensor] = None,
+                       shared: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """MoE down projection and combine: ``x`` holds one row per (token,
+    expert) pair (``(T, top_k, 1, K)`` or anything of ``T * top_k * K``
+    elements), ``rhs_indices`` ``(T, top_k)`` the experts, ``weights`` the
+    router weights of the same shape; returns ``(T, N)`` =
+    ``moe_combine(gather_qmm(x, w, ..., rhs_indices), None, weights, T,
+    top_k, sgate, shared)``, bit for bit.
+
+    For one or two decode tokens (up to 16 pairs) it is one kernel
+    (mq_gather_qmm_combine: each workgroup computes 16 output columns of
+    every pair and sums them per token), where the reference runs its decode
+    down kernel and then the combine (kernels/moe_decode_fused.py:378-397,
+    kernels/moe_combine.py:160-195); otherwise, and for configurations that
+    kernel does not take, the two calls run (faster there)."""
+    dev = _require_gpu(x, w, scales, biases, rhs_indices, weights, sgate, shared)
+    if rhs_indices.ndim < 1 or rhs_indices.shape[-1] < 1:
+        raise ValueError("rhs_indices must be (..., top_k)")
+    top_k = int(rhs_indices.shape[-1])
+    T = rhs_indices.numel() // top_k
+    if weights.numel() != T * top_k:
+        raise ValueError(f"weights has {weights.numel()} entries, expected {T * top_k}")
+    if x.numel() != T * top_k * x.shape[-1]:
+        raise ValueError("x must hold one row per (token, expert) pair")
+    xs = x.reshape(T, top_k, 1, x.shape[-1])
+    idx = rhs_indices.reshape(T, top_k)
+    if (sgate is None) != (shared is None):
+        raise ValueError("sgate and shared are given together")
+
+    def composed():
+        y = gather_qmm(xs, w, scales, biases, rhs_indices=idx, transpose=transpose,
+                       group_size=group_size, bits=bits, mode=mode)
+        return moe_combine(y.reshape(T * top_k, y.shape[-1]), None, weights, T, top_k, sgate,
+                           shared)
+
+    if T == 0 or T * top_k > _FOLD_MAX_P:
+        return composed()
+    out_pairs, a = _gather_prep(xs, [(w, scales, biases)], None, idx, transpose, group_size,
+                                bits, mode)
+    if a is None or a["route"] != "kernel" or a["M"] != 1 or a["dtype"] != x.dtype:
+        return composed()
+    N = a["N"]
+    if shared is not None:
+        if sgate.numel() != T or tuple(shared.shape) != (T, N):
+            raise ValueError(f"sgate must hold {T} gates and shared be ({T}, {N})")
+        if sgate.dtype != x.dtype or shared.dtype != x.dtype:
+            raise ValueError("sgate and shared must have x's dtype")
+    del out_pairs
+    out = torch.empty((T, N), dtype=x.dtype, device=dev)
+    w_ = weights.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    sg_ = sgate.reshape(-1).contiguous() if sgate is not None else None
+    sh_ = shared.contiguous() if shared is not None else None
+    x_ = _aligned(a["x"])
+    lib = _lib.lib()
+    rc = lib.mq_gather_qmm_combine(x_.data_ptr(), *[t.data_ptr() for t in a["flat"]],
+                                   a["rhs"].data_ptr(), w_.data_ptr(), _ptr(sg_), _ptr(sh_),
+                                   out.data_ptr(), T, top_k, N, a["K"], a["E"], group_size, bits,
+                                   _DTYPE_CODE[x.dtype], _stream_ptr(out))
+    if rc == _EUNSUPPORTED:
+        return composed()
+    _lib.check(rc, "gather_qmm_combine")
+    return out
+
+
 def moe_combine(y: torch.Tensor, inv: Optional[torch.Tensor], w: torch.Tensor, rows: int,
                 top_k: int, sgate: Optional[torch.Tensor] = None,
                 shared: Optional[torch.Tensor] = None) -> torch.Tensor:

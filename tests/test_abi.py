@@ -134,6 +134,20 @@ def test_gather_argument_validation(lib):
     assert lib.mq_gather_qmm_workspace_size(4096, 1) >= 4 * (1 + 4 * 4096)
 
 
+def test_gather_combine_argument_validation(lib):
+    f = lib.mq_gather_qmm_combine
+    def call(weights=FAKE, sgate=None, shared=None, T=1, top_k=8, dtype=0, x=FAKE):
+        return f(x, FAKE, FAKE, FAKE, FAKE, weights, sgate, shared, FAKE, T, top_k, 2048, 512,
+                 64, 64, 4, dtype, None)
+    assert call(weights=None) == -1 and "non-null" in lib.mq_last_error().decode()
+    assert call(sgate=FAKE) == -1 and "together" in lib.mq_last_error().decode()
+    assert call(top_k=0) == -1
+    assert call(T=3) == -2 and "up to 16 pairs" in lib.mq_last_error().decode()
+    assert call(dtype=2) == -2
+    assert call(x=FAKE + 2) == -1 and "aligned" in lib.mq_last_error().decode()
+    assert call(T=0) == 0
+
+
 def test_dequant_argument_validation(lib):
     rc = lib.mq_dequantize(FAKE, FAKE, None, FAKE, 4, 256, 64, 4, 0, None)
     assert rc == -1
@@ -249,6 +263,18 @@ class _FakeLib:
 
     def mq_quantize(self, w, wq, s, b, N, K, gs, bits, dtype, stream):
         self.calls.append(("quant", dict(N=N, K=K, gs=gs, bits=bits, dtype=dtype)))
+        return 0
+
+    def mq_gather_qmm_combine(self, x, w, s, b, rhs, wts, sg, sh, out, T, top_k, N, K, E, gs,
+                              bits, dtype, stream):
+        n = T * top_k
+        read_i = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int32)),
+                                                 shape=(n,)).copy()
+        read_f = lambda p: np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)),
+                                                 shape=(n,)).copy()
+        self.calls.append(("fold", dict(T=T, top_k=top_k, N=N, K=K, E=E, gs=gs, bits=bits,
+                                        dtype=dtype, rhs=read_i(rhs), w=read_f(wts),
+                                        sg=bool(sg), sh=bool(sh))))
         return 0
 
     def mq_moe_combine(self, y, y_rows, inv, w, out, rows, top_k, N, dtype, stream):
@@ -502,6 +528,34 @@ def test_combine_passes_indices_and_weights(fake):
         mlxturbo_amd.moe_combine(y[:5], None, w, rows, top_k)
     with pytest.raises(ValueError):
         mlxturbo_amd.moe_combine(y, inv[:4], w, rows, top_k)
+
+
+def test_gather_combine_folds_or_composes(fake):
+    E, N, K, top = 8, 64, 256, 4
+    bank = _qweights(N, K, E=E)
+    for T in (3, 16):
+        x = torch.zeros(T, top, 1, K, dtype=torch.bfloat16)
+        idx = torch.randint(0, E, (T, top), dtype=torch.int32)
+        w = torch.rand(T, top, dtype=torch.float64)
+        fake.calls.clear()
+        out = mlxturbo_amd.gather_qmm_combine(x, *bank, idx, w)
+        assert out.shape == (T, N) and out.dtype == torch.bfloat16
+        if T * top <= 16:                   # one folded kernel
+            [(kind, c)] = fake.calls
+            assert kind == "fold" and (c["T"], c["top_k"], c["N"], c["K"], c["E"]) == (T, top, N, K, E)
+            np.testing.assert_array_equal(c["rhs"], idx.reshape(-1).numpy())
+            np.testing.assert_array_equal(c["w"], w.reshape(-1).numpy().astype(np.float32))
+            assert not c["sh"]
+        else:                               # beyond 64 pairs: the two passes
+            assert [k for k, _ in fake.calls] == ["gather", "combine"]
+            assert fake.calls[1][1]["inv"] is None
+    with pytest.raises(ValueError, match="one row per"):
+        mlxturbo_amd.gather_qmm_combine(torch.zeros(3, top, 2, K, dtype=torch.bfloat16), *bank,
+                                        torch.zeros(3, top, dtype=torch.int32), torch.rand(3, top))
+    with pytest.raises(ValueError, match="together"):
+        mlxturbo_amd.gather_qmm_combine(torch.zeros(3, top, 1, K, dtype=torch.bfloat16), *bank,
+                                        torch.zeros(3, top, dtype=torch.int32), torch.rand(3, top),
+                                        sgate=torch.zeros(3, dtype=torch.bfloat16))
 
 
 def test_glu_passes_both_banks(fake):
