@@ -502,14 +502,25 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
                                hipStream_t st, int* nlaunch) {
   const int R = (int)(kThinBM / M);
   if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
+  // 4 waves (256 columns) per workgroup at short K, 8 (512 columns, so each
+  // x tile serves twice the columns) above K = 1024: config-4 banks, 2048
+  // tokens x top-8, one process: down (K=512) 143 / 122 us zipf / uniform
+  // with 4 against 173 / 141 with 8; gate/up (K=2048) 279 / 222 with 8
+  // against 302 / 253 for the size-class wide tiles and 282 / 264 with 16
+  // waves (whose 128-register budget spills)
+  const int nwv = K <= 1024 ? 4 : 8;
   const int64_t segs = class_seg_bound(P, R, 0, E);
-  const int64_t ntiles = (N + kWideBN - 1) / kWideBN * segs;
+  const int64_t ntiles = (N + 64 * nwv - 1) / (64 * nwv) * segs;
   if (ntiles > INT32_MAX - 8) return kStatusUnsupported;
   const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
-  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2>), grid, dim3(kThinNT), 0, st,
-                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,
-                     (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K,
-                     (int)E, 0);
+#define MQ_THIN(NWV)                                                                            \
+  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV>), grid, dim3(64 * NWV), 0,   \
+                     st, (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,     \
+                     (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K, \
+                     (int)E, 0)
+  if (nwv == 4) MQ_THIN(4);
+  else MQ_THIN(8);
+#undef MQ_THIN
   *nlaunch += kPrepLaunches + 1;
   return 0;
 }
@@ -527,11 +538,12 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
   if (rows_per_expert >= 96)
     return launch_grouped_bm<DT, BITS, GS, 128>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
                                                 st, nlaunch, false);
-  // thin experts: the register-B kernel wins on short K (config-4 down bank,
-  // K=512: 201-209 against 265-270 us); at K=2048 the LDS-shared wide tile
-  // stays ahead with uniform routing (341-352 against 427 us), with taller
-  // tiles for the experts that turn out hot
-  if (K <= 1024)
+  // thin experts: the register-B kernel (config-4 down bank, K=512: 201-209
+  // against 265-270 us for the wide tile; gate/up, K=2048, with 8 waves per
+  // workgroup: 279 / 222 us zipf / uniform against 302 / 253); beyond K =
+  // 2048 (not measured) the LDS-shared wide tile, with taller tiles for the
+  // experts that turn out hot
+  if (K <= 2048)
     return launch_grouped_thin<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
                                              nlaunch);
   return launch_grouped_bm<DT, BITS, GS, 64>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,

@@ -10,7 +10,7 @@
 // weights to LDS per k-step and reads them back from every wave row for only
 // 64 x rows, needs 92 KB of LDS (one workgroup per CU) and measured 1.4 TB/s.
 //
-// CDNA4 design: a workgroup of 4 waves owns (segment of <= 64 rows, 256
+// CDNA4 design: a workgroup of NWV waves owns (segment of <= 64 rows, 64 NWV
 // weight columns); wave w owns columns 64 w .. 64 w + 63 as two 32-column
 // blocks.  Per 64-code k-step, lane l (h = l >> 5) loads 32 codes of column
 // (l & 31) of each block, k = 32 h .. 32 h + 31 of the step (one 16-byte load
@@ -19,32 +19,38 @@
 // of the lane's 32; A rows use the same k order), so weights never touch
 // LDS.  Only the x tile (64 rows x 64 codes, 9 KB) is staged in LDS, double
 // buffered; 18 KB of LDS per workgroup leaves room for several workgroups
-// per CU.  Global loads run PS k-steps ahead in registers (two measured
-// best: deeper prefetch lowered occupancy and lost 10-15% on the down bank).
-// 32-row blocks past the segment's rows skip their MFMAs.  Measured on the
+// per CU.  Every column tile of a segment re-reads its x tile, and those
+// re-reads cost as much as the weight stream's access shape (a load-only
+// probe: 94 us for the gate/up bank's weights, 132 with the x tiles of four
+// column tiles), so long K takes 8 waves (512 columns per x tile).  Global
+// loads run PS k-steps ahead in registers (two measured best: deeper
+// prefetch lowered occupancy and lost 10-15% on the down bank).  32-row
+// blocks past the segment's rows skip their MFMAs.  Measured on the
 // config-4 banks at 2048 tokens x top-8 (prep included): down (K=512) 201-212
-// us against 265-270 for the wide tile; gate/up (K=2048) 427-475 against
-// 341-462 (its loads alone take ~200 us and the dequant + MFMA work does not
-// overlap them), so only short K is routed here.
+// us with 4 waves against 265-270 for the wide tile; gate/up (K=2048)
+// 427-475 with 4 waves against 341-462 for the wide tile, and with 8 waves
+// 279 / 222 zipf / uniform against 302 / 253 (one process, eager loops).
 #pragma once
 #include "qmm_wide.cuh"
 
 namespace mq {
 
-constexpr int kThinBM = 64, kThinNT = 256;
+constexpr int kThinBM = 64;
 
-// 1-D grid of ceil(N / 256) x segment bound workgroups (tiles placed by
-// grouped_tile), 256 threads; segments of size class cls of the prep
+// 1-D grid of ceil(N / (64 NWV)) x segment bound workgroups (tiles placed by
+// grouped_tile), 64 NWV threads; segments of size class cls of the prep
 // tables in ws hold up to 64 / Mi pairs of one expert; pair p contributes
 // rows p*Mi .. p*Mi+Mi-1 and reads x batch x_batch(lhs, p, P, B).  Segments of
 // out-of-range experts write zeros.  K % 64 == 0, B * Mi * K * 2 < 2^31.
-template <int DT, int BITS, int GS, int PS>
-__global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
+template <int DT, int BITS, int GS, int PS, int NWV>
+__global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
     int P, int B, int Mi, int N, int K, int E, int cls) {
-  constexpr int BM = kThinBM, BN = kWideBN, BK = kWideBK, LD = kWideLD, NT = kThinNT;
+  constexpr int BM = kThinBM, BN = 64 * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
+  constexpr int XT = BM * 8;                    // 16-byte x pieces per step
+  constexpr int XI = XT >= NT ? XT / NT : 1;    // x pieces per thread per step
   constexpr int WB = BITS / 4;                  // 16-byte loads per lane per block per step
   static_assert(GS >= 32, "a lane's 32 codes lie in one group");
   using T = T16<DT>;
@@ -100,18 +106,19 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
     wo[j] = (uint32_t)(c * Kw * 4) + (uint32_t)h * 16u * WB;
     so[j] = (uint32_t)c * (uint32_t)G * 2u;
   }
-  // x: thread t stages rows (t >> 3) + 32 i, codes 8 (t & 7) .. +8 of the step
-  uint32_t xo[2];
-  int xl[2];
+  // x: thread t stages rows (t >> 3) + (NT / 8) i, codes 8 (t & 7) .. +8 of
+  // the step
+  uint32_t xo[XI];
+  int xl[XI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (t >> 3) + 32 * i;
-    const uint32_t ro = s_xoff[r];
+  for (int i = 0; i < XI; ++i) {
+    const int r = min((t >> 3) + (NT / 8) * i, BM - 1);   // threads past XT: no piece
+    const uint32_t ro = (XT >= NT || t < XT) ? s_xoff[r] : 0xffffffffu;
     xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
     xl[i] = r * LD + 8 * (t & 7);
   }
   struct Stage {
-    u32x4 xa[2];
+    u32x4 xa[XI];
     u32x4 wv[2][WB];
     uint16_t s[2], b[2];
   };
@@ -137,7 +144,7 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
   auto gload = [&](Stage& st, int kt, bool per_step) {
     const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < XI; ++i)
       st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], k0 * 2, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -152,8 +159,10 @@ __global__ __launch_bounds__(kThinNT) void qmm_grouped_thin_kernel(
     }
   };
   auto store_x = [&](const Stage& st, int buf) {
+    if (XT >= NT || t < XT) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&As[buf][xl[i]]) = st.xa[i];
+      for (int i = 0; i < XI; ++i) *reinterpret_cast<u32x4*>(&As[buf][xl[i]]) = st.xa[i];
+    }
   };
 
   f32x16 acc[2][2];

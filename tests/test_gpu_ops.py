@@ -529,14 +529,14 @@ def test_gather_prefill_grouped(M, bits, gs):
 @pytest.mark.parametrize("M,bits,gs,sort", [(1, 4, 64, True), (1, 4, 64, False),
                                              (2, 8, 64, True), (2, 4, 32, False)])
 def test_gather_prefill_size_classes(M, bits, gs, sort):
-    """Long K with few rows per expert on average: the prep tables cut each
-    expert by its own row count (256-row tiles from 192 rows, 128-row tiles
-    from 96, 64-row tiles below) and one grouped launch runs all classes.
+    """K past 2048 with few rows per expert on average: the prep tables cut
+    each expert by its own row count (256-row tiles from 192 rows, 128-row
+    tiles from 96, 64-row tiles below) and one grouped launch runs all classes.
     Zipf routing over 48 experts gives all three classes (43 or 85 rows per
     expert on average: below 96, where one tile height would serve all);
     expert-sorted pairs (mlx-lm's _gather_sort) and shuffled ones; ragged N."""
     rng = np.random.default_rng(90 + M + bits + gs)
-    E, N, K, T, top = 48, 300, 1088, 512, 4
+    E, N, K, T, top = 48, 300, 2176, 512, 4
     banks = [quantized(rng, N, K, gs=gs, bits=bits) for _ in range(E)]
     w = np.stack([t[0] for t in banks]); s = np.stack([t[1] for t in banks])
     b = np.stack([t[2] for t in banks])
@@ -557,16 +557,17 @@ def test_gather_prefill_size_classes(M, bits, gs, sort):
     _check(out.reshape(idx.size, M, N), ref)
 
 
-@pytest.mark.parametrize("bits,gs,dtype,K", [(4, 32, "float16", 2048), (8, 64, "bfloat16", 2048),
-                                             (8, 32, "bfloat16", 2048), (4, 128, "bfloat16", 2048),
+@pytest.mark.parametrize("bits,gs,dtype,K", [(4, 32, "float16", 2560), (8, 64, "bfloat16", 2560),
+                                             (8, 32, "bfloat16", 2560), (4, 128, "bfloat16", 2560),
+                                             (4, 32, "float16", 2048), (8, 64, "bfloat16", 2048),
                                              (4, 64, "bfloat16", 512), (8, 32, "float16", 512)])
 def test_gather_prefill_scale_blocks(bits, gs, dtype, K):
-    """K / gs a multiple of 8: the grouped tiles (64/128-row wide tiles at
-    K=2048, the thin kernel at K=512) read scales and biases in 16-byte
-    blocks of 8 groups, one load per block (group 32: two groups per step,
-    the group index differs across a row's chunks; group 128: per-step
-    loads, the block would span 16 steps).  Ragged N, zipf routing, full
-    oracle."""
+    """K / gs a multiple of 8: the grouped tiles (64/128-row wide tiles past
+    K=2048, the thin kernel with 8 waves at K=2048 and 4 at K=512) read
+    scales and biases in 16-byte blocks of 8 groups, one load per block
+    (group 32: two groups per step, the group index differs across a row's
+    chunks; group 128: per-step loads, the block would span 16 steps).
+    Ragged N, zipf routing, full oracle."""
     rng = np.random.default_rng(90 + bits + gs + K)
     E, N, T, top = 32, 264, 384, 4
     banks = [quantized(rng, N, K, gs=gs, bits=bits, dtype=dtype) for _ in range(E)]
@@ -615,13 +616,14 @@ def test_gather_prefill_thin_experts(M, bits, gs, dtype):
 
 
 @pytest.mark.parametrize("T,top,M,K", [(150, 4, 1, 512), (300, 4, 1, 1024), (300, 4, 1, 2048),
-                                        (200, 4, 2, 512)])
+                                        (300, 4, 1, 2560), (200, 4, 2, 512)])
 def test_gather_sorted_prep_matches_counting_sort(T, top, M, K):
     """Pairs already in expert order (mlx-lm's _gather_sort) take the prep
     kernel's scan path (identity order); the same pairs shuffled take the
     counting sort.  Per-pair rows must be bit-identical, and match the
     oracle.  Covers the streaming kernel with prep tables (P*M < 1024), the
-    thin and the wide grouped kernels, runs longer than a segment."""
+    thin kernel with 4 and 8 waves and the wide grouped kernels, runs longer
+    than a segment."""
     rng = np.random.default_rng(T + top + M + K)
     E, N = 24, 160
     banks = [quantized(rng, N, K) for _ in range(E)]
