@@ -501,7 +501,6 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
                                int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
                                hipStream_t st, int* nlaunch) {
   const int R = (int)(kThinBM / M);
-  if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
   // 4 waves (256 columns) per workgroup at short K, 8 (512 columns, so each
   // x tile serves twice the columns) above K = 1024: config-4 banks, 2048
   // tokens x top-8, one process: down (K=512) 143 / 122 us zipf / uniform
@@ -509,17 +508,30 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
   // against 302 / 253 for the size-class wide tiles and 282 / 264 with 16
   // waves (whose 128-register budget spills)
   const int nwv = K <= 1024 ? 4 : 8;
-  const int64_t segs = class_seg_bound(P, R, 0, E);
-  const int64_t ntiles = (N + 64 * nwv - 1) / (64 * nwv) * segs;
-  if (ntiles > INT32_MAX - 8) return kStatusUnsupported;
-  const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
-#define MQ_THIN(NWV)                                                                            \
-  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV>), grid, dim3(64 * NWV), 0,   \
-                     st, (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,     \
+  const int64_t ncol = (N + 64 * nwv - 1) / (64 * nwv);
+  int64_t nwg = 0;
+  if (nwv == 8) {
+    // 8 waves: experts with more than 64 rows take 128-row tiles, which
+    // read their weights once per 128 rows (the workgroup's register
+    // budget already holds one workgroup per CU, so the taller tile costs
+    // no occupancy)
+    const int R1 = (int)(128 / M), C1 = R + 1;
+    if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st, R1, C1)) return rc;
+    for (const int64_t sb : {class_seg_bound(P, R1, C1, E), class_seg_bound(P, R, 0, E)})
+      nwg += (sb * ncol + 7) / 8 * 8;
+  } else {
+    if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
+    nwg = (class_seg_bound(P, R, 0, E) * ncol + 7) / 8 * 8;
+  }
+  if (nwg > INT32_MAX) return kStatusUnsupported;
+  const dim3 grid((unsigned)nwg);
+#define MQ_THIN(NWV, CLS2)                                                                      \
+  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV, CLS2>), grid, dim3(64 * NWV),\
+                     0, st, (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,  \
                      (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K, \
                      (int)E, 0)
-  if (nwv == 4) MQ_THIN(4);
-  else MQ_THIN(8);
+  if (nwv == 4) MQ_THIN(4, false);
+  else MQ_THIN(8, true);
 #undef MQ_THIN
   *nlaunch += kPrepLaunches + 1;
   return 0;

@@ -37,18 +37,20 @@ namespace mq {
 
 constexpr int kThinBM = 64;
 
-// 1-D grid of ceil(N / (64 NWV)) x segment bound workgroups (tiles placed by
-// grouped_tile), 64 NWV threads; segments of size class cls of the prep
-// tables in ws hold up to 64 / Mi pairs of one expert; pair p contributes
-// rows p*Mi .. p*Mi+Mi-1 and reads x batch x_batch(lhs, p, P, B).  Segments of
-// out-of-range experts write zeros.  K % 64 == 0, B * Mi * K * 2 < 2^31.
-template <int DT, int BITS, int GS, int PS, int NWV>
-__global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
+// One tile of the thin kernel: segment seg of the prep tables (up to BM / Mi
+// pairs of one expert; pair p contributes rows p*Mi .. p*Mi+Mi-1 and reads x
+// batch x_batch(lhs, p, P, B)) x weight columns [64 NWV col, +64 NWV), 64 NWV
+// threads.  Segments of out-of-range experts write zeros.  K % 64 == 0,
+// B * Mi * K * 2 < 2^31.
+template <int DT, int BITS, int GS, int PS, int NWV, int BM>
+__device__ __forceinline__ void thin_tile(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E, int cls) {
-  constexpr int BM = kThinBM, BN = 64 * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
+    int P, int B, int Mi, int N, int K, int E, int seg, int col) {
+  constexpr int BN = 64 * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
+  constexpr int MB = BM / 32;                   // 32-row blocks of the tile
+  static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
   constexpr int XT = BM * 8;                    // 16-byte x pieces per step
   constexpr int XI = XT >= NT ? XT / NT : 1;    // x pieces per thread per step
   constexpr int WB = BITS / 4;                  // 16-byte loads per lane per block per step
@@ -57,11 +59,6 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
   __shared__ __align__(16) uint16_t As[2][BM * LD];
   __shared__ uint32_t s_xoff[BM];
   __shared__ int s_orow[BM];
-  const int32_t* hdr = ws + gather_ws_header(P);
-  const int s0 = hdr[2 - cls];
-  int seg, col;
-  if (!grouped_tile(blockIdx.x, hdr[3 - cls] - s0, (N + BN - 1) / BN, seg, col)) return;
-  seg += s0;
   const int n0 = col * BN;
   const int32_t* perm = ws + 1;
   const int st0 = perm[P + seg], len = perm[2 * P + seg];
@@ -165,14 +162,14 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
     }
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[MB][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
-  const int live = rows > 32 ? 2 : 1;           // 32-row blocks holding rows
+  const int live = rows > 32 ? (rows + 31) / 32 : 1;   // 32-row blocks holding rows
 
   // One k-step: dequantize codes 8 ks .. 8 ks + 7 of the lane's 32 (B of MFMA
   // ks, per 32-column block) and multiply with the x rows in LDS buffer buf.
@@ -218,7 +215,7 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
         bq[j] = (u32x4){o[0], o[1], o[2], o[3]};
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < MB; ++i)
         if (i == 0 || i < live) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(A + 32 * i * LD + 8 * ks);
 #pragma unroll
@@ -281,7 +278,7 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
 
   // D[row][col] of a 32x32 tile: col = lane & 31, row = 8*(e/4) + 4*(lane>>5) + e%4
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int c = 64 * wave + 32 * j + lr;
@@ -291,6 +288,41 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
         if (r < rows && c < ncols) out[(int64_t)s_orow[r] * N + n0 + c] = T::round1(acc[i][j][q]);
       }
     }
+}
+
+// 1-D grid, 64 NWV threads, tiles placed by grouped_tile.  CLS2 false: the
+// tiles of the prep tables' size class cls (segments of up to 64 / Mi pairs),
+// ceil(N / (64 NWV)) x its segment bound workgroups.  CLS2 true: class 1
+// (segments of up to 128 / Mi pairs, 128-row tiles) in the first 8 q1
+// workgroups (q1 = its tiles / 8, rounded up), then class 0 (64-row tiles);
+// cls is ignored.  Each height runs its own code (a 128-row body for every
+// tile made the 64-row ones slower).
+template <int DT, int BITS, int GS, int PS, int NWV, bool CLS2>
+__global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
+    int P, int B, int Mi, int N, int K, int E, int cls) {
+  const int32_t* hdr = ws + gather_ws_header(P);
+  const int ncol = (N + 64 * NWV - 1) / (64 * NWV);
+  int bi = blockIdx.x;
+  if constexpr (CLS2) {
+    cls = 1;
+    const int q1 = ((hdr[2] - hdr[1]) * ncol + 7) / 8;
+    if (bi >= 8 * q1) {
+      bi -= 8 * q1;
+      cls = 0;
+    }
+  }
+  const int s0 = hdr[2 - cls];
+  int seg, col;
+  if (!grouped_tile(bi, hdr[3 - cls] - s0, ncol, seg, col)) return;
+  if (CLS2 && cls == 1)
+    thin_tile<DT, BITS, GS, PS, NWV, 128>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
+                                           seg + s0, col);
+  else
+    thin_tile<DT, BITS, GS, PS, NWV, 64>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
+                                          seg + s0, col);
 }
 
 }  // namespace mq
