@@ -70,7 +70,8 @@ def parse():
                         "(configs[1] skinny), combine (MoE combine, 2048 x top-8 x 2048), "
                         "gather_prefill_<proj>_<routing> (2048 tokens), "
                         "moe_layer_<routing>_T<T> (whole decode MoE layer), "
-                        "route<T> (MoE routing + shared gate)")
+                        "route<T> (MoE routing + shared gate), "
+                        "mfma_ceiling (the measured bf16 MFMA ceiling and its clock)")
     return p.parse_args()
 
 
@@ -87,6 +88,8 @@ def run_case(torch, mq, case: str) -> dict:
         return {"case": case, "us": round(r["us"], 2), "GBps": round(r["GBps"], 1)}
     if case == "combine":
         return {"case": case, **measure_combine(torch, mq, 2048, 8, 2048, 50, 3)}
+    if case == "mfma_ceiling":
+        return {"case": case, **measure_mfma_ceiling(torch)}
     if case.startswith("wide"):
         M = int(case[4:])
         r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 2048 else 100, 10, copies=2)
@@ -415,6 +418,43 @@ def measure_stream_read(torch, nbytes, steps=200, warmup=10):
                                     "(mlxturbo_amd/csrc/read_probe.hip)"}
 
 
+def measure_mfma_ceiling(torch, ms_target=10.0):
+    """The measured ceiling of the MFMA rooflines: 8-wave workgroups, four per
+    CU, each wave 4 chains of bf16 v_mfma_f32_32x32x16 on operands rewritten
+    every round (mlxturbo_amd/csrc/read_probe.hip `mq_mfma_probe`), timed
+    with HIP events after two warm-up launches; the shader clock they ran at
+    is the median over workgroups of (cycles / 100 MHz real-time ticks).
+    Under MFMA load the clock drops below its 2.4 GHz peak, and further with
+    more bit activity, so this is what the matrix cores sustain here."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "mlxturbo_amd",
+                                   "libmq_read_probe.so"))
+    lib.mq_mfma_probe.restype = ctypes.c_int
+    lib.mq_mfma_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    wgs = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(2048, dtype=torch.uint8, device="cuda")
+    clk = torch.zeros(4 * wgs, dtype=torch.int64, device="cuda")
+    st = torch.cuda.current_stream()
+    flop_per_iter = 4 * 32768.0 * 8 * wgs
+    iters = int(ms_target * 1e-3 * 2.0e15 / flop_per_iter)
+    for _ in range(2):
+        if lib.mq_mfma_probe(iters, wgs, sink.data_ptr(), clk.data_ptr(), st.cuda_stream):
+            raise RuntimeError("mq_mfma_probe failed")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    if lib.mq_mfma_probe(iters, wgs, sink.data_ptr(), clk.data_ptr(), st.cuda_stream):
+        raise RuntimeError("mq_mfma_probe failed")
+    e1.record(st)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3
+    c = clk.view(wgs, 4).cpu().numpy().astype(np.float64)
+    mhz = float(np.median((c[:, 1] - c[:, 0]) / np.maximum(c[:, 3] - c[:, 2], 1.0) * 100.0))
+    return {"TFLOPs": round(flop_per_iter * iters / sec / 1e12, 1), "clock_MHz": round(mhz),
+            "how": "bf16 32x32x16 MFMA loop on changing operands, 8 waves x 4 workgroups per CU "
+                   "(mlxturbo_amd/csrc/read_probe.hip mq_mfma_probe)"}
+
+
 def copy_probe(torch, nbytes, reps=4):
     """A plain device copy of known size, for calibrating rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters against the bytes actually moved."""
@@ -625,13 +665,17 @@ def main():
 
         # config 3: prefill widths on the MFMA tile kernel (compute-bound)
         # configs[2] (512/2048/8192) plus points across the bandwidth/compute
-        # crossover (M ~ 95 at the MFMA ridge): HBM GB/s and TFLOP/s for each
+        # crossover (M ~ 95 at the MFMA ridge): HBM GB/s and TFLOP/s for each,
+        # and the fraction of the measured MFMA ceiling
+        ceiling = measure_mfma_ceiling(torch)
+        sweep["mfma_ceiling"] = ceiling
         for M in (32, 96, 256, 512, 2048, 8192):
             r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 2048 else 100, 3, copies=2)
             tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
             sweep[f"b4_K{K}_N{N}_M{M}"] = {
                 "us": round(r["us"], 2), "TFLOPs": round(tflops, 1),
                 "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "frac_of_measured_mfma": round(tflops / ceiling["TFLOPs"], 4),
                 "GBps": round(r["GBps"], 1)}
 
         # the transposed (down-proj) shape at prefill widths: few column
