@@ -40,6 +40,12 @@
 //  * From 8 rows on, a workgroup runs two 16-row tiles (TJ = 2) over each x
 //    slice, halving the x traffic per weight byte; each tile keeps its own
 //    accumulator, so results do not depend on TJ.
+//  * With 48 or more weight rows per CU, 5-16 rows run one workgroup per CU
+//    of three 4-wave groups (two tiles each) that read x once for all three:
+//    5-8 rows copy all of x into LDS before the first step, and no step loads
+//    x; 9-16 rows (x too large for LDS) stage each step's x slice once for
+//    the groups, in two buffers per K slice with a workgroup barrier per
+//    step.  Each group's arithmetic is that of the one-group launch.
 //  * Dequantization is the exact fma_mix trick of mq_common.h, rounded to T
 //    per weight (bit-exact MLX dequantization); the packed T pairs are the
 //    B operand of v_mfma_f32_16x16x32 (32 k x 16 rows).  A and B use the same
@@ -221,6 +227,15 @@ __device__ __forceinline__ void rows_put_tiles(const Rows& src, int m, int nn,
   }
 }
 
+// Shared x slices of SHX wave groups (qmv_tile with SHX > 1): the groups
+// that run the same K slice (wave kw of each group) stage each step's x slice
+// once, into one of two buffers per slice, each group loading every SHX-th
+// piece; every step then ends its staging with a workgroup barrier.
+template <int BITS, int GS, int GPL>
+__host__ __device__ inline size_t qmv_shx_lds(int NW, int XM) {
+  return 2 * qmv_x_lds<BITS, GS, GPL>(NW, XM);
+}
+
 // TJ 16-row weight tiles times M <= 16 A rows, computed by a group of NW
 // waves: kw is the (wave-uniform) wave index in the group, gt = 64 kw + lane.
 // The TJ tiles share every x slice (x is read once per call, not per tile)
@@ -229,10 +244,15 @@ __device__ __forceinline__ void rows_put_tiles(const Rows& src, int m, int nn,
 // LDS at qmv_smem and red[0 .. NW*TJ-1].  Every wave of the workgroup calls
 // it the same number of times (it holds workgroup barriers); requires M <=
 // XM when XM > 0, and qmv_sb_fits(G, NW, TJ) when SBL.
-template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, class Rows>
+// SHX > 1 (XM > 0): the workgroup is SHX groups of NW waves over the same x
+// rows (group grp of them); the x slices live in the qmv_shx_lds(NW, XM)
+// bytes at xsh, shared by the groups, and qmv_smem then only holds the
+// group's scale copy.  Each group's arithmetic is the SHX = 1 arithmetic.
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, int SHX = 1,
+          bool XRES = false, class Rows>
 __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, const Rows& src,
                                          unsigned char* qmv_smem, f32x4 (*red)[64], int kw,
-                                         int gt) {
+                                         int gt, unsigned char* xsh = nullptr, int grp = 0) {
   using Gm = QmvGeom<BITS, GS, GPL>;
   constexpr int STEPG = Gm::STEPG, STEPB = Gm::STEPB, STEPK = Gm::STEPK, NSV = Gm::NSV;
   constexpr int NL = Gm::NL, CPL = Gm::CPL, MPL = Gm::MPL, SH = Gm::SH;
@@ -241,11 +261,15 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   constexpr int XPR = STEPK / 8;                          // pieces per x row per step
   constexpr int XPL = XM ? (XM * XPR + 63) / 64 : 1;      // pieces per lane per step
   constexpr int XSR = 2 * STEPK + 16;                     // LDS bytes per x row (padded)
+  static_assert(SHX == 1 || XM > 0, "shared x slices stream through LDS");
+  // pieces this wave loads: q-th of them is piece q * SHX + grp
+  constexpr int XPW = XRES ? 1 : (XPL + SHX - 1) / SHX;
+  static_assert(!XRES || (XM > 0 && SBL), "resident x is filled with the scale copy");
   using T = T16<DT>;
   struct Stage {
     u32x4 w[TJ][NL];
     uint32_t s[TJ][SBL ? 1 : NSV], b[TJ][SBL ? 1 : NSV];
-    u32x4 xq[XPL];
+    u32x4 xq[XPW];
   };
   const int lane = threadIdx.x & 63;
   const int wave = kw;
@@ -274,31 +298,37 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   const int fe = se < full ? se : full;      // pipelined (unchecked) steps: [sb, fe)
 
   const int xr = min(r, M - 1);              // A row of this lane (rows >= M repeat row M-1)
-  lds_u8* xreg = (lds_u8*)qmv_smem + wave * (XM ? XM : 1) * XSR;
-  const lds_u8* xl = xreg + xr * XSR;
+  // SHX > 1: buffer b (0, 1) of slice kw at xsh + (2 kw + b) XM XSR
+  lds_u8* xreg = SHX > 1 ? (lds_u8*)xsh + 2 * wave * XM * XSR
+                         : (lds_u8*)qmv_smem + wave * (XM ? XM : 1) * XSR;
+  // XRES: row m of x at xsh + m XRS, codes [0, nsteps STEPK), zero past K
+  const int XRS = 2 * nsteps * STEPK + 16;
+  const lds_u8* xl = XRES ? (const lds_u8*)xsh + xr * XRS : xreg + xr * XSR;
   const uint16_t* xg = src.x + src.xoff(xr);
   const int SBS = qmv_sb_stride(G);
   // tile j's scale rows at sbl + j * 32 SBS, its bias rows 16 SBS further
-  lds_u8* sbl = (lds_u8*)qmv_smem + NW * (XM ? XM : 1) * XSR;
+  lds_u8* sbl = (lds_u8*)qmv_smem + (SHX > 1 ? 0 : NW * (XM ? XM : 1) * XSR);
   // XM > 0: byte offset of this lane's x pieces from the step's x slice;
   // pieces of rows >= M are out of the buffer range (no memory access, zeros)
-  uint32_t xvo[XPL];
-  int xpk[XPL];
+  uint32_t xvo[XPW];
+  int xpk[XPW], xpi[XPW];
 #pragma unroll
-  for (int q = 0; q < XPL; ++q) {
-    const int i = lane + 64 * q;
+  for (int q = 0; q < XPW; ++q) {
+    const int qq = SHX > 1 ? q * SHX + grp : q;
+    const int i = lane + 64 * qq;
     const int m = i / XPR;
+    xpi[q] = qq < XPL && i < (XM ? XM : 1) * XPR ? i : -1;   // -1: no piece of this wave
     xpk[q] = 8 * (i - m * XPR);
-    xvo[q] = (m < M) ? (uint32_t)(src.xoff(m) + xpk[q]) * 2u : 0x80000000u;
+    xvo[q] = (m < M && xpi[q] >= 0) ? (uint32_t)(src.xoff(m) + xpk[q]) * 2u : 0x80000000u;
   }
 
   auto load = [&](Stage& s, int t, bool live) {
-    if constexpr (XM > 0) {
+    if constexpr (XM > 0 && !XRES) {
       const uint32_t xstep = (uint32_t)t * STEPK * 2;
       const auto rx = make_rsrc(reinterpret_cast<const char*>(src.x) + xstep,
                                 live ? src.x_nrec - xstep : 0u);
 #pragma unroll
-      for (int q = 0; q < XPL; ++q)
+      for (int q = 0; q < XPW; ++q)
         s.xq[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, xvo[q], 0, 0);
     }
 #pragma unroll
@@ -337,7 +367,10 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   // A fragment covering codes [k, k+8): k relative to the step (LDS slice) or
   // absolute (global).  Codes past K read zeros (LDS slices are zeroed there).
   auto afrag = [&](int krel, int kabs, bool checked) -> u32x4 {
-    if constexpr (XM > 0) {
+    if constexpr (XRES) {
+      (void)krel; (void)checked;
+      return *(const lds_u32x4*)(xl + 2 * kabs);
+    } else if constexpr (XM > 0) {
       (void)kabs; (void)checked;
       return *(const lds_u32x4*)(xl + 2 * krel);
     } else {
@@ -347,20 +380,29 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
     }
   };
 
-  auto compute = [&](const Stage& s, int t, bool checked) {
-    if constexpr (XM > 0) {
+  // par: buffer of the step's x slice (SHX > 1); dead: the step is past this
+  // wave's slice and only stages (zeros) and joins the barrier (SHX > 1)
+  auto compute = [&](const Stage& s, int t, bool checked, int par = 0, bool dead = false) {
+    if constexpr (XM > 0 && !XRES) {
+      lds_u8* xb = xreg + (SHX > 1 ? par * XM * XSR : 0);
 #pragma unroll
-      for (int q = 0; q < XPL; ++q) {
-        const int i = lane + 64 * q;
-        if (XPL * 64 == XM * XPR || i < XM * XPR) {
+      for (int q = 0; q < XPW; ++q) {
+        const int i = xpi[q];
+        if ((SHX == 1 && XPL * 64 == XM * XPR) || i >= 0) {
           u32x4 v = s.xq[q];
           if (checked && t * STEPK + xpk[q] >= K) v = (u32x4){0u, 0u, 0u, 0u};
-          *(lds_u32x4*)(xreg + (i / XPR) * XSR + 2 * xpk[q]) = v;
+          *(lds_u32x4*)(xb + (i / XPR) * XSR + 2 * xpk[q]) = v;
         }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if constexpr (SHX > 1) {
+        __syncthreads();
+        if (dead) return;
+        xl = xb + xr * XSR;
+      } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
     }
     float sf[TJ][NL], bf[TJ][NL];
     bool big = false;
@@ -472,9 +514,45 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
       }
     }
   }
+  // ---- resident x (XRES): the workgroup's threads copy rows [0, M) of x,
+  // the first XRU pieces of each thread loaded ahead of the weight prologue
+  constexpr int XRU = 8;
+  u32x4 xrq[XRES ? XRU : 1];
+  const int xnt = 64 * NW * SHX;               // threads of the workgroup
+  const int xtid = grp * 64 * NW + gt;
+  const int xrp = nsteps * STEPK / 8;          // pieces per resident row
+  const int xtot = M * xrp;
+  auto xres_piece = [&](int i, uint32_t& lofs) -> uint32_t {
+    const int m = i / xrp, k = 8 * (i - m * xrp);
+    lofs = (uint32_t)(m * XRS + 2 * k);
+    return (i < xtot && k < K) ? (uint32_t)(src.xoff(m) + k) * 2u : 0x80000000u;
+  };
+  if constexpr (XRES) {
+    const auto rx = make_rsrc(src.x, src.x_nrec);
+#pragma unroll
+    for (int u = 0; u < XRU; ++u) {
+      uint32_t lo;
+      xrq[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, xres_piece(xtid + u * xnt, lo), 0, 0);
+    }
+  }
   // ---- main loop: PF-stage pipeline over the unchecked steps --------------
 #pragma unroll
   for (int i = 0; i < PF - 1; ++i) load(S[i], sb + i, sb + i < fe);
+  if constexpr (XRES) {
+#pragma unroll
+    for (int u = 0; u < XRU; ++u) {
+      const int i = xtid + u * xnt;
+      uint32_t lo;
+      xres_piece(i, lo);
+      if (i < xtot) *(lds_u32x4*)((lds_u8*)xsh + lo) = xrq[u];
+    }
+    const auto rx = make_rsrc(src.x, src.x_nrec);
+    for (int i = xtid + XRU * xnt; i < xtot; i += xnt) {
+      uint32_t lo;
+      const uint32_t go = xres_piece(i, lo);
+      *(lds_u32x4*)((lds_u8*)xsh + lo) = __builtin_amdgcn_raw_buffer_load_b128(rx, go, 0, 0);
+    }
+  }
   if constexpr (SBL) {
 #pragma unroll
     for (int u = 0; u < kQmvSbChunks; ++u) {
@@ -490,24 +568,55 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
     }
     __syncthreads();
   }
-  for (int t = sb; t < fe; t += PF) {
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int tl2 = t + i + PF - 1;
-      load(S[(i + PF - 1) % PF], tl2, tl2 < fe);
-      if (t + i < fe) compute(S[i], t + i, false);
+  if constexpr (SHX > 1 && !XRES) {
+    // every wave takes as many steps as the longest slice (each step's
+    // staging ends with a workgroup barrier); steps past its own are dead
+    int nmax = 0;
+    for (int w2 = 0; w2 < NW; ++w2) {
+      const int b2 = (int)((int64_t)nsteps * w2 / NW);
+      const int e2 = min((int)((int64_t)nsteps * (w2 + 1) / NW), full);
+      nmax = max(nmax, e2 - b2);
     }
-  }
-  // ---- ragged tail: at most one step; groups past K are zeroed ------------
-  if (fe < se) {
-    Stage s;
-    load(s, fe, true);
+    for (int u = 0; u < nmax; u += PF) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j)
+      for (int i = 0; i < PF; ++i) {
+        const int tl2 = sb + u + i + PF - 1;
+        load(S[(i + PF - 1) % PF], tl2, tl2 < fe);
+        if (u + i < nmax) compute(S[i], sb + u + i, false, (u + i) & 1, sb + u + i >= fe);
+      }
+    }
+    // the last slice's ragged step (only its waves hold one), in every wave
+    if (full < nsteps) {
+      Stage s;
+      const bool mine = fe < se;
+      load(s, fe, mine);
 #pragma unroll
-      for (int L = 0; L < NL; ++L)
-        if (fe * STEPG + ((4 * L + c) >> SH) >= G) s.w[j][L] = (u32x4){0u, 0u, 0u, 0u};
-    compute(s, fe, true);
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int L = 0; L < NL; ++L)
+          if (fe * STEPG + ((4 * L + c) >> SH) >= G) s.w[j][L] = (u32x4){0u, 0u, 0u, 0u};
+      compute(s, fe, true, nmax & 1, !mine);
+    }
+  } else {
+    for (int t = sb; t < fe; t += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int tl2 = t + i + PF - 1;
+        load(S[(i + PF - 1) % PF], tl2, tl2 < fe);
+        if (t + i < fe) compute(S[i], t + i, false);
+      }
+    }
+    // ---- ragged tail: at most one step; groups past K are zeroed ----------
+    if (fe < se) {
+      Stage s;
+      load(s, fe, true);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int L = 0; L < NL; ++L)
+          if (fe * STEPG + ((4 * L + c) >> SH) >= G) s.w[j][L] = (u32x4){0u, 0u, 0u, 0u};
+      compute(s, fe, true);
+    }
   }
 
   // ---- sum the waves' partial tiles in wave order, round once -------------
@@ -600,6 +709,79 @@ __global__ __launch_bounds__(64 * NW) void qmv_kernel(const uint16_t* __restrict
       threadIdx.x);
 }
 
+// Bytes of a resident copy of M rows of x (rows padded to whole steps).
+template <int BITS, int GS, int GPL>
+__host__ __device__ inline size_t qmv_xres_lds(int M, int K) {
+  using Gm = QmvGeom<BITS, GS, GPL>;
+  const int nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
+  return (size_t)M * (2 * nsteps * Gm::STEPK + 16);
+}
+
+// The skinny kernel with NG wave groups per workgroup over the same x rows
+// (qmv_tile with SHX = NG): the groups stage each x slice once, so x is read
+// once per 16 NG TJ weight rows instead of once per 16 TJ; with XRES the
+// workgroup copies rows [0, M) of x into LDS once, before its first step,
+// and no step loads or stages x.  Workgroup i owns rows
+// [i N / grid, (i + 1) N / grid), group g the g-th NG-th of them as TJ tiles
+// of <= 16 rows; rows per workgroup <= 16 NG TJ.  Block 64 NW NG, dynamic
+// LDS qmv_shx_lds(NW, XM) (XRES: qmv_xres_lds(M, K)) + NG TJ
+// qmv_sb_lds(K / GS) (SBL).
+template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, int NG,
+          bool XRES>
+__global__ __launch_bounds__(64 * NW * NG) void qmv_shx_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    uint16_t* __restrict__ out, int M, int N, int K, int64_t ldx, int64_t ldo) {
+  extern __shared__ __align__(16) unsigned char qmv_smem[];
+  __shared__ f32x4 red[NG * NW * TJ][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = wave / NW, kw = wave - g * NW;
+  const int64_t wn0 = (int64_t)blockIdx.x * N / gridDim.x;
+  const int64_t wn1 = (int64_t)(blockIdx.x + 1) * N / gridDim.x;
+  const int n0 = (int)(wn0 + (wn1 - wn0) * g / NG);
+  const int n1 = (int)(wn0 + (wn1 - wn0) * (g + 1) / NG);
+  const uint32_t rowB = (uint32_t)K * BITS / 8;
+  const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  QmvTiles<TJ> tl;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int nj = n0 + 16 * j;
+    const int rj = min(16, n1 - nj);
+    const int64_t base = rj > 0 ? nj : 0;
+    tl.w[j] = reinterpret_cast<const char*>(w) + base * rowB;
+    tl.s[j] = reinterpret_cast<const char*>(scales) + base * sRowB;
+    tl.b[j] = reinterpret_cast<const char*>(biases) + base * sRowB;
+    tl.rows[j] = rj;
+  }
+  const DenseRows src{x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2), out, ldx, ldo, n0};
+  const size_t xb = XRES ? qmv_xres_lds<BITS, GS, GPL>(M, K) : qmv_shx_lds<BITS, GS, GPL>(NW, XM);
+  unsigned char* gsm = qmv_smem + xb + (SBL ? (size_t)g * TJ * qmv_sb_lds(K / GS) : 0);
+  qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL, TJ, NG, XRES>(
+      tl, M, K, src, gsm, red + g * NW * TJ, kw, threadIdx.x - 64 * NW * g, qmv_smem, g);
+}
+
+// Wave groups per shared-x workgroup and tiles per group (K=5120 N=17408
+// M=16, one process: 3 x 2 19.4 us, 2 x 3 20.5, 4 x 2 21.6, against 21.4
+// for one group of two tiles on three workgroups per CU).
+constexpr int kQmvShxNG = 3;
+constexpr int kQmvShxTJ = 2;
+
+// Grid of a shared-x launch: a multiple of the CU count (one workgroup per
+// CU, the rows spread evenly) holding at most 16 NG TJ rows per workgroup,
+// or 0 when the rows are too few for every group to fill a tile.
+inline unsigned qmv_shx_grid(int64_t N, int cus) {
+  const int64_t cap = 16 * kQmvShxNG * kQmvShxTJ;
+  if (cus <= 0 || N < (int64_t)cus * 16 * kQmvShxNG) return 0;
+  int64_t grid = cus;
+  while (grid * cap < N) grid += cus;
+  return (unsigned)grid;
+}
+
+// Dynamic LDS the shared-x kernel (4 waves per group) may use: all of the
+// CU's LDS but its static reduction buffer.
+constexpr size_t kQmvShxLdsMax =
+    160 * 1024 - (size_t)kQmvShxNG * 4 * kQmvShxTJ * 64 * sizeof(f32x4);
+
 // One skinny launch of M <= 16 rows.  Launches above 64 KiB of dynamic LDS
 // (16 streamed rows with 8 waves) need the kernel's limit raised once per
 // device.
@@ -622,6 +804,36 @@ inline int skinny_launch_one(const uint16_t* x, const uint32_t* w, const void* s
   return 0;
 }
 
+// One shared-x launch (4 waves per group, scale copy) streaming XM x rows.
+template <int DT, int BITS, int GS, int XM, bool XRES = false>
+inline int skinny_launch_shx_xm(const uint16_t* x, const uint32_t* w, const void* s,
+                                const void* b, uint16_t* out, int M, int64_t N, int64_t K,
+                                size_t lds, unsigned grid, hipStream_t st) {
+  using C = QmvConf<BITS, GS>;
+  auto kern = &qmv_shx_kernel<DT, BITS, GS, C::GPL, 4, C::PF, XM, true, kQmvShxTJ, kQmvShxNG, XRES>;
+  static std::atomic<uint64_t> lds_set{0};
+  if (hipError_t e =
+          ensure_lds_limit(reinterpret_cast<const void*>(kern), (int)kQmvShxLdsMax, lds_set))
+    return (int)e;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * 4 * kQmvShxNG), lds, st, x, w,
+                     (const uint16_t*)s, (const uint16_t*)b, out, M, (int)N, (int)K, (int64_t)K,
+                     (int64_t)N);
+  return 0;
+}
+
+template <int DT, int BITS, int GS>
+inline int skinny_launch_shx(int xm, const uint16_t* x, const uint32_t* w, const void* s,
+                             const void* b, uint16_t* out, int M, int64_t N, int64_t K,
+                             size_t lds, unsigned grid, hipStream_t st) {
+  using C = QmvConf<BITS, GS>;
+  if (xm == 8) return skinny_launch_shx_xm<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, lds, grid, st);
+  if constexpr (QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
+    if (xm == 16)
+      return skinny_launch_shx_xm<DT, BITS, GS, 16>(x, w, s, b, out, M, N, K, lds, grid, st);
+  }
+  return kStatusUnsupported;
+}
+
 template <int DT, int BITS, int GS, int NW>
 inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, const void* b,
                             void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
@@ -641,6 +853,29 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
     if (!sbl && xm) xm = xm > kQmvMaxXM ? 16 : kQmvMaxXM;
     const size_t lds = qmv_x_lds<BITS, GS, C::GPL>(NW, xm) + (sbl ? tj * qmv_sb_lds(G) : 0);
     int rc = kStatusUnsupported;
+    if constexpr (NW == 4) {
+      // 5-16 rows with the scale copy on matrices of >= 48 rows per CU: one
+      // workgroup of three wave groups per CU, x resident in LDS for 5-8
+      // rows, staged once per step for all groups for 9-16 (K=5120 N=17408,
+      // one process: M=8 16.7 against 17.5 us, M=16 19.4 against 21.4).
+      // Fewer rows keep more, smaller workgroups: there, this geometry lost
+      // 1-3 us (M=1 16.3 against 13.2), the x it saves being small.
+      const unsigned sg = qmv_shx_grid(N, device_cu_count());
+      const size_t lds_sh = qmv_shx_lds<BITS, GS, C::GPL>(NW, xm) +
+                            (size_t)kQmvShxNG * kQmvShxTJ * qmv_sb_lds(G);
+      const size_t lds_xr = qmv_xres_lds<BITS, GS, C::GPL>(mt, (int)K) +
+                            (size_t)kQmvShxNG * kQmvShxTJ * qmv_sb_lds(G);
+      if (xm == 8 && qmv_sb_fits(G, NW, kQmvShxTJ, s, b) && sg > 0 && lds_xr <= kQmvShxLdsMax) {
+        rc = skinny_launch_shx_xm<DT, BITS, GS, 8, true>(xp, w, s, b, op, mt, N, K, lds_xr, sg, st);
+        if (rc) return rc;
+        continue;
+      }
+      if (xm == 16 && qmv_sb_fits(G, NW, kQmvShxTJ, s, b) && sg > 0 && lds_sh <= kQmvShxLdsMax) {
+        rc = skinny_launch_shx<DT, BITS, GS>(xm, xp, w, s, b, op, mt, N, K, lds_sh, sg, st);
+        if (rc) return rc;
+        continue;
+      }
+    }
 #define MQ_SX(X, SB, J)                                                                   \
     if (xm == X && sbl == SB && tj == J)                                                  \
       rc = skinny_launch_one<DT, BITS, GS, NW, X, SB, J>(xp, w, s, b, op, mt, N, K, lds, st);

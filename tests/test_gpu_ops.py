@@ -166,9 +166,10 @@ def test_qmm_rows_bit_identical_across_widths():
 def test_qmv_balanced_rows_match_tiles(N, K):
     """Launches spread the rows evenly over the CUs when the workgroups do not
     divide over them: one-row calls (N=17408 on 256 CUs: 1280 workgroups of
-    13-14 rows; N=3500: 256 of 13-14) and two-tile calls of 8+ rows (N=17408:
-    768 workgroups of 22-23 rows; N=5120: 256 of 20).  Every row must be
-    bit-identical to the tiled launch of a two-row call."""
+    13-14 rows; N=3500: 256 of 13-14) and two-tile calls of 9 rows (N=5120:
+    256 workgroups of 20; N=17408: one workgroup of three wave groups per
+    CU).  Every row must be bit-identical to the tiled launch of a two-row
+    call."""
     rng = np.random.default_rng(11)
     w, s, b = random_packed(rng, N, K)
     x = act(rng, (9, K), scale=0.1)
@@ -182,6 +183,37 @@ def test_qmv_balanced_rows_match_tiles(N, K):
     if N * K <= 4 << 20:
         _check(one, O.quantized_matmul_ref(x[:1], w, s, b))
         _check(mq.quantized_matmul(xd, *args), O.quantized_matmul_ref(x, w, s, b))
+
+
+@pytest.mark.parametrize("bits, gs, dtype, N, K", [
+    (4, 64, "bfloat16", 12300, 1088),    # a ragged last step; uneven rows over the groups
+    (4, 32, "float16", 13000, 2048),
+    (8, 64, "bfloat16", 12288, 4096),
+    (4, 128, "bfloat16", 12500, 1536),   # 8 streamed rows (longer steps stream no 16)
+    (4, 64, "bfloat16", 17408, 5120),
+])
+def test_qmv_shared_x_groups(bits, gs, dtype, N, K):
+    """5-16 rows on matrices of >= 48 rows per CU run one workgroup per CU of
+    three wave groups that read x once for all of them (5-8 rows: all of x
+    resident in LDS; 9-16: each step's slice staged once).  Every row must be
+    bit-identical to the one- and two-row launches (the same K split) and
+    match the oracle on a column sample."""
+    rng = np.random.default_rng(N + K + bits + gs)
+    w, s, b = random_packed(rng, N, K, gs, bits, dtype)
+    x = act(rng, (16, K), dtype, scale=0.1)
+    args = (to_dev(w), to_dev(s, dtype), to_dev(b, dtype))
+    xd = to_dev(x, dtype)
+    two = bits16(mq.quantized_matmul(xd[:2], *args, group_size=gs, bits=bits))
+    cols = np.concatenate([np.arange(0, 40), np.arange(N - 40, N), rng.choice(N, 80, False)])
+    colt = torch.from_numpy(cols).cuda()
+    for M in (5, 7, 8, 11, 16):
+        out = mq.quantized_matmul(xd[:M], *args, group_size=gs, bits=bits)
+        ob = bits16(out)
+        np.testing.assert_array_equal(ob[:2], two)
+        ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], gs, bits, dtype)
+        _check(out[:, colt], ref, dtype)
+    one = bits16(mq.quantized_matmul(xd[15:16], *args, group_size=gs, bits=bits))
+    np.testing.assert_array_equal(ob[15], one[0])
 
 
 def test_qmm_writes_every_element():

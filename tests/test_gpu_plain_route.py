@@ -47,6 +47,23 @@ def test_qmm_huge_scales(M):
     _check_split(out, ref, huge_rows)
 
 
+@pytest.mark.parametrize("M", [6, 16])
+def test_qmm_huge_scales_shared_x(M):
+    """5-16 rows on a matrix of 48+ rows per CU: one workgroup per CU of three
+    wave groups (x resident in LDS for 6 rows, staged per step for 16)."""
+    rng = np.random.default_rng(40 + M)
+    N, K, gs = 12288, 1024, 64
+    w, s, b = quantized(rng, N, K, gs)
+    huge_rows = np.array([3, 6000, 12287])
+    s = _huge(s, huge_rows, 5)
+    x = act(rng, (M, K))
+    out = from_dev(mq.quantized_matmul(to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"),
+                                       to_dev(b, "bfloat16"), group_size=gs))
+    ref = O.quantized_matmul_ref(x, w, s, b, gs)
+    assert np.all(np.isfinite(out))
+    _check_split(out, ref, huge_rows)
+
+
 def test_grouped_gather_huge_scales():
     # prefill-width gather (grouped MFMA tiles) with one expert's scales huge
     rng = np.random.default_rng(5)
