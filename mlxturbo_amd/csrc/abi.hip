@@ -241,7 +241,12 @@ int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
                                      st);
   if (rc) return fail(rc, "quantized_matmul: no kernel for dtype=%d bits=%d group_size=%d", dtype,
                       bits, group_size);
-  return check_launch("quantized_matmul(skinny)");
+  // one skinny launch per 16 rows
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "quantized_matmul(skinny): launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)((M + 15) / 16), std::memory_order_relaxed);
+  return MQ_OK;
 }
 
 int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,

@@ -200,18 +200,31 @@ inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 // model fitted to measurements.  Few column tiles starve the wide grid
 // (K=17408 N=5120: 20 tiles; M=17..64 took 229-249 us wide against 40-87
 // in 16-row launches; K=4096 N=4096: 48 against 12-29), while at K=5120
-// N=17408 the wide tile wins from M ~ 56.  Skinny launch time: about 3 us
+// N=17408 the wide tile wins from M ~ 40.  Skinny launch time: about 3 us
 // plus the weight bytes at 3.6 TB/s for one row, x1.15 for 2-4 rows, x1.4
-// for 5-8, x1.65 for 9-16.  split_ok: a workspace is available for K splits.
+// for 5-8, x1.65 for 9-16; on matrices of 640+ row tiles and 48+ rows per CU
+// (the shared-x workgroups of 5-16 rows) x1.35 for 5-8 and x1.42 for 9-16
+// (K=5120 N=17408: 20.7 and 21.8 us against 15.4 for the one-row model).
+// split_ok: a workspace is available for K splits.
 inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus,
                        bool split_ok) {
   if (!wide_eligible(M, N, K, bits, gs)) return false;
-  const double wide_us = wide_plan(M, N, K, cus, split_ok ? 8 : 1).cost_us;
-  const double one = 3.0 + (double)N * (double)K * bits / 8.0 / 3.6e6;
+  // The wide tile never streams its weights faster than ~0.9 TB/s at these
+  // widths (few bytes in flight per CU: M=32 48.9 us, M=96 53.6 at K=5120
+  // N=17408, M=64 49.8 at K=17408 N=5120), which the tile-time model, fitted
+  // on full rounds, does not see.
+  const double wbytes = (double)N * (double)K * bits / 8.0;
+  double wide_us = wide_plan(M, N, K, cus, split_ok ? 8 : 1).cost_us;
+  if (wide_us < wbytes / 0.9e6) wide_us = wbytes / 0.9e6;
+  const double one = 3.0 + wbytes / 3.6e6;
+  const bool shared_x = (N + 15) / 16 >= 640 && cus > 0 && N >= 48 * (int64_t)cus;
   double skinny_us = 0.0;
   for (int64_t m0 = 0; m0 < M; m0 += 16) {
     const int64_t m = M - m0 < 16 ? M - m0 : 16;
-    skinny_us += one * (m > 8 ? 1.65 : m > 4 ? 1.4 : m > 1 ? 1.15 : 1.0);
+    skinny_us += one * (m > 8    ? (shared_x ? 1.42 : 1.65)
+                        : m > 4  ? (shared_x ? 1.35 : 1.4)
+                        : m > 1  ? 1.15
+                                 : 1.0);
   }
   return wide_us < skinny_us;
 }

@@ -297,7 +297,30 @@ def test_skinny_long_k_many_rows(M):
     np.testing.assert_array_equal(bits16(out)[M - 1], one[0])
 
 
-@pytest.mark.parametrize("M", [24, 256, 512, 1000])
+@pytest.mark.parametrize("shape, M", [((5120, 17408), 20), ((5120, 17408), 32),
+                                      ((17408, 5120), 17), ((17408, 5120), 24)])
+def test_skinny_launches_above_16_rows(cfg2_weights, shape, M):
+    """17-32 rows where the wide tile would stream its weights at ~0.9 TB/s
+    run as 16-row skinny launches: each block of rows is bit-identical to a
+    call of those rows alone, and the whole matches the oracle on samples."""
+    K, N = shape
+    w, s, b, deq, dev = cfg2_weights[shape]
+    rng = np.random.default_rng(500 + M)
+    x = act(rng, (M, K))
+    xd = to_dev(x, "bfloat16")
+    n0 = mq.launch_count()
+    out = mq.quantized_matmul(xd, *dev)
+    assert mq.launch_count() - n0 == (M + 15) // 16
+    ob = bits16(out)
+    for m0 in range(0, M, 16):
+        part = bits16(mq.quantized_matmul(xd[m0:m0 + 16], *dev))
+        np.testing.assert_array_equal(ob[m0:m0 + 16], part)
+    cols = np.sort(rng.choice(N, size=512, replace=False))
+    ref = (O.bf16_to_f32(x).astype(np.float64) @ deq[cols].T).astype(np.float32)
+    _check(out[:, torch.from_numpy(cols).cuda()], ref)
+
+
+@pytest.mark.parametrize("M", [40, 256, 512, 1000])
 def test_wide_split_k_narrow_matrix(cfg2_weights, M):
     """The down-proj shape (K=17408, N=5120) at prefill widths: 20 column
     tiles, so the wide kernel splits K over workgroups into the workspace
