@@ -847,6 +847,10 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
     int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? qmv_skinny_xm_for<BITS, GS, C::GPL>(mt)
                                                         : 0;
     int tj = qmv_tj_for(xm);
+    // 3-4 rows on tall matrices (256+ rows per CU, so still many workgroups
+    // per CU): two tiles per x slice (8-bit lm_head N=248320 M=4 258.8 ->
+    // 247.3 us; 1-2 rows 0-2% slower that way)
+    if (xm == 4 && N >= (int64_t)device_cu_count() * 256) tj = 2;
     if (tj == 2 && !qmv_sb_fits(G, NW, 2, s, b)) tj = 1;
     const bool sbl = qmv_sb_fits(G, NW, tj, s, b);
     // without the scale copy: one tile per workgroup, 8 or 16 streamed rows
@@ -879,7 +883,7 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
 #define MQ_SX(X, SB, J)                                                                   \
     if (xm == X && sbl == SB && tj == J)                                                  \
       rc = skinny_launch_one<DT, BITS, GS, NW, X, SB, J>(xp, w, s, b, op, mt, N, K, lds, st);
-    MQ_SX(0, true, 1) MQ_SX(1, true, 1) MQ_SX(2, true, 1) MQ_SX(4, true, 1)
+    MQ_SX(0, true, 1) MQ_SX(1, true, 1) MQ_SX(2, true, 1) MQ_SX(4, true, 1) MQ_SX(4, true, 2)
     MQ_SX(8, true, 1) MQ_SX(8, true, 2) MQ_SX(0, false, 1) MQ_SX(8, false, 1)
     if constexpr (QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
       MQ_SX(16, true, 1) MQ_SX(16, true, 2) MQ_SX(16, false, 1)

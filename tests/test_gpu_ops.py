@@ -216,6 +216,28 @@ def test_qmv_shared_x_groups(bits, gs, dtype, N, K):
     np.testing.assert_array_equal(ob[15], one[0])
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmv_two_tiles_tall_matrix(bits):
+    """3-4 rows on matrices of 256+ rows per CU run two tiles per x slice;
+    each row stays bit-identical to the one- and two-row launches."""
+    rng = np.random.default_rng(77 + bits)
+    N, K = 65600, 1024
+    w, s, b = random_packed(rng, N, K, 64, bits)
+    x = act(rng, (4, K), scale=0.1)
+    args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    xd = to_dev(x, "bfloat16")
+    two = bits16(mq.quantized_matmul(xd[:2], *args, bits=bits))
+    one = bits16(mq.quantized_matmul(xd[3:4], *args, bits=bits))
+    cols = np.concatenate([np.arange(0, 40), np.arange(N - 40, N), rng.choice(N, 80, False)])
+    for M in (3, 4):
+        out = mq.quantized_matmul(xd[:M], *args, bits=bits)
+        ob = bits16(out)
+        np.testing.assert_array_equal(ob[:2], two)
+        ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], 64, bits)
+        _check(out[:, torch.from_numpy(cols).cuda()], ref)
+    np.testing.assert_array_equal(ob[3], one[0])
+
+
 def test_qmm_writes_every_element():
     """Output poisoned with NaN before the call; no element may stay NaN."""
     rng = np.random.default_rng(8)
