@@ -63,34 +63,16 @@ __device__ __forceinline__ void thin_tile(
   const int32_t* perm = ws + 1;
   const int st0 = perm[P + seg], len = perm[2 * P + seg];
   const int e = __builtin_amdgcn_readfirstlane(perm[3 * P + seg]);
+  const bool valid = e < E;                     // uniform
   const int rows = len * Mi;                    // <= BM
   const int t = threadIdx.x;
-  if (t < BM) {
-    if (t < rows) {
-      const int p = perm[st0 + t / Mi], mi = t % Mi;
-      const int xb = x_batch(lhs, p, P, B);
-      s_xoff[t] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
-      s_orow[t] = p * Mi + mi;
-    } else {
-      s_xoff[t] = 0xffffffffu;
-      s_orow[t] = -1;
-    }
-  }
-  __syncthreads();
   const int ncols = min(BN, N - n0);
-  if (e >= E) {
-    for (int i = t; i < rows * ncols; i += NT) {
-      const int r = i / ncols, c = i - r * ncols;
-      out[(int64_t)s_orow[r] * N + n0 + c] = 0;
-    }
-    return;
-  }
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int h = lane >> 5, lr = lane & 31;
   const int G = K / GS, nk = K / BK;
   const int64_t Kw = (int64_t)K * BITS / 32;    // words per weight row
-  const int64_t wrow = (int64_t)e * N + n0;
+  const int64_t wrow = (int64_t)(valid ? e : 0) * N + n0;
   // columns past ncols are past these ranges and read zeros (never stored)
   const auto rw = wide_rsrc(w + wrow * Kw, (int64_t)ncols * Kw * 4);
   const auto rs = wide_rsrc(scales + wrow * G, (int64_t)ncols * G * 2);
@@ -104,16 +86,9 @@ __device__ __forceinline__ void thin_tile(
     so[j] = (uint32_t)c * (uint32_t)G * 2u;
   }
   // x: thread t stages rows (t >> 3) + (NT / 8) i, codes 8 (t & 7) .. +8 of
-  // the step
+  // the step (offsets known once the segment's rows are in LDS)
   uint32_t xo[XI];
   int xl[XI];
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int r = min((t >> 3) + (NT / 8) * i, BM - 1);   // threads past XT: no piece
-    const uint32_t ro = (XT >= NT || t < XT) ? s_xoff[r] : 0xffffffffu;
-    xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
-    xl[i] = r * LD + 8 * (t & 7);
-  }
   struct Stage {
     u32x4 xa[XI];
     u32x4 wv[2][WB];
@@ -137,12 +112,14 @@ __device__ __forceinline__ void thin_tile(
       nb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, so[j] + bo, 0, 0);
     }
   };
-  // per_step: also load this step's scale and bias (no block path)
-  auto gload = [&](Stage& st, int kt, bool per_step) {
-    const int k0 = kt * BK;
+  auto xload = [&](Stage& st, int kt) {
 #pragma unroll
     for (int i = 0; i < XI; ++i)
-      st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], k0 * 2, 0);
+      st.xa[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], kt * BK * 2, 0);
+  };
+  // per_step: also load this step's scale and bias (no block path)
+  auto wload = [&](Stage& st, int kt, bool per_step) {
+    const int k0 = kt * BK;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -155,12 +132,66 @@ __device__ __forceinline__ void thin_tile(
       }
     }
   };
+  auto gload = [&](Stage& st, int kt, bool per_step) {
+    xload(st, kt);
+    wload(st, kt, per_step);
+  };
   auto store_x = [&](const Stage& st, int buf) {
     if (XT >= NT || t < XT) {
 #pragma unroll
       for (int i = 0; i < XI; ++i) *reinterpret_cast<u32x4*>(&As[buf][xl[i]]) = st.xa[i];
     }
   };
+
+  // The weights of the first PS steps depend on the expert only.  With 8
+  // waves they are issued before the segment's x rows are looked up (two
+  // more dependent reads), which they would otherwise wait behind: gate/up
+  // zipf 261.7 -> 254.5 us, uniform 223.3 -> 219.4 (one process).  With 4
+  // waves the longer live range costs a wave per SIMD (3 -> 2) and the down
+  // bank lost 146 -> 173, so those issue them with the x prologue.
+  constexpr bool WFIRST = NWV >= 8;
+  Stage S[PS];
+  auto wprologue = [&]() {
+    if (sblk) {
+      if constexpr (SBLK) {
+#pragma unroll
+        for (int i = 0; i < PS; ++i) wload(S[i], i, false);    // nk >= SPB >= PS
+        bload(0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PS; ++i) wload(S[i], min(i, nk - 1), true);
+    }
+  };
+  if constexpr (WFIRST) {
+    if (valid) wprologue();
+  }
+  if (t < BM) {
+    if (t < rows) {
+      const int p = perm[st0 + t / Mi], mi = t % Mi;
+      const int xb = x_batch(lhs, p, P, B);
+      s_xoff[t] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
+      s_orow[t] = p * Mi + mi;
+    } else {
+      s_xoff[t] = 0xffffffffu;
+      s_orow[t] = -1;
+    }
+  }
+  __syncthreads();
+  if (!valid) {
+    for (int i = t; i < rows * ncols; i += NT) {
+      const int r = i / ncols, c = i - r * ncols;
+      out[(int64_t)s_orow[r] * N + n0 + c] = 0;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int r = min((t >> 3) + (NT / 8) * i, BM - 1);   // threads past XT: no piece
+    const uint32_t ro = (XT >= NT || t < XT) ? s_xoff[r] : 0xffffffffu;
+    xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
+    xl[i] = r * LD + 8 * (t & 7);
+  }
 
   f32x16 acc[MB][2];
 #pragma unroll
@@ -224,13 +255,15 @@ __device__ __forceinline__ void thin_tile(
     }
   };
 
-  Stage S[PS];
   if (sblk) {
     if constexpr (SBLK) {
-      // nk >= SPB >= PS
+      if constexpr (!WFIRST) {
 #pragma unroll
-      for (int i = 0; i < PS; ++i) gload(S[i], i, false);
-      bload(0);
+        for (int i = 0; i < PS; ++i) wload(S[i], i, false);
+        bload(0);
+      }
+#pragma unroll
+      for (int i = 0; i < PS; ++i) xload(S[i], i);
       store_x(S[0], 0);
       __syncthreads();
       // step u of a block: as the loop below, and the block of step kt + SPB
@@ -254,8 +287,12 @@ __device__ __forceinline__ void thin_tile(
       }
     }
   } else {
+    if constexpr (!WFIRST) {
 #pragma unroll
-    for (int i = 0; i < PS; ++i) gload(S[i], min(i, nk - 1), true);
+      for (int i = 0; i < PS; ++i) wload(S[i], min(i, nk - 1), true);
+    }
+#pragma unroll
+    for (int i = 0; i < PS; ++i) xload(S[i], min(i, nk - 1));
     store_x(S[0], 0);
     __syncthreads();
     // At step k: LDS buffer k & 1 holds x of step k; S[k % PS] holds step k's
