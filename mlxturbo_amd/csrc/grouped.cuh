@@ -143,55 +143,43 @@ __device__ __forceinline__ void thin_tile(
     }
   };
 
-  // The weights of the first PS steps depend on the expert only.  With 8
-  // waves they are issued before the segment's x rows are looked up (two
-  // more dependent reads), which they would otherwise wait behind: gate/up
-  // zipf 261.7 -> 254.5 us, uniform 223.3 -> 219.4 (one process).  With 4
-  // waves the longer live range costs a wave per SIMD (3 -> 2) and the down
-  // bank lost 146 -> 173, so those issue them with the x prologue.
-  constexpr bool WFIRST = NWV >= 8;
+  // The weights of the first PS steps depend on the expert only: they are
+  // issued before the segment's x rows are looked up (xsetup: two more
+  // dependent reads and a barrier), inside each prologue branch so that no
+  // stage is live across a join (4 waves keep three waves per SIMD).
+  // Gate/up zipf 261.7 -> 253.3 us, uniform 229.0 -> 219.7; down 148 -> 145
+  // (one process).
   Stage S[PS];
-  auto wprologue = [&]() {
-    if (sblk) {
-      if constexpr (SBLK) {
-#pragma unroll
-        for (int i = 0; i < PS; ++i) wload(S[i], i, false);    // nk >= SPB >= PS
-        bload(0);
+  // the segment's x rows into LDS; false (zeros written) for an invalid expert
+  auto xsetup = [&]() -> bool {
+    if (t < BM) {
+      if (t < rows) {
+        const int p = perm[st0 + t / Mi], mi = t % Mi;
+        const int xb = x_batch(lhs, p, P, B);
+        s_xoff[t] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
+        s_orow[t] = p * Mi + mi;
+      } else {
+        s_xoff[t] = 0xffffffffu;
+        s_orow[t] = -1;
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < PS; ++i) wload(S[i], min(i, nk - 1), true);
     }
+    __syncthreads();
+    if (!valid) {
+      for (int i = t; i < rows * ncols; i += NT) {
+        const int r = i / ncols, c = i - r * ncols;
+        out[(int64_t)s_orow[r] * N + n0 + c] = 0;
+      }
+      return false;
+    }
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+      const int r = min((t >> 3) + (NT / 8) * i, BM - 1);   // threads past XT: no piece
+      const uint32_t ro = (XT >= NT || t < XT) ? s_xoff[r] : 0xffffffffu;
+      xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
+      xl[i] = r * LD + 8 * (t & 7);
+    }
+    return true;
   };
-  if constexpr (WFIRST) {
-    if (valid) wprologue();
-  }
-  if (t < BM) {
-    if (t < rows) {
-      const int p = perm[st0 + t / Mi], mi = t % Mi;
-      const int xb = x_batch(lhs, p, P, B);
-      s_xoff[t] = (uint32_t)(((int64_t)xb * Mi + mi) * K * 2);
-      s_orow[t] = p * Mi + mi;
-    } else {
-      s_xoff[t] = 0xffffffffu;
-      s_orow[t] = -1;
-    }
-  }
-  __syncthreads();
-  if (!valid) {
-    for (int i = t; i < rows * ncols; i += NT) {
-      const int r = i / ncols, c = i - r * ncols;
-      out[(int64_t)s_orow[r] * N + n0 + c] = 0;
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int r = min((t >> 3) + (NT / 8) * i, BM - 1);   // threads past XT: no piece
-    const uint32_t ro = (XT >= NT || t < XT) ? s_xoff[r] : 0xffffffffu;
-    xo[i] = ro == 0xffffffffu ? 0xffffffffu : ro + 16u * (t & 7);
-    xl[i] = r * LD + 8 * (t & 7);
-  }
 
   f32x16 acc[MB][2];
 #pragma unroll
@@ -257,11 +245,12 @@ __device__ __forceinline__ void thin_tile(
 
   if (sblk) {
     if constexpr (SBLK) {
-      if constexpr (!WFIRST) {
+      if (valid) {
 #pragma unroll
         for (int i = 0; i < PS; ++i) wload(S[i], i, false);
         bload(0);
       }
+      if (!xsetup()) return;
 #pragma unroll
       for (int i = 0; i < PS; ++i) xload(S[i], i);
       store_x(S[0], 0);
@@ -287,10 +276,11 @@ __device__ __forceinline__ void thin_tile(
       }
     }
   } else {
-    if constexpr (!WFIRST) {
+    if (valid) {
 #pragma unroll
       for (int i = 0; i < PS; ++i) wload(S[i], min(i, nk - 1), true);
     }
+    if (!xsetup()) return;
 #pragma unroll
     for (int i = 0; i < PS; ++i) xload(S[i], min(i, nk - 1));
     store_x(S[0], 0);
