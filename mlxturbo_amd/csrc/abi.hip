@@ -237,15 +237,15 @@ int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
     g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
     return MQ_OK;
   }
+  int nl = 0;
   rc = dispatch_16<mq::SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
-                                     st);
+                                     st, &nl);
   if (rc) return fail(rc, "quantized_matmul: no kernel for dtype=%d bits=%d group_size=%d", dtype,
                       bits, group_size);
-  // one skinny launch per 16 rows
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail((int)e, "quantized_matmul(skinny): launch failed: %s", hipGetErrorString(e));
-  g_launches.fetch_add((uint64_t)((M + 15) / 16), std::memory_order_relaxed);
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
   return MQ_OK;
 }
 

@@ -17,11 +17,12 @@ struct DequantLaunch {
                  hipStream_t st);
 };
 
-// quantized_matmul for M rows, in launches of up to 16 rows (qmv.cuh).
+// quantized_matmul for M rows, in launches of up to 16 rows, or 32 on the
+// shared-x workgroups (qmv.cuh); *nlaunch counts the kernels enqueued.
 template <int DT, int BITS, int GS>
 struct SkinnyLaunch {
   static int run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
-                 int64_t M, int64_t N, int64_t K, hipStream_t st);
+                 int64_t M, int64_t N, int64_t K, hipStream_t st, int* nlaunch);
 };
 
 // quantized_matmul for M > 16 rows on the MFMA tile kernel (qmm_wide.cuh);
@@ -200,11 +201,13 @@ inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 // model fitted to measurements.  Few column tiles starve the wide grid
 // (K=17408 N=5120: 20 tiles; M=17..64 took 229-249 us wide against 40-87
 // in 16-row launches; K=4096 N=4096: 48 against 12-29), while at K=5120
-// N=17408 the wide tile wins from M ~ 40.  Skinny launch time: about 3 us
+// N=17408 the wide tile wins from M ~ 70.  Skinny launch time: about 3 us
 // plus the weight bytes at 3.6 TB/s for one row, x1.15 for 2-4 rows, x1.4
 // for 5-8, x1.65 for 9-16; on matrices of 640+ row tiles and 48+ rows per CU
 // (the shared-x workgroups of 5-16 rows) x1.35 for 5-8 and x1.42 for 9-16
-// (K=5120 N=17408: 20.7 and 21.8 us against 15.4 for the one-row model).
+// (K=5120 N=17408: 20.7 and 21.8 us against 15.4 for the one-row model), and
+// 17-32 rows there in one launch at x1.5 (two 16-row A tiles per weight
+// fragment: M=17/24/32 22.0/21.6/21.1 us, one process).
 // split_ok: a workspace is available for K splits.
 inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus,
                        bool split_ok) {
@@ -219,9 +222,11 @@ inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cu
   const double one = 3.0 + wbytes / 3.6e6;
   const bool shared_x = (N + 15) / 16 >= 640 && cus > 0 && N >= 48 * (int64_t)cus;
   double skinny_us = 0.0;
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
-    const int64_t m = M - m0 < 16 ? M - m0 : 16;
-    skinny_us += one * (m > 8    ? (shared_x ? 1.42 : 1.65)
+  for (int64_t m0 = 0, step = 16; m0 < M; m0 += step) {
+    step = shared_x && M - m0 > 16 ? 32 : 16;
+    const int64_t m = M - m0 < step ? M - m0 : step;
+    skinny_us += one * (m > 16   ? 1.5
+                        : m > 8  ? (shared_x ? 1.42 : 1.65)
                         : m > 4  ? (shared_x ? 1.35 : 1.4)
                         : m > 1  ? 1.15
                                  : 1.0);

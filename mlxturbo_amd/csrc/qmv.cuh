@@ -249,7 +249,7 @@ __host__ __device__ inline size_t qmv_shx_lds(int NW, int XM) {
 // bytes at xsh, shared by the groups, and qmv_smem then only holds the
 // group's scale copy.  Each group's arithmetic is the SHX = 1 arithmetic.
 template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, int SHX = 1,
-          bool XRES = false, class Rows>
+          bool XRES = false, int MT = 1, class Rows>
 __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, const Rows& src,
                                          unsigned char* qmv_smem, f32x4 (*red)[64], int kw,
                                          int gt, unsigned char* xsh = nullptr, int grp = 0) {
@@ -265,6 +265,8 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   // pieces this wave loads: q-th of them is piece q * SHX + grp
   constexpr int XPW = XRES ? 1 : (XPL + SHX - 1) / SHX;
   static_assert(!XRES || (XM > 0 && SBL), "resident x is filled with the scale copy");
+  static_assert(MT == 1 || (SHX > 1 && !XRES && XM == 16 * MT && NW > 1),
+                "16-row A tiles beyond the first share staged x slices");
   using T = T16<DT>;
   struct Stage {
     u32x4 w[TJ][NL];
@@ -298,12 +300,19 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   const int fe = se < full ? se : full;      // pipelined (unchecked) steps: [sb, fe)
 
   const int xr = min(r, M - 1);              // A row of this lane (rows >= M repeat row M-1)
-  // SHX > 1: buffer b (0, 1) of slice kw at xsh + (2 kw + b) XM XSR
-  lds_u8* xreg = SHX > 1 ? (lds_u8*)xsh + 2 * wave * XM * XSR
+  int xrm[MT];                               // same, in each 16-row A tile
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrm[mt] = min(16 * mt + r, M - 1);
+  // SHX > 1: buffer b (0, 1) of slice kw at xsh + (2 kw + b) XM XSR; with
+  // MT > 1 one buffer per slice, at xsh + kw XM XSR
+  lds_u8* xreg = SHX > 1 ? (lds_u8*)xsh + (MT > 1 ? 1 : 2) * wave * XM * XSR
                          : (lds_u8*)qmv_smem + wave * (XM ? XM : 1) * XSR;
   // XRES: row m of x at xsh + m XRS, codes [0, nsteps STEPK), zero past K
   const int XRS = 2 * nsteps * STEPK + 16;
   const lds_u8* xl = XRES ? (const lds_u8*)xsh + xr * XRS : xreg + xr * XSR;
+  const lds_u8* xlm[MT];                     // A rows of the 16-row tiles (MT > 1)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xlm[mt] = xreg + xrm[mt] * XSR;
   const uint16_t* xg = src.x + src.xoff(xr);
   const int SBS = qmv_sb_stride(G);
   // tile j's scale rows at sbl + j * 32 SBS, its bias rows 16 SBS further
@@ -360,14 +369,19 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
     }
   };
 
-  f32x4 acc[TJ];
+  f32x4 acc[TJ][MT];
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[j][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // A fragment covering codes [k, k+8): k relative to the step (LDS slice) or
   // absolute (global).  Codes past K read zeros (LDS slices are zeroed there).
-  auto afrag = [&](int krel, int kabs, bool checked) -> u32x4 {
-    if constexpr (XRES) {
+  auto afrag = [&](int krel, int kabs, bool checked, int mt = 0) -> u32x4 {
+    if constexpr (MT > 1) {
+      (void)kabs; (void)checked;
+      return *(const lds_u32x4*)(xlm[mt] + 2 * krel);
+    } else if constexpr (XRES) {
       (void)krel; (void)checked;
       return *(const lds_u32x4*)(xl + 2 * kabs);
     } else if constexpr (XM > 0) {
@@ -381,10 +395,13 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   };
 
   // par: buffer of the step's x slice (SHX > 1); dead: the step is past this
-  // wave's slice and only stages (zeros) and joins the barrier (SHX > 1)
+  // wave's slice and only stages (zeros) and joins the barrier (SHX > 1).
+  // MT > 1: one buffer per K slice, so the staging first waits for every
+  // wave to have read the previous step's slice.
   auto compute = [&](const Stage& s, int t, bool checked, int par = 0, bool dead = false) {
     if constexpr (XM > 0 && !XRES) {
-      lds_u8* xb = xreg + (SHX > 1 ? par * XM * XSR : 0);
+      lds_u8* xb = xreg + (SHX > 1 && MT == 1 ? par * XM * XSR : 0);
+      if constexpr (MT > 1) __syncthreads();
 #pragma unroll
       for (int q = 0; q < XPW; ++q) {
         const int i = xpi[q];
@@ -398,6 +415,8 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
         __syncthreads();
         if (dead) return;
         xl = xb + xr * XSR;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) xlm[mt] = xb + xrm[mt] * XSR;
       } else {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -448,7 +467,9 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
 #pragma unroll
         for (int p = 0; p < MPL; ++p) {
           const int ko = 4 * L * CPL + 8 * p;
-          const u32x4 a = afrag(kr + ko, kt + ko, checked);
+          u32x4 a[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) a[mt] = afrag(kr + ko, kt + ko, checked, mt);
 #pragma unroll
           for (int j = 0; j < TJ; ++j) {
             uint32_t bo[4];
@@ -458,7 +479,9 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
               deq8_word<DT>(s.w[j][L][2 * p], g[j], bo);
               deq8_word<DT>(s.w[j][L][2 * p + 1], g[j], bo + 2);
             }
-            acc[j] = T::mfma(a, (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc[j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[j][mt] = T::mfma(a[mt], (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc[j][mt]);
           }
         }
       }
@@ -471,7 +494,9 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
 #pragma unroll
         for (int p = 0; p < MPL; ++p) {
           const int ko = 4 * L * CPL + 8 * p;
-          const u32x4 a = afrag(kr + ko, kt + ko, checked);
+          u32x4 a[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) a[mt] = afrag(kr + ko, kt + ko, checked, mt);
 #pragma unroll
           for (int j = 0; j < TJ; ++j) {
             uint32_t bo[4];
@@ -481,7 +506,9 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
               deq_word_plain<DT, 8>(s.w[j][L][2 * p], g[j], bo);
               deq_word_plain<DT, 8>(s.w[j][L][2 * p + 1], g[j], bo + 2);
             }
-            acc[j] = T::mfma(a, (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc[j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[j][mt] = T::mfma(a[mt], (u32x4){bo[0], bo[1], bo[2], bo[3]}, acc[j][mt]);
           }
         }
       }
@@ -627,24 +654,27 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
       const int m = 4 * c + v;
       float val[TJ];
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) val[j] = acc[j][v];
+      for (int j = 0; j < TJ; ++j) val[j] = acc[j][0][v];
       if (m < M) rows_put_tiles<T, TJ>(src, m, r, val, tl.rows);
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) red[wave * TJ + j][lane] = acc[j];
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[(wave * TJ + j) * MT + mt][lane] = acc[j][mt];
     __syncthreads();
-    for (int tt = gt; tt < 256; tt += 64 * NW) {
+    for (int tu = gt; tu < 256 * MT; tu += 64 * NW) {
+      const int mt = tu >> 8, tt = tu & 255;
       const int mm = tt >> 4, nn = tt & 15;
       const int sl = ((mm >> 2) << 4) | nn, v = mm & 3;
       float sum[TJ];
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
-        sum[j] = red[j][sl][v];
+        sum[j] = red[j * MT + mt][sl][v];
 #pragma unroll
-        for (int q = 1; q < NW; ++q) sum[j] += red[q * TJ + j][sl][v];
+        for (int q = 1; q < NW; ++q) sum[j] += red[(q * TJ + j) * MT + mt][sl][v];
       }
-      if (mm < M) rows_put_tiles<T, TJ>(src, mm, nn, sum, tl.rows);
+      if (16 * mt + mm < M) rows_put_tiles<T, TJ>(src, 16 * mt + mm, nn, sum, tl.rows);
     }
     // the next tile of this workgroup reuses red and the LDS copies
     __syncthreads();
@@ -727,13 +757,13 @@ __host__ __device__ inline size_t qmv_xres_lds(int M, int K) {
 // LDS qmv_shx_lds(NW, XM) (XRES: qmv_xres_lds(M, K)) + NG TJ
 // qmv_sb_lds(K / GS) (SBL).
 template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, int NG,
-          bool XRES>
+          bool XRES, int MT = 1>
 __global__ __launch_bounds__(64 * NW * NG) void qmv_shx_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     uint16_t* __restrict__ out, int M, int N, int K, int64_t ldx, int64_t ldo) {
   extern __shared__ __align__(16) unsigned char qmv_smem[];
-  __shared__ f32x4 red[NG * NW * TJ][64];
+  __shared__ f32x4 red[NG * NW * TJ * MT][64];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = wave / NW, kw = wave - g * NW;
   const int64_t wn0 = (int64_t)blockIdx.x * N / gridDim.x;
@@ -754,10 +784,12 @@ __global__ __launch_bounds__(64 * NW * NG) void qmv_shx_kernel(
     tl.rows[j] = rj;
   }
   const DenseRows src{x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2), out, ldx, ldo, n0};
-  const size_t xb = XRES ? qmv_xres_lds<BITS, GS, GPL>(M, K) : qmv_shx_lds<BITS, GS, GPL>(NW, XM);
+  const size_t xb = XRES ? qmv_xres_lds<BITS, GS, GPL>(M, K)
+                    : MT > 1 ? qmv_x_lds<BITS, GS, GPL>(NW, XM)
+                             : qmv_shx_lds<BITS, GS, GPL>(NW, XM);
   unsigned char* gsm = qmv_smem + xb + (SBL ? (size_t)g * TJ * qmv_sb_lds(K / GS) : 0);
-  qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL, TJ, NG, XRES>(
-      tl, M, K, src, gsm, red + g * NW * TJ, kw, threadIdx.x - 64 * NW * g, qmv_smem, g);
+  qmv_tile<DT, BITS, GS, GPL, NW, PF, XM, SBL, TJ, NG, XRES, MT>(
+      tl, M, K, src, gsm, red + g * NW * TJ * MT, kw, threadIdx.x - 64 * NW * g, qmv_smem, g);
 }
 
 // Wave groups per shared-x workgroup and tiles per group (K=5120 N=17408
@@ -777,10 +809,12 @@ inline unsigned qmv_shx_grid(int64_t N, int cus) {
   return (unsigned)grid;
 }
 
-// Dynamic LDS the shared-x kernel (4 waves per group) may use: all of the
-// CU's LDS but its static reduction buffer.
-constexpr size_t kQmvShxLdsMax =
-    160 * 1024 - (size_t)kQmvShxNG * 4 * kQmvShxTJ * 64 * sizeof(f32x4);
+// Dynamic LDS the shared-x kernel (4 waves per group, MT 16-row A tiles) may
+// use: all of the CU's LDS but its static reduction buffer.
+constexpr size_t qmv_shx_lds_max(int MT) {
+  return 160 * 1024 - (size_t)kQmvShxNG * 4 * kQmvShxTJ * MT * 64 * sizeof(f32x4);
+}
+constexpr size_t kQmvShxLdsMax = qmv_shx_lds_max(1);
 
 // One skinny launch of M <= 16 rows.  Launches above 64 KiB of dynamic LDS
 // (16 streamed rows with 8 waves) need the kernel's limit raised once per
@@ -805,15 +839,16 @@ inline int skinny_launch_one(const uint16_t* x, const uint32_t* w, const void* s
 }
 
 // One shared-x launch (4 waves per group, scale copy) streaming XM x rows.
-template <int DT, int BITS, int GS, int XM, bool XRES = false>
+template <int DT, int BITS, int GS, int XM, bool XRES = false, int MT = 1>
 inline int skinny_launch_shx_xm(const uint16_t* x, const uint32_t* w, const void* s,
                                 const void* b, uint16_t* out, int M, int64_t N, int64_t K,
                                 size_t lds, unsigned grid, hipStream_t st) {
   using C = QmvConf<BITS, GS>;
-  auto kern = &qmv_shx_kernel<DT, BITS, GS, C::GPL, 4, C::PF, XM, true, kQmvShxTJ, kQmvShxNG, XRES>;
+  auto kern =
+      &qmv_shx_kernel<DT, BITS, GS, C::GPL, 4, C::PF, XM, true, kQmvShxTJ, kQmvShxNG, XRES, MT>;
   static std::atomic<uint64_t> lds_set{0};
-  if (hipError_t e =
-          ensure_lds_limit(reinterpret_cast<const void*>(kern), (int)kQmvShxLdsMax, lds_set))
+  if (hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(kern),
+                                      (int)qmv_shx_lds_max(MT), lds_set))
     return (int)e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * 4 * kQmvShxNG), lds, st, x, w,
                      (const uint16_t*)s, (const uint16_t*)b, out, M, (int)N, (int)K, (int64_t)K,
@@ -836,13 +871,33 @@ inline int skinny_launch_shx(int xm, const uint16_t* x, const uint32_t* w, const
 
 template <int DT, int BITS, int GS, int NW>
 inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, const void* b,
-                            void* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+                            void* out, int64_t M, int64_t N, int64_t K, hipStream_t st,
+                            int* nlaunch) {
   using C = QmvConf<BITS, GS>;
   const int G = (int)(K / GS);
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+  for (int64_t m0 = 0, step = 16; m0 < M; m0 += step, ++*nlaunch) {
+    step = 16;
     const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
     const uint16_t* xp = (const uint16_t*)x + m0 * K;
     uint16_t* op = (uint16_t*)out + m0 * N;
+    if constexpr (NW == 4 && QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
+      // 17-32 rows: one shared-x launch whose groups multiply every weight
+      // fragment with two 16-row A tiles (x staged once per step, in one
+      // buffer per K slice)
+      const int m2 = (int)((M - m0) < 32 ? (M - m0) : 32);
+      if (m2 > 16 && (int64_t)m2 * K * 2 < ((int64_t)1 << 31)) {
+        const unsigned sg = qmv_shx_grid(N, device_cu_count());
+        const size_t lds2 = qmv_x_lds<BITS, GS, C::GPL>(NW, 32) +
+                            (size_t)kQmvShxNG * kQmvShxTJ * qmv_sb_lds(G);
+        if (sg > 0 && qmv_sb_fits(G, NW, kQmvShxTJ, s, b) && lds2 <= qmv_shx_lds_max(2)) {
+          if (int rc = skinny_launch_shx_xm<DT, BITS, GS, 32, false, 2>(xp, w, s, b, op, m2, N, K,
+                                                                       lds2, sg, st))
+            return rc;
+          step = m2;
+          continue;
+        }
+      }
+    }
     // x streams through LDS when a buffer range covers its bytes
     int xm = ((int64_t)mt * K * 2 < ((int64_t)1 << 31)) ? qmv_skinny_xm_for<BITS, GS, C::GPL>(mt)
                                                         : 0;
@@ -897,9 +952,10 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
 template <int DT, int BITS, int GS>
 int SkinnyLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
                                     const void* b, void* out, int64_t M, int64_t N, int64_t K,
-                                    hipStream_t st) {
-  if (qmv_nw_for(N) == 8) return skinny_launch_nw<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, st);
-  return skinny_launch_nw<DT, BITS, GS, 4>(x, w, s, b, out, M, N, K, st);
+                                    hipStream_t st, int* nlaunch) {
+  if (qmv_nw_for(N) == 8)
+    return skinny_launch_nw<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, st, nlaunch);
+  return skinny_launch_nw<DT, BITS, GS, 4>(x, w, s, b, out, M, N, K, st, nlaunch);
 }
 
 }  // namespace mq

@@ -320,11 +320,15 @@ def test_skinny_long_k_many_rows(M):
 
 
 @pytest.mark.parametrize("shape, M", [((5120, 17408), 20), ((5120, 17408), 32),
+                                      ((5120, 17408), 40), ((5120, 17408), 64),
                                       ((17408, 5120), 17), ((17408, 5120), 24)])
 def test_skinny_launches_above_16_rows(cfg2_weights, shape, M):
-    """17-32 rows where the wide tile would stream its weights at ~0.9 TB/s
-    run as 16-row skinny launches: each block of rows is bit-identical to a
-    call of those rows alone, and the whole matches the oracle on samples."""
+    """Widths where the wide tile would stream its weights at ~0.9 TB/s run
+    as skinny launches: on the tall matrix (48+ rows per CU) up to 32 rows in
+    one launch whose wave groups multiply each weight fragment with two
+    16-row A tiles, on the narrow one 16 rows per launch.  Each block of 16
+    rows is bit-identical to a call of those rows alone (the same K split),
+    and the whole matches the oracle on sampled columns."""
     K, N = shape
     w, s, b, deq, dev = cfg2_weights[shape]
     rng = np.random.default_rng(500 + M)
@@ -332,7 +336,11 @@ def test_skinny_launches_above_16_rows(cfg2_weights, shape, M):
     xd = to_dev(x, "bfloat16")
     n0 = mq.launch_count()
     out = mq.quantized_matmul(xd, *dev)
-    assert mq.launch_count() - n0 == (M + 15) // 16
+    launches, m0 = 0, 0
+    while m0 < M:
+        m0 += 32 if N == 17408 and M - m0 > 16 else 16
+        launches += 1
+    assert mq.launch_count() - n0 == launches
     ob = bits16(out)
     for m0 in range(0, M, 16):
         part = bits16(mq.quantized_matmul(xd[m0:m0 + 16], *dev))
