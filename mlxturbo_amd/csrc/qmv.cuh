@@ -45,7 +45,10 @@
 //    5-8 rows copy all of x into LDS before the first step, and no step loads
 //    x; 9-16 rows (x too large for LDS) stage each step's x slice once for
 //    the groups, in two buffers per K slice with a workgroup barrier per
-//    step.  Each group's arithmetic is that of the one-group launch.
+//    step; 17-32 rows run in one such launch, each group multiplying every
+//    weight fragment with two 16-row A tiles (x staged in one buffer per
+//    slice, a barrier before and after).  Each group's arithmetic is that of
+//    the one-group launch.
 //  * Dequantization is the exact fma_mix trick of mq_common.h, rounded to T
 //    per weight (bit-exact MLX dequantization); the packed T pairs are the
 //    B operand of v_mfma_f32_16x16x32 (32 k x 16 rows).  A and B use the same
