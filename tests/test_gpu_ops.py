@@ -238,6 +238,33 @@ def test_qmv_two_tiles_tall_matrix(bits):
     np.testing.assert_array_equal(ob[3], one[0])
 
 
+@pytest.mark.parametrize("bits, gs, dtype, N, K", [
+    (4, 64, "bfloat16", 12300, 1088),    # a ragged last step; uneven rows over the groups
+    (4, 32, "float16", 13000, 2048),
+    (8, 64, "bfloat16", 12288, 4096),
+    (4, 128, "bfloat16", 12500, 1536),   # 512-code steps: 16-row launches instead
+])
+def test_qmv_two_a_tiles(bits, gs, dtype, N, K):
+    """17-32 rows in one shared-x launch (two 16-row A tiles per weight
+    fragment): rows bit-identical to the 16-row launches of the same rows,
+    and the oracle on a column sample."""
+    rng = np.random.default_rng(N + K + bits + gs + 1)
+    w, s, b = random_packed(rng, N, K, gs, bits, dtype)
+    x = act(rng, (32, K), dtype, scale=0.1)
+    args = (to_dev(w), to_dev(s, dtype), to_dev(b, dtype))
+    xd = to_dev(x, dtype)
+    lo = bits16(mq.quantized_matmul(xd[:16], *args, group_size=gs, bits=bits))
+    cols = np.concatenate([np.arange(0, 40), np.arange(N - 40, N), rng.choice(N, 80, False)])
+    for M in (17, 25, 32):
+        out = mq.quantized_matmul(xd[:M], *args, group_size=gs, bits=bits)
+        ob = bits16(out)
+        np.testing.assert_array_equal(ob[:16], lo)
+        hi = bits16(mq.quantized_matmul(xd[16:M], *args, group_size=gs, bits=bits))
+        np.testing.assert_array_equal(ob[16:], hi)
+        ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], gs, bits, dtype)
+        _check(out[:, torch.from_numpy(cols).cuda()], ref, dtype)
+
+
 def test_qmm_writes_every_element():
     """Output poisoned with NaN before the call; no element may stay NaN."""
     rng = np.random.default_rng(8)

@@ -47,10 +47,11 @@ def test_qmm_huge_scales(M):
     _check_split(out, ref, huge_rows)
 
 
-@pytest.mark.parametrize("M", [6, 16])
+@pytest.mark.parametrize("M", [6, 16, 24])
 def test_qmm_huge_scales_shared_x(M):
-    """5-16 rows on a matrix of 48+ rows per CU: one workgroup per CU of three
-    wave groups (x resident in LDS for 6 rows, staged per step for 16)."""
+    """5-32 rows on a matrix of 48+ rows per CU: one workgroup per CU of three
+    wave groups (x resident in LDS for 6 rows, staged per step for 16, two
+    16-row A tiles for 24)."""
     rng = np.random.default_rng(40 + M)
     N, K, gs = 12288, 1024, 64
     w, s, b = quantized(rng, N, K, gs)
