@@ -665,11 +665,12 @@ def main():
 
         # config 3: prefill widths on the MFMA tile kernel (compute-bound)
         # configs[2] (512/2048/8192) plus points across the bandwidth/compute
-        # crossover (M ~ 95 at the MFMA ridge): HBM GB/s and TFLOP/s for each,
-        # and the fraction of the measured MFMA ceiling
+        # crossover (M ~ 95 at the MFMA ridge; up to ~70 rows run as 32-row
+        # skinny launches): HBM GB/s and TFLOP/s for each, and the fraction
+        # of the measured MFMA ceiling
         ceiling = measure_mfma_ceiling(torch)
         sweep["mfma_ceiling"] = ceiling
-        for M in (32, 96, 256, 512, 2048, 8192):
+        for M in (32, 64, 96, 256, 512, 2048, 8192):
             r = measure_qmm(torch, mq, M, N, K, 4, 20 if M >= 2048 else 100, 3, copies=2)
             tflops = 2.0 * M * N * K / (r["us"] * 1e-6) / 1e12
             sweep[f"b4_K{K}_N{N}_M{M}"] = {
