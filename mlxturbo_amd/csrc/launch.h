@@ -209,6 +209,23 @@ inline bool wide_eligible(int64_t M, int64_t N, int64_t K, int bits, int gs) {
 // 17-32 rows there in one launch at x1.5 (two 16-row A tiles per weight
 // fragment: M=17/24/32 22.0/21.6/21.1 us, one process).
 // split_ok: a workspace is available for K splits.
+// Rows per launch of the shared-x skinny workgroups on this matrix (the
+// launch conditions of qmv.cuh restated for the route model): 32 when a
+// launch of two 16-row A tiles fits, 16 when only the 5-16-row launch does,
+// 0 when neither runs (fewer than 640 row tiles or 48 rows per CU, steps of
+// more than 256 codes, or x slices and scale copies beyond the LDS).
+inline int skinny_shared_x_rows(int64_t N, int64_t K, int bits, int gs, int cus) {
+  const int64_t stepk = 4 * (int64_t)gs * ((bits == 4 && gs == 32) ? 2 : 1);
+  const int64_t G = K / gs;
+  if ((N + 15) / 16 < 640 || cus <= 0 || N < 48 * (int64_t)cus || stepk > 256) return 0;
+  if (G % 8 != 0 || 2 * 16 * (G / 8) > 3 * 64 * 4) return 0;         // the scale copy
+  const int64_t xsr = 2 * stepk + 16, sb = 6 * 2 * 16 * (2 * G + 16);   // 3 groups x 2 tiles
+  const int64_t lds = 160 * 1024;
+  if (2 * 4 * 16 * xsr + sb > lds - 3 * 4 * 2 * 1024) return 0;       // 16 rows, two buffers
+  if (4 * 32 * xsr + sb <= lds - 3 * 4 * 2 * 2 * 1024) return 32;     // 32 rows, one buffer
+  return 16;
+}
+
 inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus,
                        bool split_ok) {
   if (!wide_eligible(M, N, K, bits, gs)) return false;
@@ -220,10 +237,11 @@ inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cu
   double wide_us = wide_plan(M, N, K, cus, split_ok ? 8 : 1).cost_us;
   if (wide_us < wbytes / 0.9e6) wide_us = wbytes / 0.9e6;
   const double one = 3.0 + wbytes / 3.6e6;
-  const bool shared_x = (N + 15) / 16 >= 640 && cus > 0 && N >= 48 * (int64_t)cus;
+  const int sx = skinny_shared_x_rows(N, K, bits, gs, cus);
+  const bool shared_x = sx > 0;
   double skinny_us = 0.0;
   for (int64_t m0 = 0, step = 16; m0 < M; m0 += step) {
-    step = shared_x && M - m0 > 16 ? 32 : 16;
+    step = sx == 32 && M - m0 > 16 ? 32 : 16;
     const int64_t m = M - m0 < step ? M - m0 : step;
     skinny_us += one * (m > 16   ? 1.5
                         : m > 8  ? (shared_x ? 1.42 : 1.65)

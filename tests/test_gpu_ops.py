@@ -186,7 +186,8 @@ def test_qmv_balanced_rows_match_tiles(N, K):
 
 
 @pytest.mark.parametrize("bits, gs, dtype, N, K", [
-    (4, 64, "bfloat16", 12300, 1088),    # a ragged last step; uneven rows over the groups
+    (4, 64, "bfloat16", 12300, 1024),    # uneven rows over the workgroups and groups
+    (4, 64, "bfloat16", 12300, 1088),    # 17 groups: no scale copy, the one-group launch
     (4, 32, "float16", 13000, 2048),
     (8, 64, "bfloat16", 12288, 4096),
     (4, 128, "bfloat16", 12500, 1536),   # 8 streamed rows (longer steps stream no 16)
@@ -239,15 +240,16 @@ def test_qmv_two_tiles_tall_matrix(bits):
 
 
 @pytest.mark.parametrize("bits, gs, dtype, N, K", [
-    (4, 64, "bfloat16", 12300, 1088),    # a ragged last step; uneven rows over the groups
+    (4, 64, "bfloat16", 12300, 1024),    # uneven rows over the workgroups and groups
     (4, 32, "float16", 13000, 2048),
     (8, 64, "bfloat16", 12288, 4096),
-    (4, 128, "bfloat16", 12500, 1536),   # 512-code steps: 16-row launches instead
 ])
 def test_qmv_two_a_tiles(bits, gs, dtype, N, K):
     """17-32 rows in one shared-x launch (two 16-row A tiles per weight
     fragment): rows bit-identical to the 16-row launches of the same rows,
-    and the oracle on a column sample."""
+    and the oracle on a column sample.  (Shapes without that launch, such as
+    group size 128 or K / group_size not a multiple of 8, price 17-32 rows
+    on the wide tile.)"""
     rng = np.random.default_rng(N + K + bits + gs + 1)
     w, s, b = random_packed(rng, N, K, gs, bits, dtype)
     x = act(rng, (32, K), dtype, scale=0.1)
