@@ -569,6 +569,19 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
 // against 30 split 4 ways; down T=4 10.0 unsplit against 12.2, T=1 (two
 // steps) the same either way.  A tile's float sum depends on it, so the
 // folded down projection below takes the same count.
+// Whether a gather tile copies its scales and biases to LDS: not when each
+// of its nwt waves runs at most two k-steps (decode gathers at T=1 and the
+// down bank), where two per-step loads beat the copy's workgroup barrier
+// (config-4 banks, one process: gate/up T=1 7.03 -> 6.85 us, down 6.14 ->
+// 5.89, GLU 7.76 -> 7.42; with eight steps per wave, gate/up T=4, they lost
+// 13.1 -> 13.8).
+template <int BITS, int GS>
+inline bool gather_tile_sb(int64_t K, int nwt) {
+  using Gm = QmvGeom<BITS, GS, QmvConf<BITS, GS>::GPL>;
+  const int64_t nsteps = (K / GS + Gm::STEPG - 1) / Gm::STEPG;
+  return (nsteps + nwt - 1) / nwt > 2;
+}
+
 template <int BITS, int GS>
 inline int gather_tile_waves(int64_t max_seg, int64_t N, int64_t K) {
   using Gm = QmvGeom<BITS, GS, QmvConf<BITS, GS>::GPL>;
@@ -605,8 +618,8 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
   const int nwt = gather_tile_waves<BITS, GS>(max_seg, N, K);
   const int ng = C::NW / nwt;
   constexpr int TJ = GLU ? 2 : 1;
-  const bool sbl =
-      qmv_sb_fits(K / GS, nwt, TJ, s, b) && (!GLU || qmv_sb_fits(K / GS, nwt, TJ, s2, b2));
+  const bool sbl = gather_tile_sb<BITS, GS>(K, nwt) && qmv_sb_fits(K / GS, nwt, TJ, s, b) &&
+                   (!GLU || qmv_sb_fits(K / GS, nwt, TJ, s2, b2));
   // without the scale copy only the 8-row streamed-x variant is built
   const int xml = (sbl || XM == 0) ? XM : kQmvMaxXM;
   auto lds_for = [&](int xmax, int wpt, bool with_sb) {
@@ -700,7 +713,7 @@ int GatherFoldLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const 
   if (P > 2 * (kFoldNW / nwt)) return kStatusUnsupported;   // more than two rounds
   // scales copied to LDS where the gather kernel copies them (the same tile
   // code either way)
-  const bool sbl = qmv_sb_fits(K / GS, nwt, 1, s, b);
+  const bool sbl = gather_tile_sb<BITS, GS>(K, nwt) && qmv_sb_fits(K / GS, nwt, 1, s, b);
   const size_t lds = (size_t)(kFoldNW / nwt) *
                      gather_group_lds<BITS, GS, C::GPL>(nwt, kQmvMaxXM, sbl, (int)(K / GS), 1);
   // group-size-128 steps are 512 codes: eight streamed x rows per wave take
