@@ -910,6 +910,9 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
     // 247.3 us; 1-2 rows 0-2% slower that way)
     if (xm == 4 && N >= (int64_t)device_cu_count() * 256) tj = 2;
     if (tj == 2 && !qmv_sb_fits(G, NW, 2, s, b)) tj = 1;
+    // two tiles need more than one tile's rows per CU, or half the CUs idle
+    // (K=N=4096 M=8: 128 workgroups on 256 CUs, 7.5 us against 5.6 with one)
+    if (tj == 2 && N <= 16 * (int64_t)device_cu_count()) tj = 1;
     const bool sbl = qmv_sb_fits(G, NW, tj, s, b);
     // without the scale copy: one tile per workgroup, 8 or 16 streamed rows
     if (!sbl && xm) xm = xm > kQmvMaxXM ? 16 : kQmvMaxXM;
