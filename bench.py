@@ -744,7 +744,7 @@ def main():
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": recorded_traffic(),
-            "kernel": "mq::qmv_kernel<bf16,4,64,...>",
+            "kernel": "mq::qmv_quad_kernel<bf16,4,64>",
             "avg_launch_us": round(head["us"], 3),
             "measured_read": read,
             "frac_of_measured_read": round(value / read["GBps"], 4),

@@ -47,6 +47,11 @@ def hipcc() -> str:
 UNITS = [("abi.hip", []), ("formats.hip", []), ("prep.hip", []), ("route.hip", [])] + [
     ("inst.hip", [f"-DMQ_INST_DT={dt}", f"-DMQ_INST_BITS={bits}"] + glu)
     for glu in ([], ["-DMQ_INST_GLU"]) for dt in (0, 1) for bits in (4, 8)
+] + [
+    # the quad kernel keeps its MFMA accumulators in VGPRs (qmv_quad.cuh)
+    ("quad.hip", [f"-DMQ_INST_DT={dt}", f"-DMQ_INST_BITS={bits}", "-mllvm",
+                  "-amdgpu-mfma-vgpr-form"])
+    for dt in (0, 1) for bits in (4, 8)
 ]
 
 _NOISE = ("packed-fp32-ops", "warning generated", "warnings generated")

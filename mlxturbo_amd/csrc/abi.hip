@@ -238,6 +238,20 @@ int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
     return MQ_OK;
   }
   int nl = 0;
+  if (M == 1) {
+    rc = dispatch_16<mq::QuadLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
+                                     st, &nl);
+    if (rc == 0) {
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess)
+        return fail((int)e, "quantized_matmul(quad): launch failed: %s", hipGetErrorString(e));
+      g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+      return MQ_OK;
+    }
+    if (rc != mq::kStatusUnsupported)
+      return fail(rc, "quantized_matmul(quad): launch failed: %s",
+                  hipGetErrorString((hipError_t)rc));
+  }
   rc = dispatch_16<mq::SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
                                      st, &nl);
   if (rc) return fail(rc, "quantized_matmul: no kernel for dtype=%d bits=%d group_size=%d", dtype,

@@ -25,6 +25,16 @@ struct SkinnyLaunch {
                  int64_t M, int64_t N, int64_t K, hipStream_t st, int* nlaunch);
 };
 
+// quantized_matmul of one row on the quad kernel (qmv_quad.cuh, its own
+// translation unit quad.hip); kStatusUnsupported where it does not apply
+// (M != 1, unaligned operands: then SkinnyLaunch runs).  *nlaunch counts the
+// kernels enqueued.
+template <int DT, int BITS, int GS>
+struct QuadLaunch {
+  static int run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
+                 int64_t M, int64_t N, int64_t K, hipStream_t st, int* nlaunch);
+};
+
 // quantized_matmul for M > 16 rows on the MFMA tile kernel (qmm_wide.cuh);
 // with a workspace of wide_workspace_bytes(wide_plan(...), M, N) bytes the
 // K range may be split over workgroups (float partial planes plus a reduce

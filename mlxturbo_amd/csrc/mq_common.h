@@ -42,6 +42,13 @@ __device__ __forceinline__ To bitcast(const From& v) {
   return __builtin_bit_cast(To, v);
 }
 
+// Buffer resource for a raw (unstructured) byte range.  Word 3 is the gfx9
+// default for 32-bit data; out-of-range loads return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
 // 16-bit storage types: bf16 (kBF16) and IEEE half (kF16).
 template <int DT> struct T16;
 

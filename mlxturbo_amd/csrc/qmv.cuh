@@ -68,13 +68,6 @@ typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
-// Buffer resource for a raw (unstructured) byte range.  Word 3 is the gfx9
-// default for 32-bit data; out-of-range loads return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-
 // v_perm selector moving 16-bit half h (0..3 of the 64-bit pair {hi:lo}) to
 // where a float conversion wants it: bf16 -> bits 16..31 (the float's bits),
 // f16 -> bits 0..15.  Selector byte 0x0c yields 0x00.

@@ -123,12 +123,12 @@ def test_dispatched_forward_matches_operator(M):
     with dispatch.dispatch_scope():
         np.testing.assert_array_equal(bits16(layer(x)), want)
     # a table routing wide inputs through 16-row skinny launches: each row is
-    # bit-identical to the one-row result (the skinny kernel's property)
+    # bit-identical to the two-row result (the skinny kernel's property)
     table = {(K, N): tuple(["stock"] + ["skinny"] * 64)}
     got = bits16(dispatch.quantized_matmul(x, layer.weight, layer.scales, layer.biases,
                                            group_size=64, bits=4, table=table))
-    one = bits16(mq.quantized_matmul(x[:1, :1], layer.weight, layer.scales, layer.biases))
-    np.testing.assert_array_equal(got[0, 0], one[0, 0])
+    two = bits16(mq.quantized_matmul(x[:1, :2], layer.weight, layer.scales, layer.biases))
+    np.testing.assert_array_equal(got[0, :2], two[0])
     assert got.shape == (2, M, N)
     dispatch.disable(layer)
 

@@ -146,7 +146,10 @@ def test_qmm_leading_dims():
 
 def test_qmm_rows_bit_identical_across_widths():
     """Each row's answer does not depend on the verify width M (the property
-    the reference's qmv_small_m test pins: bench/test_qmm_smallm.py:70-85)."""
+    the reference's qmv_small_m test pins: bench/test_qmm_smallm.py:70-85)
+    for every M >= 2, which run the 16-row skinny family.  One-row calls run
+    the quad kernel, which sums the same products in its own order: they
+    meet the oracle and stay within the tolerance of the M >= 2 rows."""
     rng = np.random.default_rng(6)
     N, K = 2048, 5120
     w, s, b = random_packed(rng, N, K)
@@ -154,32 +157,64 @@ def test_qmm_rows_bit_identical_across_widths():
     args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
     xd = to_dev(x, "bfloat16")
     full = bits16(mq.quantized_matmul(xd, *args))
-    for M in (1, 2, 5, 9, 16):
+    for M in (2, 3, 5, 9, 16):
         part = bits16(mq.quantized_matmul(xd[:M], *args))
         np.testing.assert_array_equal(part, full[:M])
-    for v in (0, 7, 15):
-        one = bits16(mq.quantized_matmul(xd[v:v + 1], *args))
-        np.testing.assert_array_equal(one[0], full[v])
+    for v in (0, 7, 14):
+        pair = bits16(mq.quantized_matmul(xd[v:v + 2], *args))
+        np.testing.assert_array_equal(pair, full[v:v + 2])
+    ref = O.quantized_matmul_ref(x, w, s, b)
+    for v in (0, 15):
+        one = mq.quantized_matmul(xd[v:v + 1], *args)
+        _check(one, ref[v:v + 1])
+    _check(mq.quantized_matmul(xd, *args), ref)
+
+
+def _qmm_abi(xd, wd, sd, bd, M, N, K, gs=64, bits=4):
+    """One mq_quantized_matmul call through the C ABI (operand pointers as
+    given, so a caller can pass unaligned scale views)."""
+    out = torch.empty((M, N), dtype=xd.dtype, device="cuda")
+    rc = _lib.lib().mq_quantized_matmul(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(),
+                                        bd.data_ptr(), out.data_ptr(), M, N, K, gs, bits,
+                                        0 if xd.dtype == torch.bfloat16 else 1, 1,
+                                        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.lib().mq_last_error()
+    return out
+
+
+def _unaligned(t):
+    """The same values at a base 2 bytes past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    v = buf[1:1 + t.numel()].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 16 == 2
+    return v
 
 
 @pytest.mark.parametrize("N, K", [(3500, 1024), (17408, 5120), (5120, 17408)])
 def test_qmv_balanced_rows_match_tiles(N, K):
-    """Launches spread the rows evenly over the CUs when the workgroups do not
-    divide over them: one-row calls (N=17408 on 256 CUs: 1280 workgroups of
-    13-14 rows; N=3500: 256 of 13-14) and two-tile calls of 9 rows (N=5120:
-    256 workgroups of 20; N=17408: one workgroup of three wave groups per
-    CU).  Every row must be bit-identical to the tiled launch of a two-row
-    call."""
+    """Launches of the 16-row skinny kernel spread the rows evenly over the
+    CUs when the workgroups do not divide over them: one-row calls (N=17408
+    on 256 CUs: 1280 workgroups of 13-14 rows; N=3500: 256 of 13-14; one-row
+    calls take that kernel when the quad kernel declines, here scales and
+    biases that are not 16-byte aligned) and two-tile calls of 9 rows
+    (N=5120: 256 workgroups of 20; N=17408: one workgroup of three wave
+    groups per CU).  Every row must be bit-identical to the tiled launch of a
+    two-row call; the aligned one-row call (quad kernel) meets the oracle."""
     rng = np.random.default_rng(11)
     w, s, b = random_packed(rng, N, K)
     x = act(rng, (9, K), scale=0.1)
     args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
     xd = to_dev(x, "bfloat16")
     two = bits16(mq.quantized_matmul(xd[:2], *args))
+    sk = _qmm_abi(xd[:1], args[0], _unaligned(args[1]), _unaligned(args[2]), 1, N, K)
+    np.testing.assert_array_equal(bits16(sk)[0], two[0])
     one = mq.quantized_matmul(xd[:1], *args)
-    np.testing.assert_array_equal(bits16(one)[0], two[0])
     nine = bits16(mq.quantized_matmul(xd, *args))
     np.testing.assert_array_equal(nine[:2], two)
+    cols = np.concatenate([np.arange(0, 40), np.arange(N - 40, N), rng.choice(N, 80, False)])
+    _check(one[:, torch.from_numpy(cols).cuda()],
+           O.quantized_matmul_ref(x[:1], w[cols], s[cols], b[cols]))
     if N * K <= 4 << 20:
         _check(one, O.quantized_matmul_ref(x[:1], w, s, b))
         _check(mq.quantized_matmul(xd, *args), O.quantized_matmul_ref(x, w, s, b))
@@ -197,7 +232,7 @@ def test_qmv_shared_x_groups(bits, gs, dtype, N, K):
     """5-16 rows on matrices of >= 48 rows per CU run one workgroup per CU of
     three wave groups that read x once for all of them (5-8 rows: all of x
     resident in LDS; 9-16: each step's slice staged once).  Every row must be
-    bit-identical to the one- and two-row launches (the same K split) and
+    bit-identical to the two-row launches (the same K split) and
     match the oracle on a column sample."""
     rng = np.random.default_rng(N + K + bits + gs)
     w, s, b = random_packed(rng, N, K, gs, bits, dtype)
@@ -213,14 +248,14 @@ def test_qmv_shared_x_groups(bits, gs, dtype, N, K):
         np.testing.assert_array_equal(ob[:2], two)
         ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], gs, bits, dtype)
         _check(out[:, colt], ref, dtype)
-    one = bits16(mq.quantized_matmul(xd[15:16], *args, group_size=gs, bits=bits))
-    np.testing.assert_array_equal(ob[15], one[0])
+    pair = bits16(mq.quantized_matmul(xd[14:16], *args, group_size=gs, bits=bits))
+    np.testing.assert_array_equal(ob[14:16], pair)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_qmv_two_tiles_tall_matrix(bits):
     """3-4 rows on matrices of 256+ rows per CU run two tiles per x slice;
-    each row stays bit-identical to the one- and two-row launches."""
+    each row stays bit-identical to the two-row launches."""
     rng = np.random.default_rng(77 + bits)
     N, K = 65600, 1024
     w, s, b = random_packed(rng, N, K, 64, bits)
@@ -228,7 +263,7 @@ def test_qmv_two_tiles_tall_matrix(bits):
     args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
     xd = to_dev(x, "bfloat16")
     two = bits16(mq.quantized_matmul(xd[:2], *args, bits=bits))
-    one = bits16(mq.quantized_matmul(xd[3:4], *args, bits=bits))
+    pair = bits16(mq.quantized_matmul(xd[2:4], *args, bits=bits))
     cols = np.concatenate([np.arange(0, 40), np.arange(N - 40, N), rng.choice(N, 80, False)])
     for M in (3, 4):
         out = mq.quantized_matmul(xd[:M], *args, bits=bits)
@@ -236,7 +271,7 @@ def test_qmv_two_tiles_tall_matrix(bits):
         np.testing.assert_array_equal(ob[:2], two)
         ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], 64, bits)
         _check(out[:, torch.from_numpy(cols).cuda()], ref)
-    np.testing.assert_array_equal(ob[3], one[0])
+    np.testing.assert_array_equal(ob[2:4], pair)
 
 
 @pytest.mark.parametrize("bits, gs, dtype, N, K", [
@@ -261,8 +296,11 @@ def test_qmv_two_a_tiles(bits, gs, dtype, N, K):
         out = mq.quantized_matmul(xd[:M], *args, group_size=gs, bits=bits)
         ob = bits16(out)
         np.testing.assert_array_equal(ob[:16], lo)
-        hi = bits16(mq.quantized_matmul(xd[16:M], *args, group_size=gs, bits=bits))
-        np.testing.assert_array_equal(ob[16:], hi)
+        # (a block of one row is compared through a two-row call: one-row
+        # calls run the quad kernel)
+        lo_row = 15 if M == 17 else 16
+        hi = bits16(mq.quantized_matmul(xd[lo_row:M], *args, group_size=gs, bits=bits))
+        np.testing.assert_array_equal(ob[16:], hi[16 - lo_row:])
         ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], gs, bits, dtype)
         _check(out[:, torch.from_numpy(cols).cuda()], ref, dtype)
 
@@ -333,7 +371,7 @@ def test_config2_skinny(cfg2_weights, shape, M):
 def test_skinny_long_k_many_rows(M):
     """K=17408 with N >= 10240 (four waves per tile): the two-tile scale copy
     would not fit, so these widths run one tile per workgroup; checked on a
-    column sample and against the one-row results."""
+    column sample and against the two-row results."""
     rng = np.random.default_rng(300 + M)
     N, K = 10256, 17408
     w, s, b = random_packed(rng, N, K)
@@ -344,8 +382,8 @@ def test_skinny_long_k_many_rows(M):
     cols = np.concatenate([np.arange(0, 48), np.arange(N - 40, N), rng.choice(N, 64, False)])
     ref = O.quantized_matmul_ref(x, w[cols], s[cols], b[cols])
     _check(out[:, torch.from_numpy(cols).cuda()], ref)
-    one = bits16(mq.quantized_matmul(xd[M - 1:], *args))
-    np.testing.assert_array_equal(bits16(out)[M - 1], one[0])
+    pair = bits16(mq.quantized_matmul(xd[M - 2:], *args))
+    np.testing.assert_array_equal(bits16(out)[M - 2:], pair)
 
 
 @pytest.mark.parametrize("shape, M", [((5120, 17408), 20), ((5120, 17408), 32),
@@ -372,8 +410,10 @@ def test_skinny_launches_above_16_rows(cfg2_weights, shape, M):
     assert mq.launch_count() - n0 == launches
     ob = bits16(out)
     for m0 in range(0, M, 16):
-        part = bits16(mq.quantized_matmul(xd[m0:m0 + 16], *dev))
-        np.testing.assert_array_equal(ob[m0:m0 + 16], part)
+        # a block of one row through a two-row call (one-row calls: quad kernel)
+        lo_row = m0 - 1 if M - m0 == 1 else m0
+        part = bits16(mq.quantized_matmul(xd[lo_row:m0 + 16], *dev))
+        np.testing.assert_array_equal(ob[m0:m0 + 16], part[m0 - lo_row:])
     cols = np.sort(rng.choice(N, size=512, replace=False))
     ref = (O.bf16_to_f32(x).astype(np.float64) @ deq[cols].T).astype(np.float32)
     _check(out[:, torch.from_numpy(cols).cuda()], ref)
@@ -487,8 +527,10 @@ def test_config5_lm_head_8bit(lm_head_8bit, M):
     cols = np.sort(rng.choice(N, size=3000, replace=False))
     ref = O.quantized_matmul_ref(x, w[cols], s[cols], b[cols], gs, bits)
     _check(out[:, torch.from_numpy(cols).cuda()], ref)
-    one = bits16(mq.quantized_matmul(to_dev(x[-1:], "bfloat16"), *dev, group_size=gs, bits=bits))
-    np.testing.assert_array_equal(one[0], bits16(out)[-1])
+    if M >= 2:   # rows of 2+ row calls do not depend on M (one-row calls: quad kernel)
+        pair = bits16(mq.quantized_matmul(to_dev(x[-2:], "bfloat16"), *dev, group_size=gs,
+                                          bits=bits))
+        np.testing.assert_array_equal(pair, bits16(out)[-2:])
 
 
 # ---------------------------------------------------------------- gather_qmm
