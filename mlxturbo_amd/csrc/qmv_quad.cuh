@@ -69,15 +69,6 @@ __device__ __forceinline__ f32x4 quad_mfma(uint32_t a0, uint32_t a1, uint32_t b0
                                               __builtin_bit_cast(qq_f16x4, b), c, 0, 0, 0);
 }
 
-// Whether the 16-bit scale in the low half of v needs the plain route
-// (|s| >= 2^100, inf or NaN; float16's finite range stays below).
-template <int DT>
-__device__ __forceinline__ bool quad_half_big(uint32_t v) {
-  const uint32_t h = v & 0x7fffu;
-  if constexpr (DT == kBF16) return h >= 0x7180u;   // bf16 2^100
-  else return h >= 0x7c00u;                          // f16 inf / NaN
-}
-
 // Geometry of one load instruction of a quad.
 template <int BITS, int GS>
 struct QuadGeom {
@@ -121,8 +112,10 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   extern __shared__ __align__(16) unsigned char qq_smem[];
   __shared__ float red[kQuadMaxKS][4];
 
+  // (the K split is a power of two, so its divisions are scalar shifts)
   const int lane = threadIdx.x & 63;
-  const int KS = blockDim.x >> 6;
+  const int lks = __builtin_ctz(blockDim.x >> 6);
+  const int KS = 1 << lks;
   const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 3, bb = lane >> 2;
   const int row0 = 4 * blockIdx.x;
@@ -130,9 +123,9 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const int G = K / GS;
   const int nI = (int)((rowB + Q::RB - 1) / Q::RB);
-  const int s0 = (int)((int64_t)nI * kp / KS), s1 = (int)((int64_t)nI * (kp + 1) / KS);
+  const int s0 = (nI * kp) >> lks, s1 = (nI * (kp + 1)) >> lks;
   const int n = s1 - s0;
-  const int nmax = (nI + KS - 1) / KS;
+  const int nmax = (nI + KS - 1) >> lks;
 
   // ---- scale / bias copy of the wave's groups: the loads -----------------
   // Row r's groups [s0 GPI, s1 GPI) start at byte a_r of the arrays; chunk c
@@ -212,33 +205,39 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   for (int i = 0; i < D; ++i) issue(i, i);
 
   // ---- the scale copy lands in LDS behind the weight prologue -------------
-  // Entries outside the row (groups < 0 or >= G: the align-down and the
-  // ragged last instruction) are stored as zeros, so a lane whose piece lies
-  // past K dequantizes zeros.  The big-scale check reads every loaded chunk,
-  // which keeps the compiler from sinking the loads into the stores' branch
-  // (a big scale of a neighbouring row only costs the wave the plain route).
-  bool big = false;
+  // Entries past the row (groups >= G: the ragged last instruction) are
+  // stored as zeros, so a lane whose piece lies past K dequantizes zeros;
+  // only a row's last chunk holds any.  The big-scale check (a packed 16-bit
+  // max over every loaded chunk) also keeps the compiler from sinking the
+  // loads into the stores' branch; a big scale of a neighbouring row only
+  // costs the wave the plain route.
+  typedef unsigned short qq_u16x2 __attribute__((ext_vector_type(2)));
+  qq_u16x2 hmax = {0, 0};
 #pragma unroll
   for (int u = 0; u < kQuadSbPerLane; ++u) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      big = big || quad_half_big<DT>(sq[u][e]) || quad_half_big<DT>(sq[u][e] >> 16);
+      hmax = __builtin_elementwise_max(hmax,
+                                       __builtin_bit_cast(qq_u16x2, sq[u][e] & 0x7fff7fffu));
     const int cc = cc0 + 16 * u;
     if (cc < CH) {
       const int g0c = (int)((ca0 + 256 * u - crow) >> 1);   // group of the chunk's entry 0
       u32x4 sv = sq[u], bv = bq[u];
+      if (g0c + 8 > G) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool lo_in = g0c + 2 * e >= 0 && g0c + 2 * e < G;
-        const bool hi_in = g0c + 2 * e + 1 >= 0 && g0c + 2 * e + 1 < G;
-        const uint32_t keep = (lo_in ? 0x0000ffffu : 0u) | (hi_in ? 0xffff0000u : 0u);
-        sv[e] &= keep;
-        bv[e] &= keep;
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t keep = (g0c + 2 * e < G ? 0x0000ffffu : 0u) |
+                                (g0c + 2 * e + 1 < G ? 0xffff0000u : 0u);
+          sv[e] &= keep;
+          bv[e] &= keep;
+        }
       }
       *(lds_u32x4*)(ls + cr * 16 * CH + 16 * cc) = sv;
       *(lds_u32x4*)(ls + 4 * 16 * CH + cr * 16 * CH + 16 * cc) = bv;
     }
   }
+  const uint32_t hm = hmax[0] > hmax[1] ? hmax[0] : hmax[1];
+  const bool big = DT == kBF16 ? hm >= 0x7180u : hm >= 0x7c00u;   // bf16 2^100 / f16 inf
   const bool plain = __builtin_amdgcn_ballot_w64(big) != 0;
   // the scale copy is this wave's own: order its LDS stores before the reads
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
