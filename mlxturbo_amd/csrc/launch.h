@@ -236,6 +236,19 @@ inline int skinny_shared_x_rows(int64_t N, int64_t K, int bits, int gs, int cus)
   return 16;
 }
 
+// Whether 5-8 rows run the shared-x launch with x resident in LDS (the
+// condition of qmv.cuh's launcher restated): m rows of x padded to whole
+// steps plus the three groups' scale copies within the launch's dynamic LDS
+// (kQmvShxLdsMax: the CU's 160 KiB less the static reduction buffers).
+inline bool skinny_resident_x_fits(int64_t m, int64_t K, int bits, int gs) {
+  const int64_t stepk = 4 * (int64_t)gs * ((bits == 4 && gs == 32) ? 2 : 1);
+  const int64_t G = K / gs, stepg = stepk / gs;
+  const int64_t nsteps = (G + stepg - 1) / stepg;
+  const int64_t xres = m * (2 * nsteps * stepk + 16);
+  const int64_t sb = 6 * 2 * 16 * (2 * G + 16);                      // 3 groups x 2 tiles
+  return xres + sb <= 160 * 1024 - 3 * 4 * 2 * 64 * 16;
+}
+
 inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus,
                        bool split_ok) {
   if (!wide_eligible(M, N, K, bits, gs)) return false;
@@ -255,7 +268,8 @@ inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cu
     const int64_t m = M - m0 < step ? M - m0 : step;
     skinny_us += one * (m > 16   ? 1.5
                         : m > 8  ? (shared_x ? 1.42 : 1.65)
-                        : m > 4  ? (shared_x ? 1.35 : 1.4)
+                        : m > 4  ? (shared_x && skinny_resident_x_fits(m, K, bits, gs) ? 1.35
+                                                                                       : 1.4)
                         : m > 1  ? 1.15
                                  : 1.0);
   }

@@ -608,18 +608,9 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
         if (u + i < nmax) compute(S[i], sb + u + i, false, (u + i) & 1, sb + u + i >= fe);
       }
     }
-    // the last slice's ragged step (only its waves hold one), in every wave
-    if (full < nsteps) {
-      Stage s;
-      const bool mine = fe < se;
-      load(s, fe, mine);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int L = 0; L < NL; ++L)
-          if (fe * STEPG + ((4 * L + c) >> SH) >= G) s.w[j][L] = (u32x4){0u, 0u, 0u, 0u};
-      compute(s, fe, true, nmax & 1, !mine);
-    }
+    // No ragged step here: these launches need the scale copy, which takes
+    // G % 8 == 0 groups (qmv_sb_fits), and the steps' 2, 4 or 8 groups
+    // divide 8, so every step lies inside K (full == nsteps).
   } else {
     for (int t = sb; t < fe; t += PF) {
 #pragma unroll
@@ -840,6 +831,8 @@ inline int skinny_launch_shx_xm(const uint16_t* x, const uint32_t* w, const void
                                 const void* b, uint16_t* out, int M, int64_t N, int64_t K,
                                 size_t lds, unsigned grid, hipStream_t st) {
   using C = QmvConf<BITS, GS>;
+  // the streamed-x launches have no ragged-step code: K must be whole steps
+  if (!XRES && (K / GS) % QmvGeom<BITS, GS, C::GPL>::STEPG != 0) return kStatusUnsupported;
   auto kern =
       &qmv_shx_kernel<DT, BITS, GS, C::GPL, 4, C::PF, XM, true, kQmvShxTJ, kQmvShxNG, XRES, MT>;
   static std::atomic<uint64_t> lds_set{0};

@@ -348,11 +348,14 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     """The gather workspace of the current stream (kernels on one stream run
     in order, so consecutive calls can share it; calls on other streams get
     their own, as concurrent calls must not share one).  A buffer outgrown
-    after a graph capture is kept alive (captured kernels may use it)."""
+    after a graph capture is kept alive (captured kernels may use it).  The
+    capture check runs on every call, cache hits included: a capture that
+    only ever found the buffer cached (warm-up on the capture stream, then
+    capture) still pins it."""
+    _capturing()
     key = (dev.type, _dev_index(dev), _stream_of(dev))
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
-        _capturing()
         if buf is not None:
             _retire([buf])
         buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
@@ -382,6 +385,7 @@ def _default_lhs(dev: torch.device, bx: tuple, shape: tuple) -> Optional[torch.T
     and stream (it is written by kernels on the stream that built it)."""
     if _repeat_broadcast(bx, shape):
         return None
+    capturing = _capturing()          # every call: a cached table used by a capture is pinned
     key = (dev.type, dev.index, _stream_of(dev), tuple(bx), tuple(shape))
     t = _LHS_CACHE.get(key)
     if t is None:
@@ -390,7 +394,7 @@ def _default_lhs(dev: torch.device, bx: tuple, shape: tuple) -> Optional[torch.T
              .reshape(-1).contiguous())
         # a table built under graph capture holds data only once the graph
         # replays, so it is not offered to later eager calls
-        if not _capturing():
+        if not capturing:
             if len(_LHS_CACHE) > 64:
                 _retire(_LHS_CACHE.values())
                 _LHS_CACHE.clear()
@@ -406,13 +410,15 @@ def _as_index(t, dev) -> torch.Tensor:
     return t.to(device=dev)
 
 
-def _gather_prep(x, banks, lhs_indices, rhs_indices, transpose, group_size, bits, mode):
+def _gather_prep(x, banks, lhs_indices, rhs_indices, transpose, group_size, bits, mode,
+                 alloc=True):
     """Validation and flattening shared by gather_qmm and gather_glu; ``banks``
     is a list of (w, scales, biases) of one shape.  Returns ``(out, args)``:
     ``args`` is None when there is nothing to compute, else the flattened
     call (``route``: "kernel", "rows" (more than 16 rows per pair), "slices"
     (more experts than the prep kernel's tables hold) or "composed" (no
-    kernel for the format or dtype))."""
+    kernel for the format or dtype)).  With ``alloc=False`` (a caller that
+    writes its own output) ``out`` is None."""
     for _, _, b in banks:
         _check_mode(mode, b)
     dev = _require_gpu(x, *[t for bank in banks for t in bank])
@@ -446,7 +452,7 @@ def _gather_prep(x, banks, lhs_indices, rhs_indices, transpose, group_size, bits
         raise ValueError(f"lhs_indices {lshape} and rhs_indices "
                          f"{tuple(rhs.shape)} do not broadcast") from exc
     P = math.prod(shape)
-    out = torch.empty((*shape, M, N), dtype=out_dtype, device=dev)
+    out = torch.empty((*shape, M, N), dtype=out_dtype, device=dev) if alloc else None
     if P == 0 or M == 0 or N == 0:
         return out, None
     lhs_f = (_default_lhs(dev, bx, tuple(shape)) if lhs is None
@@ -683,8 +689,8 @@ def gather_qmm_combine(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
 
     if T == 0 or T * top_k > _FOLD_MAX_P:
         return composed()
-    out_pairs, a = _gather_prep(xs, [(w, scales, biases)], None, idx, transpose, group_size,
-                                bits, mode)
+    _, a = _gather_prep(xs, [(w, scales, biases)], None, idx, transpose, group_size, bits, mode,
+                        alloc=False)
     if a is None or a["route"] != "kernel" or a["M"] != 1 or a["dtype"] != x.dtype:
         return composed()
     N = a["N"]
@@ -693,7 +699,6 @@ def gather_qmm_combine(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
             raise ValueError(f"sgate must hold {T} gates and shared be ({T}, {N})")
         if sgate.dtype != x.dtype or shared.dtype != x.dtype:
             raise ValueError("sgate and shared must have x's dtype")
-    del out_pairs
     out = torch.empty((T, N), dtype=x.dtype, device=dev)
     w_ = weights.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
     sg_ = sgate.reshape(-1).contiguous() if sgate is not None else None

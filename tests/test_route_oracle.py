@@ -103,6 +103,35 @@ def test_sigmoid_t_points(dtype):
     assert np.all(np.abs(sym - (1.0 - got)) <= 2 * ulp2)
 
 
+def test_sigmoid_t_per_operation_rounding_known_answers():
+    """Known answers worked by hand, where rounding every operation to T (the
+    reference's form, moe_route_decode.py:141-146) and rounding the exact
+    sigmoid once give different T values.
+
+    bf16 (8 significant bits), x = -5: exp(5) = 148.41 -> 148; 1 + 148 =
+    149 exactly; 1/149 = 219.92 * 2^-15 -> 220 * 2^-15.  The exact
+    sigmoid(-5) = 0.0066929 = 219.31 * 2^-15 rounds to 219 * 2^-15.
+    bf16, x = -5.75: exp(5.75) = 314.19 -> 314 (ulp 2 above 256); 1 + 314 =
+    315, halfway between 314 and 316 -> 316 (even mantissa); 1/316 = 207.39
+    * 2^-16 -> 207 * 2^-16.  Once: 0.0031727 = 207.92 * 2^-16 -> 208.
+    fp16 (11 bits), x = -7.75: exp(7.75) = 2321.57 -> 2322 (ulp 2 above
+    2048); 1 + 2322 = 2323 -> 2324 (tie, even); 1/2324 = 1804.78 * 2^-22 ->
+    1805 * 2^-22.  Once: 0.00043056 = 1805.91 * 2^-22 -> 1806."""
+    got = O.sigmoid_t(np.array([-5.0, -5.75], np.float32), "bfloat16")
+    assert got[0] == np.float32(220 * 2.0 ** -15)
+    assert got[1] == np.float32(207 * 2.0 ** -16)
+    got16 = O.sigmoid_t(np.array([-7.75], np.float32), "float16")
+    assert got16[0] == np.float32(1805 * 2.0 ** -22)
+
+    # the plausible mistake (the sigmoid in float, rounded to T once) differs
+    def once(x, dtype):
+        f = (1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))).astype(np.float32)
+        return O.to_f32(O.from_f32(f, dtype), dtype)
+
+    assert once([-5.0, -5.75], "bfloat16").tolist() == [219 * 2.0 ** -15, 208 * 2.0 ** -16]
+    assert once([-7.75], "float16")[0] == np.float32(1806 * 2.0 ** -22)
+
+
 def test_route_shared_gate_is_sigmoid_of_rounded_dot():
     rng = np.random.default_rng(3)
     H = 64
