@@ -121,21 +121,24 @@ def copies_for(nbytes: int, requested: int = 0) -> int:
 
 
 def make_weights(torch, N, K, copies, seed=1, bits=4, gs=64):
-    """`copies` distinct random weight sets on the GPU (synthetic, seeded).
-
-    Codes are uniform random words; scales/biases are small bf16 values, the
-    magnitudes MLX's quantizer produces for N(0, 0.02) weights.  The kernel's
-    work does not depend on the values; the parity tests cover MLX-quantized
-    N(0, 0.02) weights of the same shapes.
-    """
+    """`copies` distinct weight sets on the GPU: seeded N(0, 0.02) bf16
+    matrices quantized by the library's own ``quantize`` (MLX's affine
+    scheme), the weights the stated workload names.  The dense matrix is
+    made and quantized in slabs of rows so that only the packed copies stay
+    resident (the 8-bit lm_head is 2.5 GB of bf16 per copy)."""
+    import mlxturbo_amd as mq
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
+    slab = max(1, min(N, (256 << 20) // (2 * K)))
     out = []
     for _ in range(copies):
-        w = torch.randint(-2**31, 2**31 - 1, (N, K * bits // 32), dtype=torch.int32,
-                          device="cuda", generator=g).view(torch.uint32)
-        s = (torch.rand((N, K // gs), device="cuda", generator=g) * 0.002).to(torch.bfloat16)
-        b = (torch.rand((N, K // gs), device="cuda", generator=g) * 0.02 - 0.01).to(torch.bfloat16)
+        w = torch.empty((N, K * bits // 32), dtype=torch.uint32, device="cuda")
+        s = torch.empty((N, K // gs), dtype=torch.bfloat16, device="cuda")
+        b = torch.empty_like(s)
+        for r0 in range(0, N, slab):
+            r1 = min(N, r0 + slab)
+            dense = (torch.randn((r1 - r0, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+            w[r0:r1], s[r0:r1], b[r0:r1] = mq.quantize(dense, gs, bits)
         out.append((w, s, b))
     return out
 
@@ -652,13 +655,16 @@ def main():
     ms_per_step = head["us"] * 1e-3
     read = measure_stream_read(torch, head["bytes"])
 
+    # every sweep row runs a fixed number of steps of its own, whatever
+    # --steps says (--steps and --warmup are the headline's), so a row reads
+    # the same from any command line
     sweep = {}
     if not args.no_sweep:
         for (KK, NN, bits, Ms) in ((4096, 4096, 4, (1,)), (5120, 17408, 4, (2, 4, 8, 16)),
                                    (17408, 5120, 4, (1, 2, 4, 8, 16)),
                                    (5120, 248320, 8, (1, 2, 4))):
             for M in Ms:
-                r = measure_qmm(torch, mq, M, NN, KK, bits, min(args.steps, 100), 5)
+                r = measure_qmm(torch, mq, M, NN, KK, bits, 100, 5)
                 sweep[f"b{bits}_K{KK}_N{NN}_M{M}"] = {
                     "us": round(r["us"], 2), "GBps": round(r["GBps"], 1),
                     "pct_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}

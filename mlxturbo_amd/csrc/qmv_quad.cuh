@@ -12,11 +12,15 @@
 //    That pattern read in 8.0 us, as fast as a contiguous read (7.8); 16
 //    rows x 64 bytes per instruction (half lines, the 16-row skinny tile's
 //    B operand) took 9.0, and 11.9 with the non-temporal bit.
-//  * One wave per workgroup: N / 4 quads deal evenly over the CUs (K=5120
-//    N=17408: 17 waves per CU) where 4-wave workgroups left a quarter of the
-//    CUs a workgroup ahead (8.0 against 8.6 us, read only).  With too few
-//    quads, K is split over KS waves of a workgroup whose partial sums meet
-//    in LDS.
+//  * Waves deal evenly over the SIMDs.  With too few quads, K is split over
+//    KS waves of a workgroup whose partial sums meet in LDS.  With many, one
+//    wave per quad leaves a partial last round: K=5120 N=17408 is 4352 quads
+//    on 1024 SIMDs, 4 waves each and a fifth on a quarter of them, and the
+//    kernel is VALU-bound per SIMD (about 950 VALU per wave), so those SIMDs
+//    set the time.  The leftover quads (quads mod 4 x CUs) are then split W
+//    ways (W = 2 or 4 waves per workgroup, the full quads W to a workgroup,
+//    one wave each): every SIMD gets 4 whole quads and a quarter of one
+//    (11.5-12.0 against 12.6-13.1 us).
 //  * The scales and biases of the wave's groups are copied into the wave's
 //    LDS once, with 16-byte loads (per-instruction 4-byte scale loads cost
 //    2.1 us of a 10 us read, the copy 0.9).
@@ -34,7 +38,8 @@
 //    per-instruction check costs a branch per instruction).
 //  * The kept rows are summed in class order, then over the 16 lanes of a
 //    row in a fixed xor tree, then over the K split in wave order; one
-//    rounding.  The K split depends on (N, K, bits, group_size) only.
+//    rounding.  The K split depends on (N, K, bits, group_size) and the
+//    device's CU count only.
 //
 // Calls of 2+ rows run the 16-row skinny family (qmv.cuh): a 4 x 4 block
 // product over x rows read per lane (64 bytes per lane per instruction)
@@ -95,14 +100,17 @@ __host__ __device__ inline int quad_sb_chunks(int ninst) {
   return (ninst * QuadGeom<BITS, GS>::GPI * 2 + 15) / 16 + 1;
 }
 
-// grid = ceil(N / 4) workgroups of 64 KS threads; dynamic LDS
-// KS * 2 * 4 * 16 * quad_sb_chunks(ceil(nI / KS)) bytes, that count at most
-// 16 * kQuadSbPerLane; x, scales and biases 16-byte aligned.
+// Workgroups of W = 64 KS threads (KS a power of two).  The first full_wgs
+// run W whole quads each (wave w: quad W g + w, all of K); the rest run one
+// quad each (quad W full_wgs + g - full_wgs), K split over its W waves.
+// Dynamic LDS W * 2 * 4 * 16 * quad_sb_chunks(c) bytes, c = nI when
+// full_wgs > 0 else ceil(nI / W), that count at most 16 * kQuadSbPerLane;
+// x, scales and biases 16-byte aligned.
 template <int DT, int BITS, int GS>
 __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    uint16_t* __restrict__ out, int N, int K) {
+    uint16_t* __restrict__ out, int N, int K, int full_wgs) {
   using Q = QuadGeom<BITS, GS>;
   using T = T16<DT>;
   constexpr int D = kQuadDepth;
@@ -114,11 +122,16 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
 
   // (the K split is a power of two, so its divisions are scalar shifts)
   const int lane = threadIdx.x & 63;
-  const int lks = __builtin_ctz(blockDim.x >> 6);
+  const int lw = __builtin_ctz(blockDim.x >> 6);
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool split = (int)blockIdx.x >= full_wgs;
+  const int lks = split ? lw : 0;
   const int KS = 1 << lks;
-  const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kp = split ? wid : 0;
   const int j = lane & 3, bb = lane >> 2;
-  const int row0 = 4 * blockIdx.x;
+  const int quad = split ? (full_wgs << lw) + ((int)blockIdx.x - full_wgs)
+                         : ((int)blockIdx.x << lw) + wid;
+  const int row0 = 4 * quad;
   const int nrows = min(4, N - row0);
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const int G = K / GS;
@@ -132,7 +145,8 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   // of row r is bytes [(a_r & ~15) + 16 c, +16), at LDS row r.  Lane
   // (r = lane & 3, c = lane >> 2) loads chunks c + 16 u of row r.
   const int CH = quad_sb_chunks<BITS, GS>(nmax);
-  lds8* ls = (lds8*)qq_smem + kp * (2 * 4 * 16 * CH);
+  const int CHW = full_wgs > 0 ? quad_sb_chunks<BITS, GS>(nI) : CH;   // per-wave LDS stride
+  lds8* ls = (lds8*)qq_smem + wid * (2 * 4 * 16 * CHW);
   u32x4 sq[kQuadSbPerLane], bq[kQuadSbPerLane];
   const int cr = lane & 3, cc0 = lane >> 2;
   const int64_t crow = (int64_t)(row0 + cr) * G * 2;
@@ -317,7 +331,7 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   v += __shfl_xor(v, 8);
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
-  if (KS == 1) {
+  if (!split) {
     if (bb == 0 && j < nrows) out[row0 + j] = T::round1(v);
     return;
   }
@@ -340,6 +354,19 @@ inline int quad_ks(int64_t N, int64_t K, int bits, int cus) {
   return ks;
 }
 
+// Split of the leftover quads when one wave per quad leaves a partial round
+// (quads >= 4 cus, L = quads mod 4 cus > 0): the largest W in {2, 4} with
+// L W <= 4 cus (one split wave per SIMD at most) and at least one
+// instruction per wave; 1 when none applies.
+inline int quad_tail_split(int64_t N, int64_t K, int bits, int cus) {
+  const int64_t quads = (N + 3) / 4, S = 4 * (int64_t)cus, L = quads % S;
+  const int64_t nI = (K * bits / 8 + 255) / 256;
+  if (quads < S || L == 0) return 1;
+  int W = 1;
+  while (W < 4 && L * 2 * W <= S && nI >= 2 * W) W *= 2;
+  return W;
+}
+
 template <int DT, int BITS, int GS>
 int QuadLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s, const void* b,
                                   void* out, int64_t M, int64_t N, int64_t K, hipStream_t st,
@@ -348,8 +375,22 @@ int QuadLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* 
   if (M != 1 || !a16(x) || !a16(s) || !a16(b)) return kStatusUnsupported;
   // the scale copy addresses the whole scale array through one buffer range
   if (N * (K / GS) * 2 >= ((int64_t)1 << 31)) return kStatusUnsupported;
-  int ks = quad_ks(N, K, BITS, device_cu_count());
+  const int cus = device_cu_count();
+  int ks = quad_ks(N, K, BITS, cus);
   const int64_t nI = (K * BITS / 8 + 255) / 256;
+  if (ks == 1 && quad_sb_chunks<BITS, GS>((int)nI) <= 16 * kQuadSbPerLane) {
+    const int W = quad_tail_split(N, K, BITS, cus);
+    if (W > 1) {
+      const int64_t quads = (N + 3) / 4, L = quads % (4 * (int64_t)cus);
+      const int64_t full_wgs = (quads - L) / W;
+      const size_t lds = (size_t)W * 2 * 4 * 16 * quad_sb_chunks<BITS, GS>((int)nI);
+      hipLaunchKernelGGL((qmv_quad_kernel<DT, BITS, GS>), dim3((unsigned)(full_wgs + L)),
+                         dim3(64 * W), lds, st, (const uint16_t*)x, w, (const uint16_t*)s,
+                         (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K, (int)full_wgs);
+      ++*nlaunch;
+      return 0;
+    }
+  }
   while (ks < kQuadMaxKS &&
          quad_sb_chunks<BITS, GS>((int)((nI + ks - 1) / ks)) > 16 * kQuadSbPerLane)
     ks *= 2;
@@ -358,7 +399,7 @@ int QuadLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* 
   const size_t lds = (size_t)ks * 2 * 4 * 16 * quad_sb_chunks<BITS, GS>(nmax);
   hipLaunchKernelGGL((qmv_quad_kernel<DT, BITS, GS>), dim3((unsigned)((N + 3) / 4)),
                      dim3(64 * ks), lds, st, (const uint16_t*)x, w, (const uint16_t*)s,
-                     (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K);
+                     (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K, 0);
   ++*nlaunch;
   return 0;
 }

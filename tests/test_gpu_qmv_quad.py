@@ -71,6 +71,33 @@ def test_quad_k_splits(N, K, bits):
     _check(out[:, torch.from_numpy(cols).cuda()], ref)
 
 
+def _cus():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+@pytest.mark.parametrize("extra, K, bits", [(64, 4096, 4), (64, 2048, 8), (300, 4096, 4),
+                                            (3, 1024, 4)])
+@pytest.mark.parametrize("ragged", [0, 2])
+def test_quad_tail_split(extra, K, bits, ragged):
+    """One wave per quad over 4 x CUs SIMDs and `extra` quads more: those
+    leftover quads run split over 4 waves (extra <= CUs; K = 1024 at 4 bits
+    has 2 instructions, so 2 waves there) or 2 (300 on 256 CUs), the full
+    quads 4 or 2 to a workgroup, one wave each.  Rows of both kinds, a
+    partial last quad (ragged), the whole output against the oracle; the
+    same result on a second call; one launch."""
+    N = 4 * (4 * _cus() + extra) - ragged
+    rng = np.random.default_rng(extra + K + bits + ragged)
+    w, s, b = quantized(rng, N, K, 64, bits)
+    x = act(rng, (1, K))
+    args = (to_dev(x, "bfloat16"), to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    before = mq.launch_count()
+    out = mq.quantized_matmul(*args, bits=bits)
+    assert mq.launch_count() == before + 1
+    again = mq.quantized_matmul(*args, bits=bits)
+    np.testing.assert_array_equal(bits16(out), bits16(again))
+    _check(out, O.quantized_matmul_ref(x, w, s, b, 64, bits))
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_quad_plain_route(bits):
     """Scales of 2^100 and beyond overflow the fast dequant's s * 2^24; a wave
