@@ -37,8 +37,8 @@
 //    runs the plain float route instead, found once in the scale copy (a
 //    per-instruction check costs a branch per instruction).
 //  * The kept rows are summed in class order, then over the 16 lanes of a
-//    row in a fixed xor tree, then over the K split in wave order; one
-//    rounding.  The K split depends on (N, K, bits, group_size) and the
+//    row in a fixed tree (DPP rotations within each 16-lane row, then xor 16
+//    and 32), then over the K split in wave order; one rounding.  The K split depends on (N, K, bits, group_size) and the
 //    device's CU count only.
 //
 // Calls of 2+ rows run the 16-row skinny family (qmv.cuh): a 4 x 4 block
@@ -86,27 +86,46 @@ struct QuadGeom {
 
 // Largest K split (waves per quad).
 constexpr int kQuadMaxKS = 8;
-// 16-byte chunks of the scale copy per lane: a row's chunks <= 16 x this.
-constexpr int kQuadSbPerLane = 2;
+// 16-byte chunks of the scale copy per lane (the kernel's SB: 1 or 2): a
+// row's chunks <= 16 x SB.
+constexpr int kQuadMaxSb = 2;
 // Load instructions in flight ahead of the one computed.  Two keep the
 // kernel at 72 VGPRs (7 waves per SIMD); three and four needed 91-99 (4-5
 // waves per SIMD) and ran 0-20% slower (K=5120 N=17408, one process).
 constexpr int kQuadDepth = 2;
 
-// 16-byte chunks of one row's scale copy for ninst instructions (one more
-// than the bytes need: the copy starts at the 16-byte boundary below).
+// 16-byte chunks of one row's scale copy for ninst instructions.  The copy
+// starts at the 16-byte boundary at or below the wave's first group; it
+// needs one chunk more than the bytes unless that start is the group itself
+// for every row (tight: rows of G % 8 == 0 groups, and a wave start at a
+// 16-byte multiple of groups).
 template <int BITS, int GS>
-__host__ __device__ inline int quad_sb_chunks(int ninst) {
-  return (ninst * QuadGeom<BITS, GS>::GPI * 2 + 15) / 16 + 1;
+__host__ __device__ inline int quad_sb_chunks(int ninst, bool tight) {
+  return (ninst * QuadGeom<BITS, GS>::GPI * 2 + 15) / 16 + (tight ? 0 : 1);
 }
 
-// Workgroups of W = 64 KS threads (KS a power of two).  The first full_wgs
-// run W whole quads each (wave w: quad W g + w, all of K); the rest run one
-// quad each (quad W full_wgs + g - full_wgs), K split over its W waves.
-// Dynamic LDS W * 2 * 4 * 16 * quad_sb_chunks(c) bytes, c = nI when
-// full_wgs > 0 else ceil(nI / W), that count at most 16 * kQuadSbPerLane;
+// Whether waves of a K split over 1 << lks waves start their copies tight.
+template <int BITS, int GS>
+__host__ __device__ inline bool quad_tight(int G, int lks) {
+  return G % 8 == 0 && (lks == 0 || (QuadGeom<BITS, GS>::GPI * 2) % 16 == 0);
+}
+
+// Per-wave LDS chunk stride of a launch: nI instructions, workgroups of
+// 1 << lw waves, full_wgs > 0 when some waves run whole quads.
+template <int BITS, int GS>
+__host__ __device__ inline int quad_lds_chunks(int nI, int G, int lw, bool full) {
+  const int split = quad_sb_chunks<BITS, GS>((nI + (1 << lw) - 1) >> lw, quad_tight<BITS, GS>(G, lw));
+  if (!full) return split;
+  const int whole = quad_sb_chunks<BITS, GS>(nI, quad_tight<BITS, GS>(G, 0));
+  return whole > split ? whole : split;
+}
+
+// Workgroups of W waves (a power of two).  The first full_wgs run W whole
+// quads each (wave w: quad W g + w, all of K); the rest run one quad each
+// (quad W full_wgs + g - full_wgs), K split over its W waves.  Dynamic LDS
+// W * 2 * 4 * 16 * quad_lds_chunks(...) bytes, that count at most 16 SB;
 // x, scales and biases 16-byte aligned.
-template <int DT, int BITS, int GS>
+template <int DT, int BITS, int GS, int SB>
 __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -144,10 +163,10 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   // Row r's groups [s0 GPI, s1 GPI) start at byte a_r of the arrays; chunk c
   // of row r is bytes [(a_r & ~15) + 16 c, +16), at LDS row r.  Lane
   // (r = lane & 3, c = lane >> 2) loads chunks c + 16 u of row r.
-  const int CH = quad_sb_chunks<BITS, GS>(nmax);
-  const int CHW = full_wgs > 0 ? quad_sb_chunks<BITS, GS>(nI) : CH;   // per-wave LDS stride
+  const int CH = quad_sb_chunks<BITS, GS>(nmax, quad_tight<BITS, GS>(G, lks));
+  const int CHW = quad_lds_chunks<BITS, GS>(nI, G, lw, full_wgs > 0);   // per-wave LDS stride
   lds8* ls = (lds8*)qq_smem + wid * (2 * 4 * 16 * CHW);
-  u32x4 sq[kQuadSbPerLane], bq[kQuadSbPerLane];
+  u32x4 sq[SB], bq[SB];
   const int cr = lane & 3, cc0 = lane >> 2;
   const int64_t crow = (int64_t)(row0 + cr) * G * 2;
   const int64_t ca0 = ((crow + (int64_t)s0 * Q::GPI * 2) & ~(int64_t)15) + 16 * cc0;
@@ -156,7 +175,7 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
     const auto rs = make_rsrc(scales, sbytes);
     const auto rb = make_rsrc(biases, sbytes);
 #pragma unroll
-    for (int u = 0; u < kQuadSbPerLane; ++u) {
+    for (int u = 0; u < SB; ++u) {
       const uint32_t go = cc0 + 16 * u < CH && cr < nrows ? (uint32_t)(ca0 + 256 * u)
                                                           : 0x80000000u;
       sq[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, go, 0, 0);
@@ -228,7 +247,7 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   typedef unsigned short qq_u16x2 __attribute__((ext_vector_type(2)));
   qq_u16x2 hmax = {0, 0};
 #pragma unroll
-  for (int u = 0; u < kQuadSbPerLane; ++u) {
+  for (int u = 0; u < SB; ++u) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       hmax = __builtin_elementwise_max(hmax,
@@ -259,8 +278,6 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   f32x4 acc[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) acc[p] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // word p's MFMAs: its 8 (4-bit) or 4 (8-bit) codes against the lane's own
   // x piece, into accumulator p
@@ -268,7 +285,8 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
     acc[p] = quad_mfma<DT>(xq[0], xq[1], o[0], o[1], acc[p]);
     if constexpr (BITS == 4) acc[p] = quad_mfma<DT>(xq[2], xq[3], o[2], o[3], acc[p]);
   };
-  auto compute = [&](const u32x4& wq, const uint32_t (&xq)[XW], int t, auto plain_route) {
+  auto compute = [&](const u32x4& wq, const uint32_t (&xq)[XW], int t, auto plain_route,
+                     auto first) {
     const float sf = T::to_f32(*(const lds16*)(lsj + t * Q::GPI * 2));
     const float bf = T::to_f32(*(const lds16*)(lsj + 4 * 16 * CH + t * Q::GPI * 2));
     const GroupScale g = make_group(sf, bf);
@@ -290,7 +308,9 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
         else deq8_word<DT>(wq[p], g, o[p]);
       }
 #pragma unroll
-      for (int p = 0; p < 4; ++p) acc[p] = quad_mfma<DT>(xq[0], xq[1], o[p][0], o[p][1], acc[p]);
+      for (int p = 0; p < 4; ++p)
+        acc[p] = quad_mfma<DT>(xq[0], xq[1], o[p][0], o[p][1],
+                               decltype(first)::value ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[p]);
       if constexpr (BITS == 4) {
 #pragma unroll
         for (int p = 0; p < 4; ++p)
@@ -300,38 +320,48 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   };
 
   if (!plain) {
-    // steady state in straight-line blocks of R instructions (a branch per
-    // instruction kept the scheduler from overlapping one instruction's MFMAs
-    // with the next one's dequant), then the last n % R, whose loads are
-    // all past the range
-    int t = 0;
+    // instruction 0 (every wave has one) starts the accumulators from its
+    // products; then the steady state in straight-line blocks of R
+    // instructions (a branch per instruction kept the scheduler from
+    // overlapping one instruction's MFMAs with the next one's dequant), then
+    // the last ones, whose further loads are all past the range
+    issue(D % R, D);
+    compute(wv[0], xv[0], 0, std::false_type{}, std::true_type{});
+    int t = 1;
     for (; t + R <= n; t += R) {
 #pragma unroll
       for (int i = 0; i < R; ++i) {
-        issue((i + D) % R, t + i + D);
-        compute(wv[i], xv[i], t + i, std::false_type{});
+        issue((1 + i + D) % R, t + i + D);
+        compute(wv[(1 + i) % R], xv[(1 + i) % R], t + i, std::false_type{}, std::false_type{});
       }
     }
 #pragma unroll
     for (int i = 0; i < R - 1; ++i)
-      if (t + i < n) compute(wv[i], xv[i], t + i, std::false_type{});
+      if (t + i < n)
+        compute(wv[(1 + i) % R], xv[(1 + i) % R], t + i, std::false_type{}, std::false_type{});
   } else {
     // the plain route (|s| >= 2^100 in this wave's scales, never in real
     // checkpoints): one instruction at a time, the ring's loads discarded,
     // so it adds no registers to the kernel
+#pragma unroll
+    for (int p = 0; p < 4; ++p) acc[p] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int t = 0; t < n; ++t) {
       issue(0, t);
-      compute(wv[0], xv[0], t, std::true_type{});
+      compute(wv[0], xv[0], t, std::true_type{}, std::false_type{});
     }
   }
 
   // ---- kept rows in class order, xor tree over the row's 16 lanes ---------
   float v = acc[0][0] + acc[1][1] + acc[2][2] + acc[3][3];
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
+  // lanes 16 r + 4 b + j, b = 0..3: rotate by one and by two b within the
+  // row of 16 (DPP row_ror 4, 8), then across the rows
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0x124, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0x128, 0xf, 0xf, false));
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
-  if (!split) {
+  if (KS == 1) {
     if (bb == 0 && j < nrows) out[row0 + j] = T::round1(v);
     return;
   }
@@ -376,30 +406,34 @@ int QuadLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* 
   // the scale copy addresses the whole scale array through one buffer range
   if (N * (K / GS) * 2 >= ((int64_t)1 << 31)) return kStatusUnsupported;
   const int cus = device_cu_count();
-  int ks = quad_ks(N, K, BITS, cus);
-  const int64_t nI = (K * BITS / 8 + 255) / 256;
-  if (ks == 1 && quad_sb_chunks<BITS, GS>((int)nI) <= 16 * kQuadSbPerLane) {
-    const int W = quad_tail_split(N, K, BITS, cus);
-    if (W > 1) {
-      const int64_t quads = (N + 3) / 4, L = quads % (4 * (int64_t)cus);
-      const int64_t full_wgs = (quads - L) / W;
-      const size_t lds = (size_t)W * 2 * 4 * 16 * quad_sb_chunks<BITS, GS>((int)nI);
-      hipLaunchKernelGGL((qmv_quad_kernel<DT, BITS, GS>), dim3((unsigned)(full_wgs + L)),
-                         dim3(64 * W), lds, st, (const uint16_t*)x, w, (const uint16_t*)s,
-                         (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K, (int)full_wgs);
-      ++*nlaunch;
-      return 0;
+  const int G = (int)(K / GS);
+  const int nI = (int)((K * BITS / 8 + 255) / 256);
+  const int64_t quads = (N + 3) / 4;
+  int W = quad_ks(N, K, BITS, cus);
+  int64_t full_wgs = 0, wgs = quads;
+  if (W == 1 && quad_lds_chunks<BITS, GS>(nI, G, 0, false) <= 16 * kQuadMaxSb) {
+    const int Wt = quad_tail_split(N, K, BITS, cus);
+    if (Wt > 1) {
+      const int64_t L = quads % (4 * (int64_t)cus);
+      W = Wt;
+      full_wgs = (quads - L) / W;
+      wgs = full_wgs + L;
     }
   }
-  while (ks < kQuadMaxKS &&
-         quad_sb_chunks<BITS, GS>((int)((nI + ks - 1) / ks)) > 16 * kQuadSbPerLane)
-    ks *= 2;
-  const int nmax = (int)((nI + ks - 1) / ks);
-  if (quad_sb_chunks<BITS, GS>(nmax) > 16 * kQuadSbPerLane) return kStatusUnsupported;
-  const size_t lds = (size_t)ks * 2 * 4 * 16 * quad_sb_chunks<BITS, GS>(nmax);
-  hipLaunchKernelGGL((qmv_quad_kernel<DT, BITS, GS>), dim3((unsigned)((N + 3) / 4)),
-                     dim3(64 * ks), lds, st, (const uint16_t*)x, w, (const uint16_t*)s,
-                     (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K, 0);
+  const int lw = __builtin_ctz(W);
+  int CHW = quad_lds_chunks<BITS, GS>(nI, G, lw, full_wgs > 0);
+  if (full_wgs == 0) {
+    while (W < kQuadMaxKS && CHW > 16 * kQuadMaxSb) {
+      W *= 2;
+      CHW = quad_lds_chunks<BITS, GS>(nI, G, __builtin_ctz(W), false);
+    }
+  }
+  if (CHW > 16 * kQuadMaxSb) return kStatusUnsupported;
+  const size_t lds = (size_t)W * 2 * 4 * 16 * CHW;
+  auto kern = CHW <= 16 ? qmv_quad_kernel<DT, BITS, GS, 1> : qmv_quad_kernel<DT, BITS, GS, 2>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * W), lds, st, (const uint16_t*)x, w,
+                     (const uint16_t*)s, (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K,
+                     (int)full_wgs);
   ++*nlaunch;
   return 0;
 }
