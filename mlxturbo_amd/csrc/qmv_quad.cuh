@@ -123,9 +123,10 @@ __host__ __device__ inline int quad_lds_chunks(int nI, int G, int lw, bool full)
 // Workgroups of W waves (a power of two).  The first full_wgs run W whole
 // quads each (wave w: quad W g + w, all of K); the rest run one quad each
 // (quad W full_wgs + g - full_wgs), K split over its W waves.  Dynamic LDS
-// W * 2 * 4 * 16 * quad_lds_chunks(...) bytes, that count at most 16 SB;
-// x, scales and biases 16-byte aligned.
-template <int DT, int BITS, int GS, int SB>
+// W * 2 KB * SB (scales and biases of 4 rows x 16 SB chunks per wave; every
+// lane stores its chunks, zeros past the copy); the copy of a wave at most
+// 16 SB chunks per row; x, scales and biases 16-byte aligned.
+template <int DT, int BITS, int GS, int SB, bool LATE>
 __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -162,43 +163,31 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   // ---- scale / bias copy of the wave's groups: the loads -----------------
   // Row r's groups [s0 GPI, s1 GPI) start at byte a_r of the arrays; chunk c
   // of row r is bytes [(a_r & ~15) + 16 c, +16), at LDS row r.  Lane
-  // (r = lane & 3, c = lane >> 2) loads chunks c + 16 u of row r.
+  // (r = lane & 3, c = lane >> 2) loads chunks c + 16 u of row r (zeros
+  // past the CH chunks of the copy) and stores them unconditionally: a
+  // store under a branch let the compiler sink that lane's load into the
+  // branch, behind the weight loads.
   const int CH = quad_sb_chunks<BITS, GS>(nmax, quad_tight<BITS, GS>(G, lks));
-  const int CHW = quad_lds_chunks<BITS, GS>(nI, G, lw, full_wgs > 0);   // per-wave LDS stride
-  lds8* ls = (lds8*)qq_smem + wid * (2 * 4 * 16 * CHW);
+  constexpr int CS = 16 * SB;                      // LDS chunks per row (every lane stores)
+  lds8* ls = (lds8*)qq_smem + wid * (2 * 4 * 16 * CS);
   u32x4 sq[SB], bq[SB];
   const int cr = lane & 3, cc0 = lane >> 2;
   const int64_t crow = (int64_t)(row0 + cr) * G * 2;
   const int64_t ca0 = ((crow + (int64_t)s0 * Q::GPI * 2) & ~(int64_t)15) + 16 * cc0;
-  {
-    const uint32_t sbytes = (uint32_t)((int64_t)N * G * 2);
-    const auto rs = make_rsrc(scales, sbytes);
-    const auto rb = make_rsrc(biases, sbytes);
+  const uint32_t sbytes = (uint32_t)((int64_t)N * G * 2);
+  const auto rs = make_rsrc(scales, sbytes);
+  const auto rb = make_rsrc(biases, sbytes);
+  uint32_t go[SB];
 #pragma unroll
-    for (int u = 0; u < SB; ++u) {
-      const uint32_t go = cc0 + 16 * u < CH && cr < nrows ? (uint32_t)(ca0 + 256 * u)
-                                                          : 0x80000000u;
-      sq[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, go, 0, 0);
-      bq[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, go, 0, 0);
-      // a chunk across the end of the arrays (their size not a multiple of
-      // 16 bytes) would read zeros where it crosses the range: read its
-      // entries one by one
-      if (go < sbytes && go + 16 > sbytes) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t o = go + 4 * e;
-          sq[u][e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0) |
-                     ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o + 2, 0, 0) << 16);
-          bq[u][e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, o, 0, 0) |
-                     ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, o + 2, 0, 0) << 16);
-        }
-      }
-    }
+  for (int u = 0; u < SB; ++u) {
+    go[u] = cc0 + 16 * u < CH && cr < nrows ? (uint32_t)(ca0 + 256 * u) : 0x80000000u;
+    sq[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, go[u], 0, 0);
+    bq[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, go[u], 0, 0);
   }
   // this lane's scale at instruction s0: row j, group s0 GPI + gb
   const int gb = 16 * bb * (8 / BITS) / GS;
   const int64_t aj = ((int64_t)(row0 + j) * G + (int64_t)s0 * Q::GPI) * 2;
-  const lds8* lsj = ls + j * 16 * CH + (int)(aj & 15) + 2 * gb;
+  const lds8* lsj = ls + j * 16 * CS + (int)(aj & 15) + 2 * gb;
 
   // ---- loads: weights (4 rows x 256 B) and the x slab per instruction -----
   // A ring of R = D + 1 slots: instruction t + D is issued into the slot
@@ -234,40 +223,66 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
       xv[slot][1] = v[1];
     }
   };
+  // LATE: the first weight loads wait for the scale copy (launches of long
+  // waves: K=17408 N=5120, 9 instructions a wave, 12.8 against 13.2 us);
+  // else they go out with it (2-3 instructions a wave: 4.9 against 5.1 us
+  // at K=4096 N=4096)
+  if constexpr (!LATE) {
 #pragma unroll
-  for (int i = 0; i < D; ++i) issue(i, i);
+    for (int i = 0; i < D; ++i) issue(i, i);
+  }
 
-  // ---- the scale copy lands in LDS behind the weight prologue -------------
+  // ---- the scale copy lands in LDS --------------------------------------
   // Entries past the row (groups >= G: the ragged last instruction) are
   // stored as zeros, so a lane whose piece lies past K dequantizes zeros;
-  // only a row's last chunk holds any.  The big-scale check (a packed 16-bit
-  // max over every loaded chunk) also keeps the compiler from sinking the
-  // loads into the stores' branch; a big scale of a neighbouring row only
-  // costs the wave the plain route.
+  // only a row's last chunk holds any.  The big-scale check is a packed
+  // 16-bit max over every stored chunk; a big scale of a neighbouring row
+  // only costs the wave the plain route.
   typedef unsigned short qq_u16x2 __attribute__((ext_vector_type(2)));
   qq_u16x2 hmax = {0, 0};
-#pragma unroll
-  for (int u = 0; u < SB; ++u) {
+  // chunk u's entries past the row zeroed, into LDS, into the big check
+  auto put = [&](int u, u32x4 sv, u32x4 bv) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      hmax = __builtin_elementwise_max(hmax,
-                                       __builtin_bit_cast(qq_u16x2, sq[u][e] & 0x7fff7fffu));
-    const int cc = cc0 + 16 * u;
-    if (cc < CH) {
-      const int g0c = (int)((ca0 + 256 * u - crow) >> 1);   // group of the chunk's entry 0
-      u32x4 sv = sq[u], bv = bq[u];
-      if (g0c + 8 > G) {
+      hmax = __builtin_elementwise_max(hmax, __builtin_bit_cast(qq_u16x2, sv[e] & 0x7fff7fffu));
+    const int g0c = (int)((ca0 + 256 * u - crow) >> 1);   // group of the chunk's entry 0
+    if (g0c + 8 > G) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t keep = (g0c + 2 * e < G ? 0x0000ffffu : 0u) |
-                                (g0c + 2 * e + 1 < G ? 0xffff0000u : 0u);
-          sv[e] &= keep;
-          bv[e] &= keep;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t keep = (g0c + 2 * e < G ? 0x0000ffffu : 0u) |
+                              (g0c + 2 * e + 1 < G ? 0xffff0000u : 0u);
+        sv[e] &= keep;
+        bv[e] &= keep;
       }
-      *(lds_u32x4*)(ls + cr * 16 * CH + 16 * cc) = sv;
-      *(lds_u32x4*)(ls + 4 * 16 * CH + cr * 16 * CH + 16 * cc) = bv;
     }
+    const int cc = cc0 + 16 * u;
+    *(lds_u32x4*)(ls + cr * 16 * CS + 16 * cc) = sv;
+    *(lds_u32x4*)(ls + 4 * 16 * CS + cr * 16 * CS + 16 * cc) = bv;
+  };
+#pragma unroll
+  for (int u = 0; u < SB; ++u) put(u, sq[u], bq[u]);
+  // the one chunk across the end of the arrays (their size not a multiple
+  // of 16 bytes) read zeros where it crosses the range: its lane reads the
+  // entries one by one and stores the chunk again (after the plain stores,
+  // so no copy load waits behind this branch)
+#pragma unroll
+  for (int u = 0; u < SB; ++u) {
+    if (go[u] < sbytes && go[u] + 16 > sbytes) {
+      u32x4 sv, bv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t o = go[u] + 4 * e;
+        sv[e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0) |
+                ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o + 2, 0, 0) << 16);
+        bv[e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, o, 0, 0) |
+                ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, o + 2, 0, 0) << 16);
+      }
+      put(u, sv, bv);
+    }
+  }
+  if constexpr (LATE) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(i, i);
   }
   const uint32_t hm = hmax[0] > hmax[1] ? hmax[0] : hmax[1];
   const bool big = DT == kBF16 ? hm >= 0x7180u : hm >= 0x7c00u;   // bf16 2^100 / f16 inf
@@ -288,7 +303,7 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   auto compute = [&](const u32x4& wq, const uint32_t (&xq)[XW], int t, auto plain_route,
                      auto first) {
     const float sf = T::to_f32(*(const lds16*)(lsj + t * Q::GPI * 2));
-    const float bf = T::to_f32(*(const lds16*)(lsj + 4 * 16 * CH + t * Q::GPI * 2));
+    const float bf = T::to_f32(*(const lds16*)(lsj + 4 * 16 * CS + t * Q::GPI * 2));
     const GroupScale g = make_group(sf, bf);
     if constexpr (decltype(plain_route)::value) {
       // one word at a time, so the route's float codes add no registers
@@ -429,8 +444,13 @@ int QuadLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* 
     }
   }
   if (CHW > 16 * kQuadMaxSb) return kStatusUnsupported;
-  const size_t lds = (size_t)W * 2 * 4 * 16 * CHW;
-  auto kern = CHW <= 16 ? qmv_quad_kernel<DT, BITS, GS, 1> : qmv_quad_kernel<DT, BITS, GS, 2>;
+  const int SBn = CHW <= 16 ? 1 : 2;
+  const size_t lds = (size_t)W * 2 * 4 * 16 * 16 * SBn;
+  const bool late = (full_wgs > 0 ? nI : (nI + W - 1) / W) >= 4;
+  auto kern = SBn == 1 ? (late ? qmv_quad_kernel<DT, BITS, GS, 1, true>
+                               : qmv_quad_kernel<DT, BITS, GS, 1, false>)
+                       : (late ? qmv_quad_kernel<DT, BITS, GS, 2, true>
+                               : qmv_quad_kernel<DT, BITS, GS, 2, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * W), lds, st, (const uint16_t*)x, w,
                      (const uint16_t*)s, (const uint16_t*)b, (uint16_t*)out, (int)N, (int)K,
                      (int)full_wgs);
