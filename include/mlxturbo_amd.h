@@ -54,6 +54,21 @@ const char* mq_last_error(void);
 uint64_t mq_launch_count(void);
 
 /*
+ * Row identity across call widths (process-wide, default 0).  One-row
+ * calls (M = 1) normally run their own kernel, whose sums are rounded in a
+ * different order from the 2..32-row kernels': each row is within the
+ * output tolerance of both, not bit-identical to the same row computed in
+ * a wider call.  With on != 0, one-row calls run the 2..32-row kernel
+ * family, so a row's result does not depend on how many rows the call has
+ * (decode vs. speculative verify).  The reference keeps this property with
+ * its opt-in small-M route: rows of an M = 2..8 call bit-identical to the
+ * M = 1 call (kernels/qmv_small_m.py:289-307, dispatch.py:337-347).
+ * Returns the previous setting.  Not for calls running concurrently with a
+ * change of the setting.
+ */
+int mq_set_row_identity(int on);
+
+/*
  * out[N, K] (T) = dequantize(w, scales, biases).
  * Replaces mx.dequantize(w, scales, biases, group_size, bits, mode="affine"),
  * the format definer the reference's fp32 references call

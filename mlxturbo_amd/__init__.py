@@ -25,12 +25,13 @@ layers to another width (dequantize + quantize on the GPU).
 
 from . import checkpoint, dispatch, nn, rebit
 from .ops import (dequantize, gather_glu, gather_qmm, gather_qmm_combine, launch_count,
-                  moe_combine, moe_route, quantize, quantized_matmul)
+                  moe_combine, moe_route, quantize, quantized_matmul, row_identity,
+                  set_row_identity)
 
 __version__ = "0.2.0"
 
 __all__ = ["checkpoint", "rebit", "dequantize", "dispatch", "gather_glu", "gather_qmm",
            "gather_qmm_combine", "launch_count",
            "moe_combine", "moe_route",
-           "nn", "quantize", "quantized_matmul",
+           "nn", "quantize", "quantized_matmul", "row_identity", "set_row_identity",
            "__version__"]

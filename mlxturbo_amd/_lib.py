@@ -26,6 +26,7 @@ EXPORTED = (
     "mq_version",
     "mq_last_error",
     "mq_launch_count",
+    "mq_set_row_identity",
     "mq_dequantize",
     "mq_quantize",
     "mq_quantized_matmul",
@@ -60,6 +61,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_last_error.argtypes = []
     lib.mq_launch_count.restype = ctypes.c_uint64
     lib.mq_launch_count.argtypes = []
+    lib.mq_set_row_identity.restype = _int
+    lib.mq_set_row_identity.argtypes = [_int]
     lib.mq_dequantize.restype = _int
     lib.mq_dequantize.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]
     lib.mq_quantize.restype = _int

@@ -16,6 +16,8 @@ namespace {
 
 thread_local std::string g_last_error;
 std::atomic<uint64_t> g_launches{0};
+// one-row calls on the 2..32-row kernel family (mq_set_row_identity)
+std::atomic<int> g_row_identity{0};
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -145,11 +147,13 @@ int moe_combine_checked(const void* y, int64_t y_rows, const int32_t* inv, const
 
 extern "C" {
 
-int mq_version(void) { return 4; }
+int mq_version(void) { return 5; }
 
 const char* mq_last_error(void) { return g_last_error.c_str(); }
 
 uint64_t mq_launch_count(void) { return g_launches.load(std::memory_order_relaxed); }
+
+int mq_set_row_identity(int on) { return g_row_identity.exchange(on != 0 ? 1 : 0); }
 
 int mq_dequantize(const uint32_t* w, const void* scales, const void* biases, void* out,
                   int64_t N, int64_t K, int group_size, int bits, int dtype, void* hip_stream) {
@@ -238,7 +242,7 @@ int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
     return MQ_OK;
   }
   int nl = 0;
-  if (M == 1) {
+  if (M == 1 && !g_row_identity.load(std::memory_order_relaxed)) {
     rc = dispatch_16<mq::QuadLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
                                      st, &nl);
     if (rc == 0) {

@@ -27,6 +27,7 @@ bit-exact dequantize plus one GPU GEMM.  Nothing runs on the CPU.
 
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Optional, Sequence
 
@@ -831,6 +832,29 @@ def launch_count() -> int:
     return _lib.launch_count()
 
 
+def set_row_identity(on: bool) -> bool:
+    """Run one-row ``quantized_matmul`` calls on the 2..32-row kernel family,
+    so every output row is bit-identical whatever the number of rows in the
+    call (a decode step and a speculative verify of the same token agree bit
+    for bit).  Off by default: one-row calls then take their own faster
+    kernel, within the output tolerance of the wide rows but rounded in
+    another order.  The reference's counterpart is its opt-in small-M route,
+    whose rows of 2..8-row calls are bit-identical to the one-row call
+    (kernels/qmv_small_m.py:289-307, dispatch.py:337-347).  Process-wide;
+    returns the previous setting."""
+    return bool(_lib.lib().mq_set_row_identity(1 if on else 0))
+
+
+@contextlib.contextmanager
+def row_identity(on: bool = True):
+    """``set_row_identity(on)`` for the ``with`` block, restored after."""
+    prev = set_row_identity(on)
+    try:
+        yield
+    finally:
+        set_row_identity(prev)
+
+
 __all__: Sequence[str] = ("quantize", "dequantize", "quantized_matmul", "quantized_matmul_prepared",
                           "PreparedWeights", "gather_qmm", "gather_glu", "moe_combine",
-                          "launch_count")
+                          "launch_count", "set_row_identity", "row_identity")

@@ -170,6 +170,35 @@ def test_qmm_rows_bit_identical_across_widths():
     _check(mq.quantized_matmul(xd, *args), ref)
 
 
+@pytest.mark.parametrize("N, K, bits", [(17408, 5120, 4), (5120, 17408, 4), (2048, 4096, 8),
+                                        (1001, 4224, 4)])
+def test_row_identity_switch(N, K, bits):
+    """With mq.row_identity() one-row calls run the 2..32-row family: every
+    row of a 1-, 2-, 5- or 16-row call is then bit-identical (decode equal to
+    verify bit for bit, the reference's opt-in small-M guarantee,
+    kernels/qmv_small_m.py:289-307).  Outside the block one-row calls are back
+    on their own kernel (still within the oracle's tolerance) and the
+    setting is restored."""
+    rng = np.random.default_rng(N + K + bits)
+    w, s, b = random_packed(rng, N, K, 64, bits)
+    x = act(rng, (16, K), scale=0.1)
+    args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    xd = to_dev(x, "bfloat16")
+    full = bits16(mq.quantized_matmul(xd, *args, bits=bits))
+    with mq.row_identity():
+        for v in (0, 5, 15):
+            one = bits16(mq.quantized_matmul(xd[v:v + 1], *args, bits=bits))
+            np.testing.assert_array_equal(one, full[v:v + 1])
+        for M in (2, 5):
+            np.testing.assert_array_equal(bits16(mq.quantized_matmul(xd[:M], *args, bits=bits)),
+                                          full[:M])
+    assert mq.set_row_identity(False) is False
+    cols = np.unique(np.concatenate([np.arange(min(N, 64)), rng.choice(N, min(N, 64), False)]))
+    one = mq.quantized_matmul(xd[3:4], *args, bits=bits)
+    _check(one[:, torch.from_numpy(cols).cuda()],
+           O.quantized_matmul_ref(x[3:4], w[cols], s[cols], b[cols], 64, bits))
+
+
 def _qmm_abi(xd, wd, sd, bd, M, N, K, gs=64, bits=4):
     """One mq_quantized_matmul call through the C ABI (operand pointers as
     given, so a caller can pass unaligned scale views)."""
