@@ -17,10 +17,12 @@ Mirrors mlxturbo/kernels/dispatch.py on torch modules:
 
 On MI355X every route is a HIP kernel of this library: ``stock`` is
 :func:`mlxturbo_amd.quantized_matmul` with the library's own width choice
-(skinny streaming kernel up to 16 rows, MFMA tile kernel above);
-``skinny`` and ``wide`` name those two kernels.  The measured crossover is
-the library's: at K=5120, N=17408 one skinny launch of 16 rows costs ~40 us
-while the MFMA tile kernel does 512 rows in ~120 us.
+(the one-row quad kernel, the skinny streaming kernel for 2..32 rows, and
+above that 32- or 16-row skinny launches or the MFMA tile kernel, whichever
+the library's per-geometry cost model prices lower); ``skinny`` and
+``wide`` name the two families.  At K=5120, N=17408 one skinny launch of
+16 rows costs ~21 us and of 32 rows ~23 us, while the MFMA tile kernel does
+96 rows in ~53 us and 512 rows in ~112 us.
 """
 
 from __future__ import annotations
