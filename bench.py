@@ -70,6 +70,8 @@ def parse():
                         "(configs[1] skinny), combine (MoE combine, 2048 x top-8 x 2048), "
                         "gather_prefill_<proj>_<routing> (2048 tokens), "
                         "moe_layer_<routing>_T<T> (whole decode MoE layer), "
+                        "moe_layer_prefill_<routing>[_sortpath] (whole prefill MoE layer, "
+                        "2048 tokens), "
                         "route<T> (MoE routing + shared gate), "
                         "mfma_ceiling (the measured bf16 MFMA ceiling and its clock)")
     return p.parse_args()
@@ -102,6 +104,12 @@ def run_case(torch, mq, case: str) -> dict:
         return {"case": case, **measure_gather_prefill(torch, mq, 2048, NN, KK, routing, 20, 3)}
     if case.startswith("route"):
         return {"case": case, **measure_route(torch, mq, int(case[len("route"):] or 1), 100, 5)}
+    if case.startswith("moe_layer_prefill_"):
+        routing = case[len("moe_layer_prefill_"):]
+        sort = routing.endswith("_sortpath")
+        routing = routing[:-len("_sortpath")] if sort else routing
+        return {"case": case, **measure_moe_layer_prefill(torch, mq, 2048, routing, 20, 3,
+                                                          tables=not sort)}
     if case.startswith("moe_layer_"):
         routing, t = case[len("moe_layer_"):].rsplit("_T", 1)
         return {"case": case, **measure_moe_layer(torch, mq, int(t), routing, 100, 5)}
@@ -305,6 +313,57 @@ def measure_moe_layer(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidd
     return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
             "distinct_experts": round(sum(len(np.unique(r)) for r in routes) / nroute, 1),
             "launches": int(launches)}
+
+
+def measure_moe_layer_prefill(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidden=2048,
+                              inter=512, nroute=4, seed=9, tables=True):
+    """One whole prefill MoE layer of configs[3] (SwitchGLU with router
+    scores over T tokens x top_k experts): the segment tables built once and
+    shared by the gate, up and down gathers (x read through each pair's
+    token), one SwiGLU pass, one combine -- the reference's prefill path
+    (fused.py:3283-3316).  tables=False times the sort path instead (two
+    argsorts, the gathered x, three table builds, torch's SwiGLU, the
+    combine through the inverse permutation).  Reported as dense-equivalent
+    TFLOP/s of the three projections (2 P (2 inter hidden + hidden inter))
+    and HBM GB/s of the algorithmic bytes (every expert's weights once plus
+    activations); "launches" counts library kernels."""
+    from mlxturbo_amd import nn as mqnn
+    rng = np.random.default_rng(seed + T)
+    routes = [(zipf_routing(rng, T, top_k, E) if routing == "zipf" else
+               np.stack([rng.choice(E, size=top_k, replace=False) for _ in range(T)]).astype(np.int32))
+              for _ in range(nroute)]
+
+    def bank(N, K, s):
+        (w, sc, b), = make_weights(torch, E * N, K, 1, seed=s)
+        return mqnn.QuantizedSwitchLinear(w.view(E, N, -1), sc.view(E, N, -1), b.view(E, N, -1))
+
+    layer = mqnn.SwitchGLU(bank(inter, hidden, seed), bank(inter, hidden, seed + 1),
+                           bank(hidden, inter, seed + 2), prefill_tables=tables)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((T, hidden), device="cuda", generator=g).to(torch.bfloat16)
+    scores = torch.softmax(torch.randn((T, top_k), device="cuda", generator=g), -1)
+    idx = [torch.from_numpy(r).cuda() for r in routes]
+    P = T * top_k
+
+    def per_expert(N, K):
+        return N * K // 2 + 4 * N * (K // 64)
+
+    nbytes = (E * (2 * per_expert(inter, hidden) + per_expert(hidden, inter)) + 2 * T * hidden * 2
+              + 2 * P * inter * 2 * 3 + 2 * P * hidden + 4 * P)
+    flops = 2.0 * P * (2 * inter * hidden + hidden * inter)
+
+    def fn(i):
+        layer(x, idx[i % nroute], scores)
+
+    n0 = mq.launch_count()
+    fn(0)
+    launches = mq.launch_count() - n0
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    del layer
+    torch.cuda.empty_cache()
+    return {"us": round(per_step * 1e6, 2), "TFLOPs": round(flops / per_step / 1e12, 1),
+            "GBps": round(nbytes / per_step / 1e9, 1), "launches": int(launches)}
 
 
 def measure_gather_prefill(torch, mq, T, N, K, routing, steps, warmup, E=512, top_k=8, seed=5):
@@ -714,6 +773,12 @@ def main():
             for name, (NN, KK) in (("gate_up", (1024, 2048)), ("down", (2048, 512))):
                 sweep[f"gather_prefill_{name}_{routing}_T2048"] = measure_gather_prefill(
                     torch, mq, 2048, NN, KK, routing, 20, 3)
+            # the whole prefill layer (tables shared by its three gathers),
+            # and the sort path it replaces
+            sweep[f"moe_layer_prefill_{routing}_T2048"] = measure_moe_layer_prefill(
+                torch, mq, 2048, routing, 20, 3)
+            sweep[f"moe_layer_prefill_{routing}_T2048_sortpath"] = measure_moe_layer_prefill(
+                torch, mq, 2048, routing, 20, 3, tables=False)
         sweep["moe_combine_T2048_k8_N2048"] = measure_combine(torch, mq, 2048, 8, 2048, 50, 3)
         sweep["dequant_b4_K5120_N17408"] = measure_dequant(torch, mq, N, K, 50, 3)
 

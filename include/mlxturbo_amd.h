@@ -187,6 +187,47 @@ int mq_gather_qmm_noalloc(const void* x, const uint32_t* w, const void* scales,
                           int sorted_indices, void* hip_stream);
 
 /*
+ * Segment tables of a MoE layer's prefill gathers, built once for a routing
+ * and reused by every gather of the layer over it: the reference builds them
+ * once per layer (`tables = _moe_gemm_tables(idx_s, E)`, fused.py:3290) and
+ * passes them to the up, gate and down grouped GEMMs (fused.py:3294-3316,
+ * kernels/moe_grouped_gemm.py:913-1066).  Pairs as for mq_gather_qmm
+ * (lhs_indices NULL: pair p's x batch is p / (P / B)); rows M per pair.
+ * tables must hold mq_gather_qmm_workspace_size(P, M) bytes and stay
+ * untouched until the last mq_gather_qmm_tables call using them has run.
+ * Prefill widths only (P * M >= 1024, E <= 2048, M <= 16), else
+ * MQ_EUNSUPPORTED.  Enqueues two kernels.
+ */
+int mq_gather_tables(const int32_t* lhs_indices, const int32_t* rhs_indices, int64_t P,
+                     int64_t B, int64_t M, int64_t E, void* tables, size_t tables_bytes,
+                     void* hip_stream);
+
+/*
+ * mq_gather_qmm over tables from mq_gather_tables for the same rhs_indices,
+ * lhs_indices validity (NULL, or the same table), P, M and E; x, B, N, K
+ * and the bank may differ from the call that built them (a layer's gate /
+ * up bank over the tokens, its down bank over the SwiGLU rows, B = P).
+ * Results are those of mq_gather_qmm, bit for bit.  Runs the thin grouped
+ * kernel only: calls that mq_gather_qmm would run on another kernel (more
+ * than 96 rows per expert, K > 2048) return MQ_EUNSUPPORTED, and the caller
+ * runs mq_gather_qmm.
+ */
+int mq_gather_qmm_tables(const void* x, const uint32_t* w, const void* scales,
+                         const void* biases, const int32_t* lhs_indices,
+                         const int32_t* rhs_indices, void* out, int64_t P, int64_t B, int64_t M,
+                         int64_t N, int64_t K, int64_t E, int group_size, int bits, int dtype,
+                         const void* tables, size_t tables_bytes, void* hip_stream);
+
+/*
+ * out[i] = T(T(silu(gate[i])) * up[i]) for i < n, silu(g) = g / (1 + exp(-g))
+ * in float, dtype bf16 or fp16: mlx-lm SwitchGLU's activation between the
+ * gate / up and down gathers (`act = switch_mlp.activation(x_up, x_gate)` in
+ * the reference's prefill path, fused.py:3302), one pass.
+ */
+int mq_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
+              void* hip_stream);
+
+/*
  * Fused MoE gate+up+SiLU at decode / verify widths:
  *   out[p, M, N] = silu(x[lhs[p]] . dequantize(w_gate[rhs[p]])^T)
  *                * (x[lhs[p]] . dequantize(w_up[rhs[p]])^T)

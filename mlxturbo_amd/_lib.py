@@ -35,6 +35,9 @@ EXPORTED = (
     "mq_gather_qmm_workspace_size",
     "mq_gather_qmm",
     "mq_gather_qmm_noalloc",
+    "mq_gather_tables",
+    "mq_gather_qmm_tables",
+    "mq_swiglu",
     "mq_gather_glu",
     "mq_gather_qmm_combine",
     "mq_moe_combine",
@@ -48,6 +51,7 @@ _lib = None
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
+_sz = ctypes.c_size_t
 
 
 class LibraryMissing(RuntimeError):
@@ -83,6 +87,13 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_gather_qmm_noalloc.restype = _int
     lib.mq_gather_qmm_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _int, _int, _int, _int, _vp]
+    lib.mq_gather_tables.restype = _int
+    lib.mq_gather_tables.argtypes = [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]
+    lib.mq_gather_qmm_tables.restype = _int
+    lib.mq_gather_qmm_tables.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                         _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]
+    lib.mq_swiglu.restype = _int
+    lib.mq_swiglu.argtypes = [_vp, _vp, _vp, _i64, _int, _vp]
     lib.mq_moe_combine_shared.restype = _int
     lib.mq_moe_combine_shared.argtypes = [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                           _int, _vp]

@@ -44,7 +44,8 @@ def hipcc() -> str:
 
 
 # (source, extra defines) of each translation unit
-UNITS = [("abi.hip", []), ("formats.hip", []), ("prep.hip", []), ("route.hip", [])] + [
+UNITS = [("abi.hip", []), ("formats.hip", []), ("prep.hip", []), ("route.hip", []),
+         ("swiglu.hip", [])] + [
     ("inst.hip", [f"-DMQ_INST_DT={dt}", f"-DMQ_INST_BITS={bits}"] + glu)
     for glu in ([], ["-DMQ_INST_GLU"]) for dt in (0, 1) for bits in (4, 8)
 ] + [

@@ -308,12 +308,91 @@ int mq_gather_qmm(const void* x, const uint32_t* w, const void* scales, const vo
   int nl = 0;
   (void)sorted_indices;  // segments are discovered either way; sortedness only orders them
   rc = dispatch_16<mq::GatherLaunch>(dtype, bits, group_size, x, w, scales, biases, lhs_indices,
-                                     rhs_indices, out, P, B, M, N, K, E, workspace, st, &nl);
+                                     rhs_indices, out, P, B, M, N, K, E, workspace, false, st,
+                                     &nl);
   if (rc) return fail(rc, "gather_qmm: no kernel for this configuration");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail((int)e, "gather_qmm: launch failed: %s", hipGetErrorString(e));
   g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
   return MQ_OK;
+}
+
+int mq_gather_tables(const int32_t* lhs_indices, const int32_t* rhs_indices, int64_t P,
+                     int64_t B, int64_t M, int64_t E, void* tables, size_t tables_bytes,
+                     void* hip_stream) {
+  if (!rhs_indices) return fail(MQ_EINVAL, "rhs_indices must be non-null");
+  if (P < 1 || M < 1 || E < 1 || B < 1)
+    return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
+                (long long)M, (long long)E, (long long)B);
+  if (!lhs_indices && P % B)
+    return fail(MQ_EINVAL, "lhs_indices=NULL requires B to divide P (B=%lld P=%lld)",
+                (long long)B, (long long)P);
+  if (P > INT32_MAX || P * M < mq::kGroupedMinRows || E > mq::kGatherPrepMaxE || M > 16)
+    return fail(MQ_EUNSUPPORTED,
+                "gather tables are built for prefill widths (P * M >= %lld output rows, "
+                "E <= %d, M <= 16; got P=%lld M=%lld E=%lld)",
+                (long long)mq::kGroupedMinRows, mq::kGatherPrepMaxE, (long long)P, (long long)M,
+                (long long)E);
+  const size_t need = mq::gather_workspace_bytes(P, M);
+  if (!tables || tables_bytes < need)
+    return fail(MQ_EINVAL, "tables too small: need %zu bytes", need);
+  const int rc = mq::launch_thin_tables(rhs_indices, lhs_indices, P, E, B, M, tables,
+                                        reinterpret_cast<hipStream_t>(hip_stream));
+  if (rc) return fail(rc, "gather_tables: launch failed: %s", hipGetErrorString((hipError_t)rc));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "gather_tables: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)mq::kPrepLaunches, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
+int mq_gather_qmm_tables(const void* x, const uint32_t* w, const void* scales,
+                         const void* biases, const int32_t* lhs_indices,
+                         const int32_t* rhs_indices, void* out, int64_t P, int64_t B, int64_t M,
+                         int64_t N, int64_t K, int64_t E, int group_size, int bits, int dtype,
+                         const void* tables, size_t tables_bytes, void* hip_stream) {
+  int rc = check_common(w, scales, biases, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !out || !rhs_indices || !tables)
+    return fail(MQ_EINVAL, "x, out, rhs_indices and tables must be non-null");
+  if (P < 1 || M < 1 || E < 1 || B < 1)
+    return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
+                (long long)M, (long long)E, (long long)B);
+  if (!lhs_indices && P % B)
+    return fail(MQ_EINVAL, "lhs_indices=NULL requires B to divide P (B=%lld P=%lld)",
+                (long long)B, (long long)P);
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (N > INT32_MAX || K > INT32_MAX || P > INT32_MAX || M > 16 ||
+      !mq::gather_thin_path(P, M, K, E))
+    return fail(MQ_EUNSUPPORTED, "this gather does not run on the tables' kernel");
+  if (tables_bytes < mq::gather_workspace_bytes(P, M))
+    return fail(MQ_EINVAL, "tables too small: need %zu bytes", mq::gather_workspace_bytes(P, M));
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (N == 0) return MQ_OK;
+  int nl = 0;
+  rc = dispatch_16<mq::GatherLaunch>(dtype, bits, group_size, x, w, scales, biases, lhs_indices,
+                                     rhs_indices, out, P, B, M, N, K, E, const_cast<void*>(tables),
+                                     true, reinterpret_cast<hipStream_t>(hip_stream), &nl);
+  if (rc) return fail(rc, "gather_qmm_tables: no kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "gather_qmm_tables: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
+int mq_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
+              void* hip_stream) {
+  if (n < 0) return fail(MQ_EINVAL, "invalid size n=%lld", (long long)n);
+  if (n == 0) return MQ_OK;
+  if (!gate || !up || !out) return fail(MQ_EINVAL, "gate, up and out must be non-null");
+  if (dtype != MQ_BFLOAT16 && dtype != MQ_FLOAT16)
+    return fail(MQ_EUNSUPPORTED, "swiglu supports bf16 and fp16 (dtype %d)", dtype);
+  const int rc = mq::launch_swiglu(gate, up, out, n, dtype,
+                                   reinterpret_cast<hipStream_t>(hip_stream));
+  if (rc) return fail(rc, "swiglu: no kernel for this configuration");
+  return check_launch("swiglu");
 }
 
 int mq_gather_qmm_noalloc(const void* x, const uint32_t* w, const void* scales,

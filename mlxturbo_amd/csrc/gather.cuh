@@ -493,13 +493,15 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
   return 0;
 }
 
-// Prefill gather_qmm with thin experts: prep tables with segments of 64 / M
-// pairs, then the register-B grouped kernel (grouped.cuh).
+// Prefill gather_qmm with thin experts: the register-B grouped kernel
+// (grouped.cuh) over two-class tables (launch_thin_tables: segments of R =
+// 64 / M pairs, and of 2 R for experts with more than R pairs), built here
+// unless the caller built them for this routing already (prepped).
 template <int DT, int BITS, int GS>
 inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, const void* b,
                                const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
                                int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
-                               hipStream_t st, int* nlaunch) {
+                               hipStream_t st, int* nlaunch, bool prepped) {
   const int R = (int)(kThinBM / M);
   // 4 waves (256 columns) per workgroup at short K, 8 (512 columns, so each
   // x tile serves twice the columns) above K = 1024: config-4 banks, 2048
@@ -509,31 +511,31 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
   // waves (whose 128-register budget spills)
   const int nwv = K <= 1024 ? 4 : 8;
   const int64_t ncol = (N + 64 * nwv - 1) / (64 * nwv);
-  int64_t nwg = 0;
-  if (nwv == 8) {
-    // 8 waves: experts with more than 64 rows take 128-row tiles, which
-    // read their weights once per 128 rows (the workgroup's register
-    // budget already holds one workgroup per CU, so the taller tile costs
-    // no occupancy)
-    const int R1 = (int)(128 / M), C1 = R + 1;
-    if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st, R1, C1)) return rc;
-    for (const int64_t sb : {class_seg_bound(P, R1, C1, E), class_seg_bound(P, R, 0, E)})
-      nwg += (sb * ncol + 7) / 8 * 8;
-  } else {
-    if (int rc = launch_prep(rhs, lhs, P, E, B, R, ws, st)) return rc;
-    nwg = (class_seg_bound(P, R, 0, E) * ncol + 7) / 8 * 8;
+  // 8 waves: experts with more than 64 rows take 128-row tiles, which read
+  // their weights once per 128 rows (the workgroup's register budget
+  // already holds one workgroup per CU, so the taller tile costs no
+  // occupancy).  4 waves run those segments as two 64-row tiles (128-row
+  // tiles with 4 waves: config-4 down 261 against 176 us zipf), the same
+  // work as one-class tables, so one table build serves both widths.
+  if (!prepped) {
+    if (int rc = launch_thin_tables(rhs, lhs, P, E, B, M, ws, st)) return rc;
+    *nlaunch += kPrepLaunches;
   }
+  const int64_t h1 = nwv == 4 ? 2 : 1;
+  int64_t nwg = 0;
+  for (const int64_t sb : {h1 * class_seg_bound(P, 2 * R, R + 1, E), class_seg_bound(P, R, 0, E)})
+    nwg += (sb * ncol + 7) / 8 * 8;
   if (nwg > INT32_MAX) return kStatusUnsupported;
   const dim3 grid((unsigned)nwg);
-#define MQ_THIN(NWV, CLS2)                                                                      \
-  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV, CLS2>), grid, dim3(64 * NWV),\
-                     0, st, (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b, lhs,  \
-                     (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K, \
-                     (int)E, 0)
-  if (nwv == 4) MQ_THIN(4, false);
-  else MQ_THIN(8, true);
+#define MQ_THIN(NWV, HALVES)                                                                    \
+  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV, true, HALVES>), grid,       \
+                     dim3(64 * NWV), 0, st, (const uint16_t*)x, w, (const uint16_t*)s,           \
+                     (const uint16_t*)b, lhs, (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, \
+                     (int)M, (int)N, (int)K, (int)E, 0)
+  if (nwv == 4) MQ_THIN(4, true);
+  else MQ_THIN(8, false);
 #undef MQ_THIN
-  *nlaunch += kPrepLaunches + 1;
+  *nlaunch += 1;
   return 0;
 }
 
@@ -541,7 +543,11 @@ template <int DT, int BITS, int GS>
 inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const void* b,
                           const int32_t* lhs, const int32_t* rhs, void* out, int64_t P, int64_t B,
                           int64_t M, int64_t N, int64_t K, int64_t E, void* ws, hipStream_t st,
-                          int* nlaunch) {
+                          int* nlaunch, bool prepped) {
+  if (gather_thin_path(P, M, K, E))
+    return launch_grouped_thin<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
+                                             nlaunch, prepped);
+  if (prepped) return kStatusUnsupported;      // the tables are the thin kernel's
   const int64_t active = P < E ? P : E;
   const int64_t rows_per_expert = P * M / (active > 0 ? active : 1);
   if (rows_per_expert >= 192)
@@ -550,14 +556,6 @@ inline int launch_grouped(const void* x, const uint32_t* w, const void* s, const
   if (rows_per_expert >= 96)
     return launch_grouped_bm<DT, BITS, GS, 128>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws,
                                                 st, nlaunch, false);
-  // thin experts: the register-B kernel (config-4 down bank, K=512: 201-209
-  // against 265-270 us for the wide tile; gate/up, K=2048, with 8 waves per
-  // workgroup: 279 / 222 us zipf / uniform against 302 / 253); beyond K =
-  // 2048 (not measured) the LDS-shared wide tile, with taller tiles for the
-  // experts that turn out hot
-  if (K <= 2048)
-    return launch_grouped_thin<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
-                                             nlaunch);
   return launch_grouped_bm<DT, BITS, GS, 64>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
                                              nlaunch, true);
 }
@@ -673,14 +671,15 @@ template <int DT, int BITS, int GS>
 int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
                                     const void* b, const int32_t* lhs, const int32_t* rhs,
                                     void* out, int64_t P, int64_t B, int64_t M, int64_t N,
-                                    int64_t K, int64_t E, void* ws, hipStream_t st,
+                                    int64_t K, int64_t E, void* ws, bool prepped, hipStream_t st,
                                     int* nlaunch) {
   if (P > kGatherFusedMaxP && E > kGatherPrepMaxE) return kStatusUnsupported;
   if ((N + 15) / 16 > 65535) return kStatusUnsupported;
   if (P * M >= kGroupedMinRows && E <= kGatherPrepMaxE && K % kWideBK == 0 &&
       B * M * K * 2 < ((int64_t)1 << 31) && 256 * K * 2 < ((int64_t)1 << 31))
     return launch_grouped<DT, BITS, GS>(x, w, s, b, lhs, rhs, out, P, B, M, N, K, E, ws, st,
-                                        nlaunch);
+                                        nlaunch, prepped);
+  if (prepped) return kStatusUnsupported;
   return gather_qmv_launch<DT, BITS, GS, false>(x, w, s, b, nullptr, nullptr, nullptr, lhs, rhs,
                                                 out, P, B, M, N, K, E, ws, st, nlaunch);
 }

@@ -47,7 +47,7 @@ __device__ __forceinline__ void thin_tile(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E, int seg, int col) {
+    int P, int B, int Mi, int N, int K, int E, int seg, int col, int pofs) {
   constexpr int BN = 64 * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
   constexpr int MB = BM / 32;                   // 32-row blocks of the tile
   static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
@@ -61,7 +61,9 @@ __device__ __forceinline__ void thin_tile(
   __shared__ int s_orow[BM];
   const int n0 = col * BN;
   const int32_t* perm = ws + 1;
-  const int st0 = perm[P + seg], len = perm[2 * P + seg];
+  // the tile's pairs: the segment's from pair pofs on, at most BM / Mi
+  const int st0 = perm[P + seg] + pofs, len = min(perm[2 * P + seg] - pofs, BM / Mi);
+  if (len <= 0) return;                         // uniform: an empty half of a segment
   const int e = __builtin_amdgcn_readfirstlane(perm[3 * P + seg]);
   const bool valid = e < E;                     // uniform
   const int rows = len * Mi;                    // <= BM
@@ -320,11 +322,13 @@ __device__ __forceinline__ void thin_tile(
 // 1-D grid, 64 NWV threads, tiles placed by grouped_tile.  CLS2 false: the
 // tiles of the prep tables' size class cls (segments of up to 64 / Mi pairs),
 // ceil(N / (64 NWV)) x its segment bound workgroups.  CLS2 true: class 1
-// (segments of up to 128 / Mi pairs, 128-row tiles) in the first 8 q1
+// (segments of up to 2 (64 / Mi) pairs, 128-row tiles) in the first 8 q1
 // workgroups (q1 = its tiles / 8, rounded up), then class 0 (64-row tiles);
 // cls is ignored.  Each height runs its own code (a 128-row body for every
-// tile made the 64-row ones slower).
-template <int DT, int BITS, int GS, int PS, int NWV, bool CLS2>
+// tile made the 64-row ones slower).  HALVES: class 1's segments run as two
+// 64-row tiles each (first and second 64 / Mi pairs, adjacent tiles), the
+// work of one-class tables, from the same two-class tables.
+template <int DT, int BITS, int GS, int PS, int NWV, bool CLS2, bool HALVES = false>
 __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -333,23 +337,28 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
   const int32_t* hdr = ws + gather_ws_header(P);
   const int ncol = (N + 64 * NWV - 1) / (64 * NWV);
   int bi = blockIdx.x;
+  constexpr int H1 = HALVES ? 2 : 1;           // tiles per class-1 segment
   if constexpr (CLS2) {
     cls = 1;
-    const int q1 = ((hdr[2] - hdr[1]) * ncol + 7) / 8;
+    const int q1 = (H1 * (hdr[2] - hdr[1]) * ncol + 7) / 8;
     if (bi >= 8 * q1) {
       bi -= 8 * q1;
       cls = 0;
     }
   }
   const int s0 = hdr[2 - cls];
+  const int nv = (hdr[3 - cls] - s0) * (CLS2 && cls == 1 ? H1 : 1);
   int seg, col;
-  if (!grouped_tile(bi, hdr[3 - cls] - s0, ncol, seg, col)) return;
-  if (CLS2 && cls == 1)
+  if (!grouped_tile(bi, nv, ncol, seg, col)) return;
+  if (CLS2 && cls == 1 && !HALVES)
     thin_tile<DT, BITS, GS, PS, NWV, 128>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
-                                           seg + s0, col);
+                                           seg + s0, col, 0);
+  else if (CLS2 && cls == 1)
+    thin_tile<DT, BITS, GS, PS, NWV, 64>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
+                                          (seg >> 1) + s0, col, (seg & 1) * (64 / Mi));
   else
     thin_tile<DT, BITS, GS, PS, NWV, 64>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
-                                          seg + s0, col);
+                                          seg + s0, col, 0);
 }
 
 }  // namespace mq

@@ -47,13 +47,15 @@ struct WideLaunch {
 };
 
 // gather_qmm over P (x batch, expert) pairs (gather.cuh); *nlaunch counts the
-// kernels enqueued.
+// kernels enqueued.  prepped: ws already holds launch_thin_tables' tables for
+// this routing; only the thin grouped kernel takes them (kStatusUnsupported
+// for any other path).
 template <int DT, int BITS, int GS>
 struct GatherLaunch {
   static int run(const void* x, const uint32_t* w, const void* s, const void* b,
                  const int32_t* lhs, const int32_t* rhs, void* out, int64_t P, int64_t B,
-                 int64_t M, int64_t N, int64_t K, int64_t E, void* ws, hipStream_t st,
-                 int* nlaunch);
+                 int64_t M, int64_t N, int64_t K, int64_t E, void* ws, bool prepped,
+                 hipStream_t st, int* nlaunch);
 };
 
 // Fused gate+up+SiLU over P pairs: out = silu(x . Wg^T) * (x . Wu^T) with
@@ -92,6 +94,11 @@ struct GatherFoldLaunch {
 int launch_moe_route(const float* logits, int32_t* idx, float* w, int64_t rows, int64_t E,
                      int64_t top_k, const void* x, const void* sgw, void* sgate, int64_t H,
                      int dtype, hipStream_t st);
+
+// SwiGLU of a MoE layer's gate and up outputs (swiglu.hip): out = T(T(silu(g))
+// * u) elementwise over n values of dtype T (bf16 / f16), silu(g) = g / (1 +
+// exp(-g)) in float.  kStatusUnsupported for other dtypes.
+int launch_swiglu(const void* g, const void* u, void* out, int64_t n, int dtype, hipStream_t st);
 
 // MLX affine quantize of N x K float values (dtype DT: weights, scales and
 // biases share it) into the bitstream format, and dequantize of any width
@@ -316,6 +323,25 @@ __host__ __device__ inline size_t gather_ws_words(int64_t P) {
 constexpr int kPrepLaunches = 2;
 int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, int64_t B, int R,
                 void* ws, hipStream_t st, int R1 = 0, int C1 = 0, int R2 = 0, int C2 = 0);
+
+// Whether gather_qmm runs the thin grouped kernel (grouped.cuh): prefill
+// widths (P M >= kGroupedMinRows output rows), banks within the prep
+// tables, fewer than 96 rows per active expert, K <= 2048 in whole 64-code
+// steps.  The same routing then serves calls of different K (a MoE layer's
+// gate / up and down banks) from one table build.
+inline bool gather_thin_path(int64_t P, int64_t M, int64_t K, int64_t E) {
+  if (P * M < kGroupedMinRows || E > kGatherPrepMaxE || M > 64 || K > 2048 || K % 64) return false;
+  const int64_t active = P < E ? P : E;
+  return P * M / (active > 0 ? active : 1) < 96;
+}
+
+// The thin kernel's tables (launch_prep): segments of R = 64 / M pairs, and
+// of 2 R pairs for experts with more than R pairs (class 1).
+inline int launch_thin_tables(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E,
+                              int64_t B, int64_t M, void* ws, hipStream_t st) {
+  const int R = (int)(64 / M);
+  return launch_prep(rhs, lhs, P, E, B, R, ws, st, 2 * R, R + 1);
+}
 
 inline size_t gather_workspace_bytes(int64_t P, int64_t M) {
   if (P <= kGatherFusedMaxP && P * M < kGroupedMinRows) return 0;

@@ -134,10 +134,11 @@ class QuantizedSwitchLinear(torch.nn.Module):
         self.register_buffer("bias", bias)
 
     def forward(self, x: torch.Tensor, indices: torch.Tensor,
-                sorted_indices: bool = False) -> torch.Tensor:
+                sorted_indices: bool = False,
+                tables: Optional[ops.GatherTables] = None) -> torch.Tensor:
         out = ops.gather_qmm(x, self.weight, self.scales, self.biases, rhs_indices=indices,
                              transpose=True, group_size=self.group_size, bits=self.bits,
-                             mode=self.mode, sorted_indices=sorted_indices)
+                             mode=self.mode, sorted_indices=sorted_indices, tables=tables)
         if self.bias is not None:
             # bias [E, N] per expert, broadcast over the M rows of each pair
             out = out + self.bias[indices.long()].unsqueeze(-2)
@@ -148,12 +149,23 @@ class SwitchGLU(torch.nn.Module):
     """mlx-lm's ``SwitchGLU``: ``down(silu(gate(x)) * up(x))`` over the top-k
     experts of each token, with the ``_gather_sort`` reordering for long
     inputs (pairs sorted by expert once, then unsorted at the end, as
-    mlx-lm does at 64+ indices: fused.py:2402-2418)."""
+    mlx-lm does at 64+ indices: fused.py:2402-2418).
+
+    At prefill widths (1024+ pairs) the layer runs as the reference's prefill
+    path does (fused.py:3283-3316): the segment tables are built once for
+    the routing and shared by the gate, up and down gathers; the gate and up
+    gathers read x through the token of each pair (no gathered copy of x);
+    the SwiGLU is one pass; the router-weighted sum is one combine.  The
+    pairs stay in (token, expert) order throughout (the grouped kernels
+    group them by expert themselves), so no sort or unsort runs.  Each step
+    computes what the sort path computes, bit for bit."""
 
     SORT_THRESHOLD = 64
+    TABLES_THRESHOLD = 1024
 
     def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
-                 down_proj: QuantizedSwitchLinear, fuse_gate_up: bool = False):
+                 down_proj: QuantizedSwitchLinear, fuse_gate_up: bool = False,
+                 prefill_tables: bool = True):
         """``fuse_gate_up``: at decode widths (fewer than 1024 pairs) compute
         ``silu(gate) * up`` in one fused kernel (:func:`ops.gather_glu`, float
         sums, one rounding) with no expert sort -- the reference's opt-in
@@ -164,6 +176,39 @@ class SwitchGLU(torch.nn.Module):
         self.up_proj = up_proj
         self.down_proj = down_proj
         self.fuse_gate_up = fuse_gate_up
+        self.prefill_tables = prefill_tables
+
+    def _prefill(self, xe: torch.Tensor, idx: torch.Tensor,
+                 scores: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        """The prefill layer over shared tables, or None where it does not
+        apply (biases on the projections, other formats, no tables)."""
+        g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        if not self.prefill_tables or idx.numel() < self.TABLES_THRESHOLD:
+            return None
+        if g.bias is not None or u.bias is not None or d.bias is not None:
+            return None
+        if xe.dtype not in (torch.bfloat16, torch.float16) or g.scales.dtype != xe.dtype:
+            return None
+        E = g.num_experts
+        if u.num_experts != E or d.num_experts != E:
+            return None
+        # the gathers run the thin grouped kernel, which takes the tables,
+        # below 96 rows per active expert and at K <= 2048 (the library's
+        # gather_thin_path); elsewhere each gather builds its own
+        P = idx.numel()
+        if P >= 96 * min(P, E) or max(g.input_dims, u.input_dims, d.input_dims) > 2048:
+            return None
+        tables = ops.gather_tables(idx, E)
+        if tables is None:
+            return None
+        gk = g(xe, idx, tables=tables)                          # (T, k, 1, I)
+        uk = u(xe, idx, tables=tables)
+        h = ops.swiglu(gk, uk)
+        y = d(h, idx, tables=tables)                            # (T, k, 1, N)
+        T, top_k = idx.shape
+        if scores is not None:
+            return ops.moe_combine(y.reshape(-1, y.shape[-1]), None, scores.reshape(-1), T, top_k)
+        return y.reshape(T, top_k, y.shape[-1])
 
     def _fused(self, pairs: int) -> bool:
         g, u = self.gate_proj, self.up_proj
@@ -206,6 +251,10 @@ class SwitchGLU(torch.nn.Module):
                                       idx.shape[0], top_k)
                 return out.reshape(*lead, y.shape[-1])
             return y.reshape(*lead, top_k, y.shape[-1])
+        pre = self._prefill(xe, idx, scores)
+        if pre is not None:
+            return pre.reshape(*lead, *pre.shape[1:]) if scores is None else \
+                pre.reshape(*lead, pre.shape[-1])
         do_sort = idx.numel() >= self.SORT_THRESHOLD
         if do_sort:
             flat = idx.reshape(-1)

@@ -502,6 +502,75 @@ def _gather_launch(x3, flat, lhs, rhs, out, P, B, M, N, K, E, group_size, bits,
     _lib.check(rc, "gather_qmm")
 
 
+class GatherTables:
+    """Segment tables of prefill gathers over one routing (mq_gather_tables):
+    built once per MoE layer and passed to each of its gathers, as the
+    reference builds ``_moe_gemm_tables`` once per layer for its up, gate and
+    down grouped GEMMs (fused.py:3290-3316).  Holds its own device buffer,
+    so gathers in between do not disturb it."""
+
+    def __init__(self, buf: torch.Tensor, P: int, M: int, E: int):
+        self.buf, self.P, self.M, self.E = buf, P, M, E
+
+
+def gather_tables(rhs_indices: torch.Tensor, num_experts: int,
+                  rows: int = 1) -> Optional[GatherTables]:
+    """Tables for gathers whose pairs are the elements of ``rhs_indices``
+    (each pair ``rows`` rows, x reached without an index table: mlx-lm's
+    ``(T, 1)`` tokens against ``(T, top_k)`` experts, or one row per pair),
+    or None below prefill widths (1024 output rows), where the gathers build
+    none."""
+    dev = _require_gpu(rhs_indices)
+    rhs = _as_index(rhs_indices, dev).reshape(-1).to(torch.int32).contiguous()
+    P = rhs.numel()
+    if P * rows < _GLU_FUSED_MAX_ROWS or num_experts > _GATHER_PREP_MAX_E or rows > 16:
+        return None
+    lib = _lib.lib()
+    nbytes = int(lib.mq_gather_qmm_workspace_size(P, rows))
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    rc = lib.mq_gather_tables(None, rhs.data_ptr(), P, P, rows, num_experts, buf.data_ptr(),
+                              nbytes, _stream_ptr(buf))
+    if rc == _EUNSUPPORTED:
+        return None
+    _lib.check(rc, "gather_tables")
+    return GatherTables(buf, P, rows, num_experts)
+
+
+def _tables_launch(a, out, tables: GatherTables, group_size, bits) -> bool:
+    """mq_gather_qmm_tables for a validated call; False when the call is not
+    on the tables' kernel (the caller then runs the plain gather)."""
+    if (tables.P, tables.M, tables.E) != (a["P"], a["M"], a["E"]) or a["lhs"] is not None:
+        return False
+    x_ = _aligned(a["x"])
+    rc = _lib.lib().mq_gather_qmm_tables(
+        x_.data_ptr(), *[t.data_ptr() for t in a["flat"]], None, a["rhs"].data_ptr(),
+        out.data_ptr(), a["P"], a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
+        _DTYPE_CODE[a["x"].dtype], tables.buf.data_ptr(), tables.buf.numel(), _stream_ptr(out))
+    if rc == _EUNSUPPORTED:
+        return False
+    _lib.check(rc, "gather_qmm(tables)")
+    return True
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``T(T(silu(gate)) * up)`` elementwise, ``silu(g) = g / (1 + exp(-g))``
+    in float: mlx-lm SwitchGLU's activation between a MoE layer's gate / up
+    and down projections (``switch_mlp.activation`` in the reference's
+    prefill path, fused.py:3302), in one kernel pass (mq_swiglu)."""
+    dev = _require_gpu(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError(f"gate {tuple(gate.shape)} {gate.dtype} and up {tuple(up.shape)} "
+                         f"{up.dtype} differ")
+    if gate.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"swiglu takes bfloat16 or float16, got {gate.dtype}")
+    g, u = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(g)
+    rc = _lib.lib().mq_swiglu(g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(),
+                              _DTYPE_CODE[g.dtype], _stream_ptr(out))
+    _lib.check(rc, "swiglu")
+    return out
+
+
 def _lhs_table(P: int, B: int, dev) -> torch.Tensor:
     """The table the C ABI's NULL lhs stands for: pair p reads batch p / (P / B)."""
     return torch.arange(P, device=dev, dtype=torch.int32) // (P // B)
@@ -576,7 +645,8 @@ def _gather_composed(a, out, bank, group_size, bits) -> torch.Tensor:
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                biases: Optional[torch.Tensor] = None, lhs_indices=None, rhs_indices=None,
                transpose: bool = True, group_size: int = 64, bits: int = 4,
-               mode: str = "affine", sorted_indices: bool = False) -> torch.Tensor:
+               mode: str = "affine", sorted_indices: bool = False,
+               tables: Optional["GatherTables"] = None) -> torch.Tensor:
     """``mx.gather_qmm``: per index pair, ``x[lhs] @ dequantize(w[rhs]).T``.
 
     ``x`` is ``(..., M, K)`` and ``w`` ``(..., N, K*bits/32)``; ``lhs_indices``
@@ -586,10 +656,18 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     activations in the scales' dtype run on the gather kernels (more than 16
     rows per pair as one-row pairs, banks beyond the prep tables in expert
     slices); other formats and dtypes run as :func:`_gather_composed`.
+
+    ``tables`` (:func:`gather_tables` of the same routing) skips building the
+    segment tables where the call runs the thin grouped kernel (a MoE
+    layer's gathers over one routing share one build); the result is the
+    same bit for bit.
     """
     out, a = _gather_prep(x, [(w, scales, biases)], lhs_indices, rhs_indices, transpose,
                           group_size, bits, mode)
     if a is None:
+        return out
+    if tables is not None and a["route"] == "kernel" and _tables_launch(a, out, tables,
+                                                                        group_size, bits):
         return out
     if a["route"] == "composed":
         return _gather_composed(a, out, a["flat"][:3], group_size, bits)
@@ -857,4 +935,5 @@ def row_identity(on: bool = True):
 
 __all__: Sequence[str] = ("quantize", "dequantize", "quantized_matmul", "quantized_matmul_prepared",
                           "PreparedWeights", "gather_qmm", "gather_glu", "moe_combine",
+                          "gather_tables", "GatherTables", "swiglu",
                           "launch_count", "set_row_identity", "row_identity")
