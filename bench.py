@@ -70,6 +70,8 @@ def parse():
                         "(configs[1] skinny), combine (MoE combine, 2048 x top-8 x 2048), "
                         "gather_prefill_<proj>_<routing> (2048 tokens), "
                         "moe_layer_<routing>_T<T> (whole decode MoE layer), "
+                        "moe_block_<routing>_T<T> (decode MoE block: routing, layer, "
+                        "shared-expert merge), "
                         "moe_layer_prefill_<routing>[_sortpath] (whole prefill MoE layer, "
                         "2048 tokens), "
                         "route<T> (MoE routing + shared gate), "
@@ -104,6 +106,9 @@ def run_case(torch, mq, case: str) -> dict:
         return {"case": case, **measure_gather_prefill(torch, mq, 2048, NN, KK, routing, 20, 3)}
     if case.startswith("route"):
         return {"case": case, **measure_route(torch, mq, int(case[len("route"):] or 1), 100, 5)}
+    if case.startswith("moe_block_"):
+        routing, t = case[len("moe_block_"):].rsplit("_T", 1)
+        return {"case": case, **measure_moe_block(torch, mq, int(t), routing, 100, 5)}
     if case.startswith("moe_layer_prefill_"):
         routing = case[len("moe_layer_prefill_"):]
         sort = routing.endswith("_sortpath")
@@ -312,6 +317,60 @@ def measure_moe_layer(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidd
     torch.cuda.empty_cache()
     return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
             "distinct_experts": round(sum(len(np.unique(r)) for r in routes) / nroute, 1),
+            "launches": int(launches)}
+
+
+def measure_moe_block(torch, mq, T, routing, steps, warmup, E=512, top_k=8, hidden=2048,
+                      inter=512, nroute=64, seed=11):
+    """The decode MoE block after its router matmul as one timed unit
+    (ops.moe_block): routing of float logits with the shared expert's gate,
+    the fused gate+up+SiLU gather, the down projection with the combine and
+    the shared-expert merge folded in.  Logits rotate over `nroute` sets:
+    Gumbel noise plus log p_e, so the top-k is a draw without replacement
+    from p (zipf(1.1) over the experts through a fixed permutation, or
+    uniform).  Algorithmic bytes: each distinct expert's gate, up and down
+    weights once, plus logits, activations and the shared expert's row."""
+    rng = np.random.default_rng(seed + T)
+    if routing == "zipf":
+        p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
+        logp = np.log(p / p.sum())[np.argsort(np.random.default_rng(12345).permutation(E))]
+    else:
+        logp = np.zeros(E)
+    logit_sets = [(rng.gumbel(size=(T, E)) + logp).astype(np.float32) for _ in range(nroute)]
+    logits = [torch.from_numpy(l).cuda() for l in logit_sets]
+    experts = [np.unique(np.argsort(-l, axis=1, kind="stable")[:, :top_k]) for l in logit_sets]
+
+    def bank(N, K, s):
+        (w, sc, b), = make_weights(torch, E * N, K, 1, seed=s)
+        return w.view(E, N, -1), sc.view(E, N, -1), b.view(E, N, -1)
+
+    gate, up, down = bank(inter, hidden, seed), bank(inter, hidden, seed + 1), \
+        bank(hidden, inter, seed + 2)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((T, hidden), device="cuda", generator=g).to(torch.bfloat16)
+    sgw = (torch.randn((hidden,), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    shared = (torch.randn((T, hidden), device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+
+    def per_expert(N, K):
+        return N * K // 2 + 4 * N * (K // 64)
+
+    pe = 2 * per_expert(inter, hidden) + per_expert(hidden, inter)
+    act = 4 * T * E + 2 * T * hidden * 3 + 2 * hidden + 2 * T * top_k * inter + 2 * T * hidden
+    nbytes = [len(e) * pe + act for e in experts]
+
+    def fn(i):
+        mq.ops.moe_block(x, logits[i % nroute], top_k, gate, up, down, sgw=sgw, shared=shared)
+
+    n0 = mq.launch_count()
+    fn(0)
+    launches = mq.launch_count() - n0
+    _, per_step = time_graph(torch, fn, steps, warmup)
+    avg_bytes = sum(nbytes[i % nroute] for i in range(steps)) / steps
+    del gate, up, down
+    torch.cuda.empty_cache()
+    return {"us": round(per_step * 1e6, 2), "GBps": round(avg_bytes / per_step / 1e9, 1),
+            "distinct_experts": round(sum(len(e) for e in experts) / nroute, 1),
             "launches": int(launches)}
 
 
@@ -765,6 +824,9 @@ def main():
                     torch, mq, T, 1024, 2048, routing, 100, 5, glu=True)
                 # the whole layer: gate+up+SiLU, down, router-weighted combine
                 sweep[f"moe_layer_{routing}_T{T}"] = measure_moe_layer(
+                    torch, mq, T, routing, 100, 5)
+                # the block: routing + shared gate, the layer, the shared merge
+                sweep[f"moe_block_{routing}_T{T}"] = measure_moe_block(
                     torch, mq, T, routing, 100, 5)
         for T in (1, 4, 8):
             sweep[f"moe_route_T{T}_E512_k8"] = measure_route(torch, mq, T, 100, 5)

@@ -905,6 +905,30 @@ def moe_route(logits: torch.Tensor, top_k: int, x: Optional[torch.Tensor] = None
     return idx, wts, sg
 
 
+def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
+              sgw: Optional[torch.Tensor] = None, shared: Optional[torch.Tensor] = None,
+              group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """A decode MoE block after its router matmul, as the reference's decode
+    path runs it (kernels/moe_route_decode.py:151-327 and 353-398 around
+    moe_decode_fused.py:331-397): ``moe_route`` (top-k, softmax weights and,
+    with ``sgw``, the shared expert's gate ``sigmoid(T(x . sgw))``), the
+    fused gate+up+SiLU gather over the selected experts, and the down
+    projection with the router-weighted combine folded in, the shared
+    expert's output ``shared`` ``(T, H)`` merged with its gate.  ``x`` is
+    ``(T, H)``, ``logits`` float32 ``(T, E)``; ``gate``, ``up``, ``down``
+    are ``(w, scales, biases)`` banks.  Returns ``(T, H_out)``: the same
+    bits as calling the three steps one by one."""
+    if (sgw is None) != (shared is None):
+        raise ValueError("sgw and shared are given together")
+    T, H = x.shape
+    idx, wts, sg = moe_route(logits, top_k, x, sgw) if sgw is not None else \
+        moe_route(logits, top_k)
+    h = gather_glu(x.reshape(T, 1, 1, H), *gate, *up, rhs_indices=idx, group_size=group_size,
+                   bits=bits)                                      # (T, k, 1, I)
+    return gather_qmm_combine(h, *down, idx, wts, group_size=group_size, bits=bits,
+                              sgate=sg, shared=shared)
+
+
 def launch_count() -> int:
     """Kernel launches made through the library so far (proof the HIP path ran)."""
     return _lib.launch_count()
@@ -935,5 +959,5 @@ def row_identity(on: bool = True):
 
 __all__: Sequence[str] = ("quantize", "dequantize", "quantized_matmul", "quantized_matmul_prepared",
                           "PreparedWeights", "gather_qmm", "gather_glu", "moe_combine",
-                          "gather_tables", "GatherTables", "swiglu",
+                          "gather_tables", "GatherTables", "swiglu", "moe_block",
                           "launch_count", "set_row_identity", "row_identity")
