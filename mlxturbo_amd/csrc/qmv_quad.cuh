@@ -172,22 +172,23 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   lds8* ls = (lds8*)qq_smem + wid * (2 * 4 * 16 * CS);
   u32x4 sq[SB], bq[SB];
   const int cr = lane & 3, cc0 = lane >> 2;
-  const int64_t crow = (int64_t)(row0 + cr) * G * 2;
-  const int64_t ca0 = ((crow + (int64_t)s0 * Q::GPI * 2) & ~(int64_t)15) + 16 * cc0;
-  const uint32_t sbytes = (uint32_t)((int64_t)N * G * 2);
+  // (32-bit offsets: the launch keeps the arrays below 2^31 bytes)
+  const uint32_t crow = (uint32_t)(row0 + cr) * (uint32_t)G * 2u;
+  const uint32_t ca0 = ((crow + (uint32_t)s0 * (Q::GPI * 2)) & ~15u) + 16u * cc0;
+  const uint32_t sbytes = (uint32_t)N * (uint32_t)G * 2u;
   const auto rs = make_rsrc(scales, sbytes);
   const auto rb = make_rsrc(biases, sbytes);
   uint32_t go[SB];
 #pragma unroll
   for (int u = 0; u < SB; ++u) {
-    go[u] = cc0 + 16 * u < CH && cr < nrows ? (uint32_t)(ca0 + 256 * u) : 0x80000000u;
+    go[u] = cc0 + 16 * u < CH && cr < nrows ? ca0 + 256u * u : 0x80000000u;
     sq[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, go[u], 0, 0);
     bq[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, go[u], 0, 0);
   }
   // this lane's scale at instruction s0: row j, group s0 GPI + gb
   const int gb = 16 * bb * (8 / BITS) / GS;
-  const int64_t aj = ((int64_t)(row0 + j) * G + (int64_t)s0 * Q::GPI) * 2;
-  const lds8* lsj = ls + j * 16 * CS + (int)(aj & 15) + 2 * gb;
+  const uint32_t aj = ((uint32_t)(row0 + j) * (uint32_t)G + (uint32_t)s0 * Q::GPI) * 2u;
+  const lds8* lsj = ls + j * 16 * CS + (int)(aj & 15u) + 2 * gb;
 
   // ---- loads: weights (4 rows x 256 B) and the x slab per instruction -----
   // A ring of R = D + 1 slots: instruction t + D is issued into the slot
@@ -240,13 +241,19 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
   // only costs the wave the plain route.
   typedef unsigned short qq_u16x2 __attribute__((ext_vector_type(2)));
   qq_u16x2 hmax = {0, 0};
-  // chunk u's entries past the row zeroed, into LDS, into the big check
-  auto put = [&](int u, u32x4 sv, u32x4 bv) {
+  // Chunk u's entries past the row zeroed, into LDS, into the big check.
+  // Only a wave whose copy reaches past G (a ragged last instruction, or an
+  // untight copy's extra chunk) has such entries in a live chunk (dead
+  // chunks read zeros): a uniform flag keeps the others off the masking
+  // (else the compiler selects every entry, ~30 VALU per wave).
+  const bool ragged = s1 * Q::GPI > G || !quad_tight<BITS, GS>(G, lks);
+  auto put = [&](int u, u32x4 sv, u32x4 bv, auto masked) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       hmax = __builtin_elementwise_max(hmax, __builtin_bit_cast(qq_u16x2, sv[e] & 0x7fff7fffu));
-    const int g0c = (int)((ca0 + 256 * u - crow) >> 1);   // group of the chunk's entry 0
-    if (g0c + 8 > G) {
+    if constexpr (decltype(masked)::value) {
+      // group of the chunk's entry 0 (negative: the chunk starts before the row)
+      const int g0c = (int)(ca0 + 256u * u - crow) >> 1;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t keep = (g0c + 2 * e < G ? 0x0000ffffu : 0u) |
@@ -259,8 +266,13 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
     *(lds_u32x4*)(ls + cr * 16 * CS + 16 * cc) = sv;
     *(lds_u32x4*)(ls + 4 * 16 * CS + cr * 16 * CS + 16 * cc) = bv;
   };
+  if (ragged) {
 #pragma unroll
-  for (int u = 0; u < SB; ++u) put(u, sq[u], bq[u]);
+    for (int u = 0; u < SB; ++u) put(u, sq[u], bq[u], std::true_type{});
+  } else {
+#pragma unroll
+    for (int u = 0; u < SB; ++u) put(u, sq[u], bq[u], std::false_type{});
+  }
   // the one chunk across the end of the arrays (their size not a multiple
   // of 16 bytes) read zeros where it crosses the range: its lane reads the
   // entries one by one and stores the chunk again (after the plain stores,
@@ -277,7 +289,7 @@ __global__ __launch_bounds__(64 * kQuadMaxKS) void qmv_quad_kernel(
         bv[e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, o, 0, 0) |
                 ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, o + 2, 0, 0) << 16);
       }
-      put(u, sv, bv);
+      put(u, sv, bv, std::true_type{});
     }
   }
   if constexpr (LATE) {
