@@ -49,8 +49,14 @@ def _row() -> tuple[str, ...]:
     return tuple([STOCK] + [SKINNY] * SKINNY_MAX_M)
 
 
-# The reference's measured production geometries (dispatch.py:59-68); the
-# skinny kernel is the measured winner at M = 1..16 on each of them.
+# The reference's measured production geometries (dispatch.py:59-68).  Its
+# rows choose among Metal kernels per M; here the per-geometry choice is the
+# library's own cost model (csrc/launch.h wide_route / wide_plan: skinny
+# launch time 3 us + weight bytes at 3.6 TB/s times a factor per row count,
+# wide tile time per round of workgroups, each constant measured on MI355X),
+# which every call consults, so the default rows only name the streaming
+# kernels at M = 1..16 (what the model picks there on every geometry) and a
+# row is where a caller forces 16-row launches above 16 rows ("skinny").
 DEFAULT_ROUTE_TABLE: dict[tuple[int, int], tuple[str, ...]] = {
     (5120, 17408): _row(),     # MLP up/gate
     (17408, 5120): _row(),     # MLP down
