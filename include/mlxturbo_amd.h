@@ -219,6 +219,26 @@ int mq_gather_qmm_tables(const void* x, const uint32_t* w, const void* scales,
                          const void* tables, size_t tables_bytes, void* hip_stream);
 
 /*
+ * The decode MoE block's routing and fused gate+up+SiLU in one launch:
+ * mq_moe_route(logits, idx, weights, T, E, top_k, x, sgw, sgate, K, dtype)
+ * followed by mq_gather_glu(x [T, 1, K], gate bank, up bank, lhs NULL, rhs
+ * idx, out [T * top_k, N], P = T * top_k, B = T, M = 1, ...), bit for bit:
+ * every workgroup routes the tokens itself (the routing kernel's pieces) and
+ * workgroup 0 writes idx / weights (and, with sgw, sgate) for the down
+ * projection that follows (mq_gather_qmm_combine).  The reference runs its
+ * decode route (kernels/moe_route_decode.py:151-327) and its fused decode
+ * gate/up (kernels/moe_decode_fused.py:331-350) as separate dispatches.
+ * Up to 64 pairs (T * top_k) over up to 512 experts; other calls return
+ * MQ_EUNSUPPORTED and the caller makes the two calls.
+ */
+int mq_moe_glu_route(const void* x, const float* logits, const uint32_t* w_gate,
+                     const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
+                     const void* scales_up, const void* biases_up, const void* sgw, int32_t* idx,
+                     float* weights, void* sgate, void* out, int64_t T, int64_t top_k, int64_t N,
+                     int64_t K, int64_t E, int group_size, int bits, int dtype,
+                     void* hip_stream);
+
+/*
  * out[i] = T(T(silu(gate[i])) * up[i]) for i < n, silu(g) = g / (1 + exp(-g))
  * in float, dtype bf16 or fp16: mlx-lm SwitchGLU's activation between the
  * gate / up and down gathers (`act = switch_mlp.activation(x_up, x_gate)` in

@@ -382,6 +382,50 @@ int mq_gather_qmm_tables(const void* x, const uint32_t* w, const void* scales,
   return MQ_OK;
 }
 
+int mq_moe_glu_route(const void* x, const float* logits, const uint32_t* w_gate,
+                     const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
+                     const void* scales_up, const void* biases_up, const void* sgw, int32_t* idx,
+                     float* weights, void* sgate, void* out, int64_t T, int64_t top_k, int64_t N,
+                     int64_t K, int64_t E, int group_size, int bits, int dtype,
+                     void* hip_stream) {
+  int rc = check_common(w_gate, scales_gate, biases_gate, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  rc = check_common(w_up, scales_up, biases_up, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !logits || !idx || !weights || !out)
+    return fail(MQ_EINVAL, "x, logits, idx, weights and out must be non-null");
+  if ((sgw == nullptr) != (sgate == nullptr))
+    return fail(MQ_EINVAL, "sgw and sgate are given together or not at all");
+  if (T < 0 || E < 1 || top_k < 1 || top_k > E)
+    return fail(MQ_EINVAL, "invalid sizes T=%lld E=%lld top_k=%lld", (long long)T, (long long)E,
+                (long long)top_k);
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (T == 0 || N == 0) return MQ_OK;
+  if (T * top_k > 64 || E > 512 || N > INT32_MAX || K > INT32_MAX)
+    return fail(MQ_EUNSUPPORTED,
+                "moe_glu_route routes up to 64 pairs over up to 512 experts (T=%lld top_k=%lld "
+                "E=%lld)", (long long)T, (long long)top_k, (long long)E);
+  mq::RouteArgs ra;
+  ra.logits = logits;
+  ra.sgw = static_cast<const uint16_t*>(sgw);
+  ra.idx = idx;
+  ra.w = weights;
+  ra.sgate = static_cast<uint16_t*>(sgate);
+  ra.top_k = (int)top_k;
+  int nl = 0;
+  rc = dispatch_16<mq::GluRouteLaunch>(dtype, bits, group_size, x, w_gate, scales_gate,
+                                       biases_gate, w_up, scales_up, biases_up, out, T, N, K, E,
+                                       ra, reinterpret_cast<hipStream_t>(hip_stream), &nl);
+  if (rc) return fail(rc, "moe_glu_route: no kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "moe_glu_route: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
 int mq_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
               void* hip_stream) {
   if (n < 0) return fail(MQ_EINVAL, "invalid size n=%lld", (long long)n);

@@ -27,6 +27,7 @@
 #include "grouped.cuh"
 #include "qmm_wide.cuh"
 #include "qmv.cuh"
+#include "route.cuh"
 
 namespace mq {
 
@@ -90,14 +91,20 @@ __host__ __device__ inline size_t gather_group_lds(int NWT, int XM, bool sbl, in
 // GLU: (w, scales, biases) is the gate bank and (w2, scales2, biases2) the up
 // bank of the same shape; out = silu(gate) * up (GluRows: the gate and up
 // tiles of a row block run as the two tiles of one qmv_tile call).
-template <int DT, int BITS, int GS, int GPL, int NW, int NWT, int PF, int XM, bool SBL, bool GLU>
+// ROUTE (P <= 64, no lhs, B = P / top_k tokens): the pairs' experts are not
+// read from rhs but routed here from the tokens' float logits (ra.logits
+// [B, E], E <= 512) with the routing kernel's wave pieces (route.cuh), every
+// wave alike; workgroup 0 also writes the routing (ra.idx, ra.w) and, with
+// ra.sgw, the shared expert's gate (ra.sgate) for the down projection.
+template <int DT, int BITS, int GS, int GPL, int NW, int NWT, int PF, int XM, bool SBL, bool GLU,
+          bool ROUTE = false>
 __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint32_t* __restrict__ w2, const uint16_t* __restrict__ scales2,
     const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
     const int32_t* __restrict__ rhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E, int R, int wg_target) {
+    int P, int B, int Mi, int N, int K, int E, int R, int wg_target, RouteArgs ra) {
   extern __shared__ __align__(16) unsigned char qmv_smem[];
   constexpr int TJ = GLU ? 2 : 1;
   __shared__ f32x4 red[NW * TJ][64];
@@ -135,7 +142,36 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     // Wave-level discovery (every wave computes the same answer; no barrier):
     // lane p holds pair p's key and cb = number of earlier pairs with that key.
     const int lane = t & 63;
-    const int key = lane < P ? key_of(lane) : -1;
+    int key = -1;
+    if constexpr (ROUTE) {
+      // token tok routed by wave tok % NW (pair p = tok * top_k + rank r
+      // takes lane r's expert), the pairs' experts met in LDS; in
+      // workgroup 0 the routing wave also writes the token's routing and
+      // shared gate
+      const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+      const bool writer = blockIdx.x == 0;
+      for (int tok = wv; tok < B; tok += NW) {
+        int sel_e;
+        float sel_v;
+        route_wave_topk<8>(ra.logits + (int64_t)tok * E, E, ra.top_k, lane, sel_e, sel_v);
+        if (lane < ra.top_k) s_key[tok * ra.top_k + lane] = sel_e;
+        if (writer) {
+          const float wgt = route_wave_softmax(sel_v, lane, ra.top_k);
+          if (lane < ra.top_k) {
+            ra.idx[tok * ra.top_k + lane] = sel_e;
+            ra.w[tok * ra.top_k + lane] = wgt;
+          }
+          if (ra.sgw != nullptr) {
+            const uint16_t g = route_wave_shared_gate<DT>(x + (int64_t)tok * K, ra.sgw, K, lane);
+            if (lane == 0) ra.sgate[tok] = g;
+          }
+        }
+      }
+      __syncthreads();
+      key = lane < P ? s_key[lane] : -1;
+    } else {
+      key = lane < P ? key_of(lane) : -1;
+    }
     int cb = 0;
     for (int q = 0; q < P; ++q) {
       const int kq = __builtin_amdgcn_readlane(key, q);
@@ -155,7 +191,7 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     __builtin_amdgcn_wave_barrier();
     if (lane < P && key == e && d >= 0 && d < R) {
       s_members[d] = lane;
-      s_xbase[d] = x_batch(lhs, lane, P, B);       // loaded with rhs by key_of: cache hit
+      s_xbase[d] = ROUTE ? lane / ra.top_k : x_batch(lhs, lane, P, B);
     }
     if (t == 0) s_expert = e;
     __syncthreads();
@@ -593,12 +629,12 @@ inline int gather_tile_waves(int64_t max_seg, int64_t N, int64_t K) {
 
 // The streaming gather kernel over segments (GLU: fused gate+up+SiLU with the
 // up bank in w2 / s2 / b2).
-template <int DT, int BITS, int GS, bool GLU>
+template <int DT, int BITS, int GS, bool GLU, bool ROUTE = false>
 inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, const void* b,
                              const uint32_t* w2, const void* s2, const void* b2,
                              const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
                              int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
-                             hipStream_t st, int* nlaunch) {
+                             hipStream_t st, int* nlaunch, RouteArgs ra = RouteArgs{}) {
   using C = QmvConf<BITS, GS>;
   // Segments of up to R pairs; R * M <= 8 A rows stream x through LDS, one
   // pair of more than 8 rows reads x fragments from global memory.  A segment
@@ -651,11 +687,12 @@ inline int gather_qmv_launch(const void* x, const uint32_t* w, const void* s, co
   const dim3 grid((unsigned)nwg);
 #define MQ_GX(WPT, X, SB)                                                                    \
   if (nwt == WPT && xml == X && sbl == SB) {                                                  \
-    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, WPT, C::PF, X, SB, GLU>), \
+    hipLaunchKernelGGL((gather_qmv_kernel<DT, BITS, GS, C::GPL, C::NW, WPT, C::PF, X, SB, GLU, \
+                                          ROUTE>),                                           \
                        grid, dim3(64 * C::NW), lds_for(X, WPT, SB), st, (const uint16_t*)x, w, \
                        (const uint16_t*)s, (const uint16_t*)b, w2, (const uint16_t*)s2,       \
                        (const uint16_t*)b2, lhs, rhs, (uint16_t*)out, wsp, (int)P, (int)B,    \
-                       (int)M, (int)N, (int)K, (int)E, R, wg_target);                        \
+                       (int)M, (int)N, (int)K, (int)E, R, wg_target, ra);                    \
   }
 #define MQ_GXW(WPT)                                                                          \
   MQ_GX(WPT, 0, true) MQ_GX(WPT, 1, true) MQ_GX(WPT, 2, true) MQ_GX(WPT, 4, true)            \
@@ -682,6 +719,20 @@ int GatherLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void
   if (prepped) return kStatusUnsupported;
   return gather_qmv_launch<DT, BITS, GS, false>(x, w, s, b, nullptr, nullptr, nullptr, lhs, rhs,
                                                 out, P, B, M, N, K, E, ws, st, nlaunch);
+}
+
+template <int DT, int BITS, int GS>
+int GluRouteLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const void* sg,
+                                      const void* bg, const uint32_t* wu, const void* su,
+                                      const void* bu, void* out, int64_t T, int64_t N, int64_t K,
+                                      int64_t E, const RouteArgs& ra, hipStream_t st,
+                                      int* nlaunch) {
+  const int64_t P = T * ra.top_k;
+  if (T < 1 || ra.top_k < 1 || ra.top_k > E || P > 64 || E > 64 * 8 || (N + 15) / 16 > 65535)
+    return kStatusUnsupported;
+  return gather_qmv_launch<DT, BITS, GS, true, true>(x, wg, sg, bg, wu, su, bu, nullptr, nullptr,
+                                                     out, P, T, 1, N, K, E, nullptr, st, nlaunch,
+                                                     ra);
 }
 
 template <int DT, int BITS, int GS>

@@ -18,6 +18,7 @@ namespace mq {
 #ifdef MQ_INST_GLU
 #define MQ_INST(GS)                                                  \
   template struct GluLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;           \
+  template struct GluRouteLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;      \
   template struct GatherFoldLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
 #else
 #define MQ_INST(GS)                                                  \

@@ -69,6 +69,31 @@ struct GluLaunch {
                  int64_t K, int64_t E, void* ws, hipStream_t st, int* nlaunch);
 };
 
+// Routing arguments of the decode GLU gather that routes its own tokens
+// (gather.cuh, ROUTE): float logits [T, E], top_k, and where workgroup 0
+// writes the routing (idx int32 / w float [T, top_k]) and, with sgw [H],
+// the shared expert's gate (sgate [T]).
+struct RouteArgs {
+  const float* logits = nullptr;
+  const uint16_t* sgw = nullptr;
+  int32_t* idx = nullptr;
+  float* w = nullptr;
+  uint16_t* sgate = nullptr;
+  int top_k = 0;
+};
+
+// The fused gate+up+SiLU gather of T decode tokens with the tokens' routing
+// computed inside it from their logits (the routing kernel's pieces, so idx,
+// w and sgate are mq_moe_route's bits and out is mq_gather_glu's over them);
+// kStatusUnsupported beyond T * top_k = 64 pairs or E = 512 experts.
+template <int DT, int BITS, int GS>
+struct GluRouteLaunch {
+  static int run(const void* x, const uint32_t* wg, const void* sg, const void* bg,
+                 const uint32_t* wu, const void* su, const void* bu, void* out, int64_t T,
+                 int64_t N, int64_t K, int64_t E, const RouteArgs& ra, hipStream_t st,
+                 int* nlaunch);
+};
+
 // Down projection with the MoE combine folded in (gather.cuh), decode widths:
 // x [T * top_k, K] (one row per pair), rhs and cw (float router weights)
 // [T * top_k], out [T, N] = the combine of mq_moe_combine (inv = NULL) over

@@ -1,0 +1,194 @@
+// MoE routing pieces shared by the routing kernel (route.hip) and the decode
+// GLU gather that routes its own tokens (gather.cuh, ROUTE): each piece is
+// computed by one whole wave, so both kernels give the same bits.
+//
+// Reference behaviour: mlxturbo/kernels/moe_route_decode.py:151-327
+// (`route`): per row, top_k rounds of "take the largest logit and drop it"
+// (equal values: the smaller expert index wins, as torch.topk / HF decide),
+// then a softmax over the selected logits with the largest subtracted, summed
+// in float in selection order; the shared expert's gate sigmoid(T(x . sgw))
+// with the dot summed in float and the sigmoid evaluated in T one operation
+// at a time (MLX's form: y = 1 / (1 + exp(|s|)), s < 0 ? y : 1 - y, each
+// step rounded to T).
+#pragma once
+#include "mq_common.h"
+
+namespace mq {
+
+// experts per lane: E <= 64 kRouteMaxPerLane
+constexpr int kRouteMaxPerLane = 16;
+
+#define MQ_DPP_STEP(x, OP, CTRL, ROWS)                                                        \
+  x = OP(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROWS, 0xf, false))
+// Largest / smallest uint32 over the 64 lanes, returned to every lane:
+// inclusive row scans (row_shr 1, 2, 4, 8), the row ends broadcast into the
+// following rows (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2
+// and 3), the total read from lane 63.  Lanes without a source keep their
+// own value (bound_ctrl off, old = x).  (v_max_u32 / v_min_u32 directly: a
+// compare-and-select lets the compiler re-run the DPP move under a partial
+// exec mask, where disabled source lanes read as out of range.)
+template <bool MAX>
+__device__ __forceinline__ uint32_t route_wave_reduce_u32(uint32_t x) {
+#define MQ_OP(a, b) (MAX ? __builtin_elementwise_max(a, b) : __builtin_elementwise_min(a, b))
+  MQ_DPP_STEP(x, MQ_OP, 0x111, 0xf);
+  MQ_DPP_STEP(x, MQ_OP, 0x112, 0xf);
+  MQ_DPP_STEP(x, MQ_OP, 0x114, 0xf);
+  MQ_DPP_STEP(x, MQ_OP, 0x118, 0xf);
+  MQ_DPP_STEP(x, MQ_OP, 0x142, 0xa);
+  MQ_DPP_STEP(x, MQ_OP, 0x143, 0xc);
+#undef MQ_OP
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+#undef MQ_DPP_STEP
+
+// Sum over the 64 lanes (lanes without a source add 0), returned to every lane.
+__device__ __forceinline__ float route_wave_sum_f32(float x) {
+#define MQ_DPP_ADD(CTRL, ROWS)                                                                 \
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),    \
+                                                             CTRL, ROWS, 0xf, false))
+  MQ_DPP_ADD(0x111, 0xf);
+  MQ_DPP_ADD(0x112, 0xf);
+  MQ_DPP_ADD(0x114, 0xf);
+  MQ_DPP_ADD(0x118, 0xf);
+  MQ_DPP_ADD(0x142, 0xa);
+  MQ_DPP_ADD(0x143, 0xc);
+#undef MQ_DPP_ADD
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// float -> uint32 with the same order (larger float, larger key; -0 and +0
+// equal); 0 is below every float's key and marks a taken expert.
+__device__ __forceinline__ uint32_t route_order_key(float v) {
+  const uint32_t u = v == 0.0f ? 0u : __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float route_from_key(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// sigmoid in T, one rounding per operation (MLX's Sigmoid form)
+template <int DT>
+__device__ __forceinline__ uint16_t route_sigmoid_t(uint16_t s16) {
+  using T = T16<DT>;
+  const float s = T::to_f32(s16);
+  const float e = T::to_f32(T::round1(expf(__builtin_fabsf(s))));
+  const float d = T::to_f32(T::round1(1.0f + e));
+  const float y = T::to_f32(T::round1(1.0f / d));
+  return s < 0.0f ? T::round1(y) : T::round1(1.0f - y);
+}
+
+// x before y in the per-lane order: larger key, then smaller slot
+__device__ __forceinline__ bool route_key_before(uint32_t kx, int ix, uint32_t ky, int iy) {
+  return kx > ky || (kx == ky && ix < iy);
+}
+
+// The top_k experts of one row of E float logits, by one whole wave: lane l
+// holds experts l, l + 64, ... (NK of them, NK the power of two covering E /
+// 64) as order-preserving keys, sorts them once with a bitonic network, and
+// each round is two wave reductions over the lanes' heads (the largest key,
+// then the smallest expert holding it), after which the winning lane drops
+// its head.  Lane r < top_k gets round r's expert and logit.
+template <int NK>
+__device__ __forceinline__ void route_wave_topk(const float* __restrict__ lr, int E, int top_k,
+                                                int lane, int& sel_e, float& sel_v) {
+  uint32_t key[NK];
+  int slot[NK];                                 // expert = lane + 64 slot
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    const int e = lane + 64 * j;
+    key[j] = e < E ? route_order_key(lr[e]) : 0u;
+    slot[j] = j;
+  }
+  // bitonic sort of the lane's NK keys, descending in route_key_before order
+#pragma unroll
+  for (int k = 2; k <= NK; k <<= 1)
+#pragma unroll
+    for (int jj = k >> 1; jj > 0; jj >>= 1)
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const int l = i ^ jj;
+        if (l > i) {
+          const bool swap = (i & k) == 0 ? route_key_before(key[l], slot[l], key[i], slot[i])
+                                         : route_key_before(key[i], slot[i], key[l], slot[l]);
+          const uint32_t ka = key[i], kb = key[l];
+          const int sa = slot[i], sb = slot[l];
+          key[i] = swap ? kb : ka;
+          key[l] = swap ? ka : kb;
+          slot[i] = swap ? sb : sa;
+          slot[l] = swap ? sa : sb;
+        }
+      }
+  sel_v = 0.0f;
+  sel_e = 0;
+  for (int r = 0; r < top_k; ++r) {
+    // the lane's head is its best remaining expert (ties: smaller expert)
+    const uint32_t mk = route_wave_reduce_u32<true>(key[0]);
+    const uint32_t cand =
+        (key[0] == mk && mk != 0u) ? (uint32_t)(lane + 64 * slot[0]) : 0xffffffffu;
+    const uint32_t win = route_wave_reduce_u32<false>(cand);
+    if ((int)win % 64 == lane) {
+#pragma unroll
+      for (int j = 0; j + 1 < NK; ++j) {
+        key[j] = key[j + 1];
+        slot[j] = slot[j + 1];
+      }
+      key[NK - 1] = 0u;
+    }
+    if (lane == r) {
+      sel_v = route_from_key(mk);
+      sel_e = (int)win;
+    }
+  }
+}
+
+// Softmax weight of lane r < top_k over the selected logits (round 0 holds
+// the largest), summed in float in selection order; 0 on other lanes.
+__device__ __forceinline__ float route_wave_softmax(float sel_v, int lane, int top_k) {
+  const float m =
+      __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sel_v), 0));
+  const float ex = lane < top_k ? expf(sel_v - m) : 0.0f;
+  float s = 0.0f;
+  for (int r = 0; r < top_k; ++r)
+    s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
+  return lane < top_k ? ex / s : 0.0f;
+}
+
+// The shared expert's gate sigmoid(T(x . sgw)) of one row by one whole
+// wave: lane l sums the 16-byte pieces l, l + 64, ... of x and the gate
+// weight (eight values each, in piece order) in float, or the elements l,
+// l + 64, ... of a ragged or unaligned row; then the wave sum, rounded to T.
+template <int DT>
+__device__ __forceinline__ uint16_t route_wave_shared_gate(const uint16_t* __restrict__ xr,
+                                                           const uint16_t* __restrict__ sgw,
+                                                           int H, int lane) {
+  using T = T16<DT>;
+  float acc = 0.0f;
+  const bool vec = H % 8 == 0 && (((uintptr_t)xr | (uintptr_t)sgw) & 15u) == 0;
+  if (vec) {
+    const u32x4* xv = reinterpret_cast<const u32x4*>(xr);
+    const u32x4* gv = reinterpret_cast<const u32x4*>(sgw);
+    for (int c0 = lane; c0 < H / 8; c0 += 4 * 64) {
+      u32x4 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + i * 64;
+        a[i] = c < H / 8 ? xv[c] : (u32x4){0u, 0u, 0u, 0u};
+        b[i] = c < H / 8 ? gv[c] : (u32x4){0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          acc += T::to_f32((uint16_t)a[i][v]) * T::to_f32((uint16_t)b[i][v]);
+          acc += T::to_f32((uint16_t)(a[i][v] >> 16)) * T::to_f32((uint16_t)(b[i][v] >> 16));
+        }
+    }
+  } else {
+    for (int h = lane; h < H; h += 64) acc += T::to_f32(xr[h]) * T::to_f32(sgw[h]);
+  }
+  acc = route_wave_sum_f32(acc);
+  return route_sigmoid_t<DT>(T::round1(acc));
+}
+
+}  // namespace mq

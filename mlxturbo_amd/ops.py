@@ -917,16 +917,61 @@ def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
     expert's output ``shared`` ``(T, H)`` merged with its gate.  ``x`` is
     ``(T, H)``, ``logits`` float32 ``(T, E)``; ``gate``, ``up``, ``down``
     are ``(w, scales, biases)`` banks.  Returns ``(T, H_out)``: the same
-    bits as calling the three steps one by one."""
+    bits as calling the three steps one by one.  Up to 64 (token, expert)
+    pairs over up to 512 experts the routing runs inside the gate+up
+    launch (mq_moe_glu_route), one launch less on the dependent chain."""
     if (sgw is None) != (shared is None):
         raise ValueError("sgw and shared are given together")
     T, H = x.shape
-    idx, wts, sg = moe_route(logits, top_k, x, sgw) if sgw is not None else \
-        moe_route(logits, top_k)
-    h = gather_glu(x.reshape(T, 1, 1, H), *gate, *up, rhs_indices=idx, group_size=group_size,
-                   bits=bits)                                      # (T, k, 1, I)
+    routed = _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits)
+    if routed is not None:
+        h, idx, wts, sg = routed
+    else:
+        idx, wts, sg = moe_route(logits, top_k, x, sgw) if sgw is not None else \
+            moe_route(logits, top_k)
+        h = gather_glu(x.reshape(T, 1, 1, H), *gate, *up, rhs_indices=idx,
+                       group_size=group_size, bits=bits)           # (T, k, 1, I)
     return gather_qmm_combine(h, *down, idx, wts, group_size=group_size, bits=bits,
                               sgate=sg, shared=shared)
+
+
+def _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits):
+    """Routing and the fused gate+up+SiLU in one launch (mq_moe_glu_route:
+    the same bits as moe_route then gather_glu), or None where that launch
+    does not apply (more than 64 pairs or 512 experts, other formats)."""
+    T, H = x.shape
+    (wg, sg_, bg), (wu, su, bu) = gate, up
+    E = logits.shape[-1]
+    if (x.dtype not in (torch.bfloat16, torch.float16) or logits.dtype != torch.float32
+            or tuple(logits.shape) != (T, E) or T * top_k > 64 or E > 512 or top_k > E
+            or bits not in (4, 8) or bg is None or bu is None
+            or wg.ndim != 3 or wg.shape != wu.shape or wg.shape[0] != E
+            or sg_.dtype != x.dtype or su.dtype != x.dtype
+            or (sgw is not None and sgw.dtype != x.dtype)):
+        return None
+    _require_gpu(x, logits, wg, sg_, bg, wu, su, bu, sgw)
+    N = wg.shape[1]
+    K = _check_quant(wg, sg_, bg, group_size, bits)
+    _check_quant(wu, su, bu, group_size, bits)
+    if K != H:
+        raise ValueError(f"x last dimension {H} does not match the quantized weight K={K}")
+    dev = x.device
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    sgate = torch.empty((T, 1), dtype=x.dtype, device=dev) if sgw is not None else None
+    h = torch.empty((T, top_k, 1, N), dtype=x.dtype, device=dev)
+    x_ = _aligned(x.contiguous())
+    lg = logits.contiguous()
+    g_ = sgw.reshape(-1).contiguous() if sgw is not None else None
+    banks = [_aligned(t) for t in (wg, sg_, bg, wu, su, bu)]
+    rc = _lib.lib().mq_moe_glu_route(x_.data_ptr(), lg.data_ptr(),
+                                     *[t.data_ptr() for t in banks], _ptr(g_), idx.data_ptr(),
+                                     wts.data_ptr(), _ptr(sgate), h.data_ptr(), T, top_k, N, K,
+                                     E, group_size, bits, _DTYPE_CODE[x.dtype], _stream_ptr(h))
+    if rc == _EUNSUPPORTED:
+        return None
+    _lib.check(rc, "moe_glu_route")
+    return h, idx, wts, sgate
 
 
 def launch_count() -> int:

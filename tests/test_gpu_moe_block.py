@@ -10,7 +10,9 @@ Checked at config-4 size (512 experts, top-8, hidden 2048, intermediate
 steps called one by one, bit for bit; the routing equals the oracle's
 exactly; each step meets the oracle on the previous step's GPU output (the
 GLU and the down projection at the matmul tolerance, the combine with the
-shared merge bit for bit); launch counts (3 launches at T <= 2, 4 above).
+shared merge bit for bit); the routing inside the gate+up launch gives the
+routing kernel's and the GLU gather's bits; launch counts (2 launches at
+T <= 2, 3 above).
 """
 
 import numpy as np
@@ -56,7 +58,9 @@ def test_moe_block(banks, T, with_shared):
     before = mq.launch_count()
     out = ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
     launches = mq.launch_count() - before
-    assert launches == (3 if T * TOP <= 16 else 4)
+    # routing inside the gate+up launch, then the folded down (T <= 2) or
+    # the down gather and the combine
+    assert launches == (2 if T * TOP <= 16 else 3)
     assert out.shape == (T, H)
 
     # the three steps one by one
@@ -64,6 +68,14 @@ def test_moe_block(banks, T, with_shared):
     h = ops.gather_glu(x.reshape(T, 1, 1, H), *gate, *up, rhs_indices=idx)
     want = ops.gather_qmm_combine(h, *down, idx, w, sgate=sg, shared=shared)
     np.testing.assert_array_equal(bits16(out), bits16(want))
+    # the routed launch's own outputs are the two launches' bits
+    h2, idx2, w2, sg2 = ops._glu_routed(x, logits, TOP, gate, up, sgw, 64, 4)
+    assert torch.equal(idx2, idx) and torch.equal(w2, w)
+    np.testing.assert_array_equal(bits16(h2), bits16(h))
+    if with_shared:
+        np.testing.assert_array_equal(bits16(sg2), bits16(sg))
+    else:
+        assert sg2 is None
 
     # against the oracle, each step from the previous step's GPU output
     ridx, rw, rsg = O.moe_route_ref(logits_np, TOP, xh if with_shared else None,
@@ -86,3 +98,41 @@ def test_moe_block(banks, T, with_shared):
                             sgate=bits16(sg).reshape(-1) if with_shared else None,
                             shared=sh_np if with_shared else None)
     np.testing.assert_array_equal(bits16(out), O.from_f32(ref, "bfloat16"))
+
+
+@pytest.mark.parametrize("E_, top, T", [(64, 4, 16), (512, 8, 8), (100, 2, 3), (512, 1, 1)])
+def test_routed_glu_matches_route_then_glu(E_, top, T):
+    """Other expert counts, top-k widths and token counts (up to 64 pairs),
+    logits with ties (quantized to quarters): mq_moe_glu_route equals
+    mq_moe_route then mq_gather_glu, bit for bit, routing and output."""
+    rng = np.random.default_rng(E_ + top + T)
+    K, N = 512, 256
+    def bank():
+        w, s, b = quantized(rng, E_ * N, K)
+        return (to_dev(w).view(E_, N, -1), to_dev(s, "bfloat16").view(E_, N, -1),
+                to_dev(b, "bfloat16").view(E_, N, -1))
+    gate, up = bank(), bank()
+    x = to_dev(act(rng, (T, K)), "bfloat16")
+    logits = torch.from_numpy((np.round(rng.standard_normal((T, E_)) * 4) / 4)
+                              .astype(np.float32)).cuda()
+    sgw = to_dev(act(rng, (K,), scale=0.02), "bfloat16")
+    got = ops._glu_routed(x, logits, top, gate, up, sgw, 64, 4)
+    assert got is not None
+    h2, idx2, w2, sg2 = got
+    idx, w, sg = ops.moe_route(logits, top, x, sgw)
+    h = ops.gather_glu(x.reshape(T, 1, 1, K), *gate, *up, rhs_indices=idx)
+    assert torch.equal(idx2, idx) and torch.equal(w2, w)
+    np.testing.assert_array_equal(bits16(sg2), bits16(sg))
+    np.testing.assert_array_equal(bits16(h2), bits16(h))
+
+
+def test_routed_glu_declines_beyond_its_range():
+    """More than 64 pairs or 512 experts: the block composes the launches."""
+    rng = np.random.default_rng(5)
+    E_, K, N = 600, 256, 128
+    w, s, b = quantized(rng, E_ * N, K)
+    bank = (to_dev(w).view(E_, N, -1), to_dev(s, "bfloat16").view(E_, N, -1),
+            to_dev(b, "bfloat16").view(E_, N, -1))
+    x = to_dev(act(rng, (2, K)), "bfloat16")
+    logits = torch.from_numpy(rng.standard_normal((2, E_)).astype(np.float32)).cuda()
+    assert ops._glu_routed(x, logits, 8, bank, bank, None, 64, 4) is None
