@@ -146,10 +146,18 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
     if constexpr (ROUTE) {
       // token tok routed by wave tok % NW (pair p = tok * top_k + rank r
       // takes lane r's expert), the pairs' experts met in LDS; in
-      // workgroup 0 the routing wave also writes the token's routing and
-      // shared gate
+      // workgroup 0 the routing wave also writes the token's routing, and
+      // wave (tok + NW / 2) % NW the token's shared gate, so that with few
+      // tokens the gate's loads and dot run beside the top-k instead of
+      // after it (the rest of the grid waits for workgroup 0's last wave)
       const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
       const bool writer = blockIdx.x == 0;
+      if (writer && ra.sgw != nullptr) {
+        for (int tok = (wv + NW / 2) % NW; tok < B; tok += NW) {
+          const uint16_t g = route_wave_shared_gate<DT>(x + (int64_t)tok * K, ra.sgw, K, lane);
+          if (lane == 0) ra.sgate[tok] = g;
+        }
+      }
       for (int tok = wv; tok < B; tok += NW) {
         int sel_e;
         float sel_v;
@@ -160,10 +168,6 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
           if (lane < ra.top_k) {
             ra.idx[tok * ra.top_k + lane] = sel_e;
             ra.w[tok * ra.top_k + lane] = wgt;
-          }
-          if (ra.sgw != nullptr) {
-            const uint16_t g = route_wave_shared_gate<DT>(x + (int64_t)tok * K, ra.sgw, K, lane);
-            if (lane == 0) ra.sgate[tok] = g;
           }
         }
       }

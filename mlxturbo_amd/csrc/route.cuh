@@ -84,22 +84,35 @@ __device__ __forceinline__ bool route_key_before(uint32_t kx, int ix, uint32_t k
 }
 
 // The top_k experts of one row of E float logits, by one whole wave: lane l
-// holds experts l, l + 64, ... (NK of them, NK the power of two covering E /
-// 64) as order-preserving keys, sorts them once with a bitonic network, and
-// each round is two wave reductions over the lanes' heads (the largest key,
-// then the smallest expert holding it), after which the winning lane drops
-// its head.  Lane r < top_k gets round r's expert and logit.
+// holds experts NK l .. NK l + NK - 1 (NK the power of two covering E / 64;
+// 16-byte loads where the lane's block is whole and aligned) as
+// order-preserving keys, sorts them once with a bitonic network, and each
+// round is one wave reduction over the lanes' heads (the largest key) and a
+// ballot: a lane's experts are one contiguous block, so the lowest lane
+// whose head holds that key holds the smallest such expert.  That lane drops
+// its head.  Lane r < top_k gets round r's expert and logit (expert -1 for a
+// round with no expert left: E < top_k, or logits whose key is 0).
 template <int NK>
 __device__ __forceinline__ void route_wave_topk(const float* __restrict__ lr, int E, int top_k,
                                                 int lane, int& sel_e, float& sel_v) {
   uint32_t key[NK];
-  int slot[NK];                                 // expert = lane + 64 slot
+  int slot[NK];                                 // expert = NK lane + slot
+  const int e0 = NK * lane;
+  bool vec = false;
+  if constexpr (NK % 4 == 0) vec = e0 + NK <= E && ((uintptr_t)lr & 15u) == 0;
+  if (vec) {
 #pragma unroll
-  for (int j = 0; j < NK; ++j) {
-    const int e = lane + 64 * j;
-    key[j] = e < E ? route_order_key(lr[e]) : 0u;
-    slot[j] = j;
+    for (int q = 0; q < NK / 4; ++q) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(lr + e0 + 4 * q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) key[4 * q + i] = route_order_key(v[i]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NK; ++j) key[j] = e0 + j < E ? route_order_key(lr[e0 + j]) : 0u;
   }
+#pragma unroll
+  for (int j = 0; j < NK; ++j) slot[j] = j;
   // bitonic sort of the lane's NK keys, descending in route_key_before order
 #pragma unroll
   for (int k = 2; k <= NK; k <<= 1)
@@ -124,20 +137,23 @@ __device__ __forceinline__ void route_wave_topk(const float* __restrict__ lr, in
   for (int r = 0; r < top_k; ++r) {
     // the lane's head is its best remaining expert (ties: smaller expert)
     const uint32_t mk = route_wave_reduce_u32<true>(key[0]);
-    const uint32_t cand =
-        (key[0] == mk && mk != 0u) ? (uint32_t)(lane + 64 * slot[0]) : 0xffffffffu;
-    const uint32_t win = route_wave_reduce_u32<false>(cand);
-    if ((int)win % 64 == lane) {
+    const uint64_t held = __builtin_amdgcn_ballot_w64(key[0] == mk && mk != 0u);
+    int win = -1;
+    if (held != 0) {
+      const int wl = __builtin_ctzll(held);
+      win = NK * wl + __builtin_amdgcn_readlane(slot[0], wl);
+      if (lane == wl) {
 #pragma unroll
-      for (int j = 0; j + 1 < NK; ++j) {
-        key[j] = key[j + 1];
-        slot[j] = slot[j + 1];
+        for (int j = 0; j + 1 < NK; ++j) {
+          key[j] = key[j + 1];
+          slot[j] = slot[j + 1];
+        }
+        key[NK - 1] = 0u;
       }
-      key[NK - 1] = 0u;
     }
     if (lane == r) {
       sel_v = route_from_key(mk);
-      sel_e = (int)win;
+      sel_e = win;
     }
   }
 }

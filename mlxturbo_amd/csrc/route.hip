@@ -13,15 +13,16 @@
 // CDNA4 design: one workgroup of two waves per row, each piece one whole
 // wave (csrc/route.cuh, shared with the decode GLU gather that routes its
 // own tokens, so both give the same bits).  Wave 0 runs the top-k: lane l
-// holds experts l, l + 64, ... (NK per lane, the power of two covering E /
-// 64, up to 16 for E <= 1024) as order-preserving integer keys, sorts them
-// once with a bitonic network, and each round is two DPP wave reductions
-// over the lanes' heads (the largest key, then the smallest expert holding
-// it) after which the winning lane drops its head, no barrier.  (A
-// lane-local argmax per round made each round one long dependent chain: 3.2
-// us for eight rounds.)  Wave 1 computes the shared gate's dot product (16-
-// byte loads, four per lane in flight, one DPP wave sum).  Latency-bound:
-// bytes per row 4 E + 4 H (x and the gate weight, 16-bit) plus 8 top_k out.
+// holds the contiguous block of experts NK l .. NK l + NK - 1 (NK the power
+// of two covering E / 64, up to 16 for E <= 1024) as order-preserving
+// integer keys, sorts them once with a bitonic network, and each round is
+// one DPP wave reduction over the lanes' heads (the largest key) and a
+// ballot (the lowest lane holding it holds the smallest such expert), after
+// which the winning lane drops its head, no barrier.  (A lane-local argmax
+// per round made each round one long dependent chain: 3.2 us for eight
+// rounds.)  Wave 1 computes the shared gate's dot product (16-byte loads,
+// four per lane in flight, one DPP wave sum).  Latency-bound: bytes per row
+// 4 E + 4 H (x and the gate weight, 16-bit) plus 8 top_k out.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
