@@ -219,6 +219,26 @@ int mq_gather_qmm_tables(const void* x, const uint32_t* w, const void* scales,
                          const void* tables, size_t tables_bytes, void* hip_stream);
 
 /*
+ * A prefill MoE layer's gate and up gathers and its SwiGLU in one launch,
+ * over tables from mq_gather_tables (same conditions as
+ * mq_gather_qmm_tables): out [P * M, N] = mq_swiglu of mq_gather_qmm_tables
+ * on the gate bank and on the up bank (both of N x K), bit for bit, with
+ * each gathered x tile read once for both banks.  The reference's prefill
+ * layer runs the gate and up grouped GEMMs over its shared tables and then
+ * the activation (fused.py:3294-3302, kernels/moe_grouped_gemm.py:
+ * 913-1066); mlx-lm's SwitchGLU applies it as nn.silu(gate) * up.  Calls the
+ * tables' kernel does not take return MQ_EUNSUPPORTED, and the caller makes
+ * the three calls.
+ */
+int mq_gather_swiglu_tables(const void* x, const uint32_t* w_gate, const void* scales_gate,
+                            const void* biases_gate, const uint32_t* w_up, const void* scales_up,
+                            const void* biases_up, const int32_t* lhs_indices,
+                            const int32_t* rhs_indices, void* out, int64_t P, int64_t B,
+                            int64_t M, int64_t N, int64_t K, int64_t E, int group_size, int bits,
+                            int dtype, const void* tables, size_t tables_bytes,
+                            void* hip_stream);
+
+/*
  * The decode MoE block's routing and fused gate+up+SiLU in one launch:
  * mq_moe_route(logits, idx, weights, T, E, top_k, x, sgw, sgate, K, dtype)
  * followed by mq_gather_glu(x [T, 1, K], gate bank, up bank, lhs NULL, rhs

@@ -37,6 +37,7 @@ EXPORTED = (
     "mq_gather_qmm_noalloc",
     "mq_gather_tables",
     "mq_gather_qmm_tables",
+    "mq_gather_swiglu_tables",
     "mq_swiglu",
     "mq_moe_glu_route",
     "mq_gather_glu",
@@ -93,6 +94,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_gather_qmm_tables.restype = _int
     lib.mq_gather_qmm_tables.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                          _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]
+    lib.mq_gather_swiglu_tables.restype = _int
+    lib.mq_gather_swiglu_tables.argtypes = [_vp] * 10 + [_i64] * 6 + [_int, _int, _int, _vp,
+                                                                      _sz, _vp]
     lib.mq_moe_glu_route.restype = _int
     lib.mq_moe_glu_route.argtypes = [_vp] * 13 + [_i64] * 5 + [_int, _int, _int, _vp]
     lib.mq_swiglu.restype = _int

@@ -147,7 +147,7 @@ int moe_combine_checked(const void* y, int64_t y_rows, const int32_t* inv, const
 
 extern "C" {
 
-int mq_version(void) { return 5; }
+int mq_version(void) { return 6; }
 
 const char* mq_last_error(void) { return g_last_error.c_str(); }
 
@@ -378,6 +378,47 @@ int mq_gather_qmm_tables(const void* x, const uint32_t* w, const void* scales,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail((int)e, "gather_qmm_tables: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
+int mq_gather_swiglu_tables(const void* x, const uint32_t* w_gate, const void* scales_gate,
+                            const void* biases_gate, const uint32_t* w_up, const void* scales_up,
+                            const void* biases_up, const int32_t* lhs_indices,
+                            const int32_t* rhs_indices, void* out, int64_t P, int64_t B,
+                            int64_t M, int64_t N, int64_t K, int64_t E, int group_size, int bits,
+                            int dtype, const void* tables, size_t tables_bytes,
+                            void* hip_stream) {
+  int rc = check_common(w_gate, scales_gate, biases_gate, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  rc = check_common(w_up, scales_up, biases_up, N, K, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !out || !rhs_indices || !tables)
+    return fail(MQ_EINVAL, "x, out, rhs_indices and tables must be non-null");
+  if (P < 1 || M < 1 || E < 1 || B < 1)
+    return fail(MQ_EINVAL, "invalid sizes P=%lld M=%lld E=%lld B=%lld", (long long)P,
+                (long long)M, (long long)E, (long long)B);
+  if (!lhs_indices && P % B)
+    return fail(MQ_EINVAL, "lhs_indices=NULL requires B to divide P (B=%lld P=%lld)",
+                (long long)B, (long long)P);
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (N > INT32_MAX || K > INT32_MAX || P > INT32_MAX || M > 16 ||
+      !mq::gather_thin_path(P, M, K, E))
+    return fail(MQ_EUNSUPPORTED, "this gather does not run on the tables' kernel");
+  if (tables_bytes < mq::gather_workspace_bytes(P, M))
+    return fail(MQ_EINVAL, "tables too small: need %zu bytes", mq::gather_workspace_bytes(P, M));
+  if (!aligned16(x)) return fail(MQ_EINVAL, "x must be 16-byte aligned");
+  if (N == 0) return MQ_OK;
+  int nl = 0;
+  rc = dispatch_16<mq::SwigluTablesLaunch>(dtype, bits, group_size, x, w_gate, scales_gate,
+                                           biases_gate, w_up, scales_up, biases_up, lhs_indices,
+                                           out, P, B, M, N, K, E, tables,
+                                           reinterpret_cast<hipStream_t>(hip_stream), &nl);
+  if (rc) return fail(rc, "gather_swiglu_tables: no kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail((int)e, "gather_swiglu_tables: launch failed: %s", hipGetErrorString(e));
   g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
   return MQ_OK;
 }

@@ -533,15 +533,15 @@ inline int launch_grouped_bm(const void* x, const uint32_t* w, const void* s, co
   return 0;
 }
 
-// Prefill gather_qmm with thin experts: the register-B grouped kernel
-// (grouped.cuh) over two-class tables (launch_thin_tables: segments of R =
-// 64 / M pairs, and of 2 R for experts with more than R pairs), built here
-// unless the caller built them for this routing already (prepped).
-template <int DT, int BITS, int GS>
-inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, const void* b,
-                               const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
-                               int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
-                               hipStream_t st, int* nlaunch, bool prepped) {
+// The thin grouped kernel (grouped.cuh) over two-class tables already built
+// in ws (launch_thin_tables: segments of R = 64 / M pairs, and of 2 R for
+// experts with more than R pairs).  GLU: gate bank (w, s, b) and up bank
+// (w2, s2, b2), out = SwiGLU of the two gathers (N columns).
+template <int DT, int BITS, int GS, bool GLU>
+inline int launch_thin_kernel(const void* x, const uint32_t* w, const void* s, const void* b,
+                              const uint32_t* w2, const void* s2, const void* b2,
+                              const int32_t* lhs, void* out, int64_t P, int64_t B, int64_t M,
+                              int64_t N, int64_t K, int64_t E, const void* ws, hipStream_t st) {
   const int R = (int)(kThinBM / M);
   // 4 waves (256 columns) per workgroup at short K, 8 (512 columns, so each
   // x tile serves twice the columns) above K = 1024: config-4 banks, 2048
@@ -550,17 +550,14 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
   // against 302 / 253 for the size-class wide tiles and 282 / 264 with 16
   // waves (whose 128-register budget spills)
   const int nwv = K <= 1024 ? 4 : 8;
-  const int64_t ncol = (N + 64 * nwv - 1) / (64 * nwv);
+  const int64_t bn = (GLU ? 32 : 64) * nwv;     // output columns per tile
+  const int64_t ncol = (N + bn - 1) / bn;
   // 8 waves: experts with more than 64 rows take 128-row tiles, which read
   // their weights once per 128 rows (the workgroup's register budget
   // already holds one workgroup per CU, so the taller tile costs no
   // occupancy).  4 waves run those segments as two 64-row tiles (128-row
   // tiles with 4 waves: config-4 down 261 against 176 us zipf), the same
   // work as one-class tables, so one table build serves both widths.
-  if (!prepped) {
-    if (int rc = launch_thin_tables(rhs, lhs, P, E, B, M, ws, st)) return rc;
-    *nlaunch += kPrepLaunches;
-  }
   const int64_t h1 = nwv == 4 ? 2 : 1;
   int64_t nwg = 0;
   for (const int64_t sb : {h1 * class_seg_bound(P, 2 * R, R + 1, E), class_seg_bound(P, R, 0, E)})
@@ -568,13 +565,32 @@ inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, 
   if (nwg > INT32_MAX) return kStatusUnsupported;
   const dim3 grid((unsigned)nwg);
 #define MQ_THIN(NWV, HALVES)                                                                    \
-  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV, true, HALVES>), grid,       \
+  hipLaunchKernelGGL((qmm_grouped_thin_kernel<DT, BITS, GS, 2, NWV, true, HALVES, GLU>), grid,  \
                      dim3(64 * NWV), 0, st, (const uint16_t*)x, w, (const uint16_t*)s,           \
-                     (const uint16_t*)b, lhs, (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, \
-                     (int)M, (int)N, (int)K, (int)E, 0)
+                     (const uint16_t*)b, w2, (const uint16_t*)s2, (const uint16_t*)b2, lhs,      \
+                     (uint16_t*)out, (const int32_t*)ws, (int)P, (int)B, (int)M, (int)N, (int)K, \
+                     (int)E, 0)
   if (nwv == 4) MQ_THIN(4, true);
   else MQ_THIN(8, false);
 #undef MQ_THIN
+  return 0;
+}
+
+// Prefill gather_qmm with thin experts: the register-B grouped kernel over
+// two-class tables, built here unless the caller built them for this
+// routing already (prepped).
+template <int DT, int BITS, int GS>
+inline int launch_grouped_thin(const void* x, const uint32_t* w, const void* s, const void* b,
+                               const int32_t* lhs, const int32_t* rhs, void* out, int64_t P,
+                               int64_t B, int64_t M, int64_t N, int64_t K, int64_t E, void* ws,
+                               hipStream_t st, int* nlaunch, bool prepped) {
+  if (!prepped) {
+    if (int rc = launch_thin_tables(rhs, lhs, P, E, B, M, ws, st)) return rc;
+    *nlaunch += kPrepLaunches;
+  }
+  if (int rc = launch_thin_kernel<DT, BITS, GS, false>(x, w, s, b, nullptr, nullptr, nullptr, lhs,
+                                                       out, P, B, M, N, K, E, ws, st))
+    return rc;
   *nlaunch += 1;
   return 0;
 }
@@ -751,6 +767,21 @@ int GluLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const void* 
                                                N, K, E, ws, st, nlaunch);
 }
 
+
+template <int DT, int BITS, int GS>
+int SwigluTablesLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const void* sg,
+                                          const void* bg, const uint32_t* wu, const void* su,
+                                          const void* bu, const int32_t* lhs, void* out,
+                                          int64_t P, int64_t B, int64_t M, int64_t N, int64_t K,
+                                          int64_t E, const void* tables, hipStream_t st,
+                                          int* nlaunch) {
+  if (!gather_thin_path(P, M, K, E)) return kStatusUnsupported;
+  if (int rc = launch_thin_kernel<DT, BITS, GS, true>(x, wg, sg, bg, wu, su, bu, lhs, out, P, B,
+                                                      M, N, K, E, tables, st))
+    return rc;
+  *nlaunch += 1;
+  return 0;
+}
 
 template <int DT, int BITS, int GS>
 int GatherFoldLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,

@@ -42,13 +42,21 @@ constexpr int kThinBM = 64;
 // batch x_batch(lhs, p, P, B)) x weight columns [64 NWV col, +64 NWV), 64 NWV
 // threads.  Segments of out-of-range experts write zeros.  K % 64 == 0,
 // B * Mi * K * 2 < 2^31.
-template <int DT, int BITS, int GS, int PS, int NWV, int BM>
+// GLU: (w, scales, biases) is the gate bank and (w2, scales2, biases2) the
+// up bank of the same shape; the tile owns output columns [32 NWV col,
+// +32 NWV), wave w's two 32-column blocks are the gate and the up rows of
+// columns 32 w .. 32 w + 31, and out = swiglu_t(T(gate), T(up)): the two
+// gathers and the SwiGLU pass, bit for bit, with each x tile read once for
+// both banks.
+template <int DT, int BITS, int GS, int PS, int NWV, int BM, bool GLU = false>
 __device__ __forceinline__ void thin_tile(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E, int seg, int col, int pofs) {
-  constexpr int BN = 64 * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
+    const uint32_t* __restrict__ w2, const uint16_t* __restrict__ scales2,
+    const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
+    uint16_t* __restrict__ out, const int32_t* __restrict__ ws, int P, int B, int Mi, int N,
+    int K, int E, int seg, int col, int pofs) {
+  constexpr int BN = (GLU ? 32 : 64) * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
   constexpr int MB = BM / 32;                   // 32-row blocks of the tile
   static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
   constexpr int XT = BM * 8;                    // 16-byte x pieces per step
@@ -76,14 +84,19 @@ __device__ __forceinline__ void thin_tile(
   const int64_t Kw = (int64_t)K * BITS / 32;    // words per weight row
   const int64_t wrow = (int64_t)(valid ? e : 0) * N + n0;
   // columns past ncols are past these ranges and read zeros (never stored)
-  const auto rw = wide_rsrc(w + wrow * Kw, (int64_t)ncols * Kw * 4);
-  const auto rs = wide_rsrc(scales + wrow * G, (int64_t)ncols * G * 2);
-  const auto rb = wide_rsrc(biases + wrow * G, (int64_t)ncols * G * 2);
+  __amdgpu_buffer_rsrc_t rw[2], rs[2], rb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const bool up = GLU && j == 1;
+    rw[j] = wide_rsrc((up ? w2 : w) + wrow * Kw, (int64_t)ncols * Kw * 4);
+    rs[j] = wide_rsrc((up ? scales2 : scales) + wrow * G, (int64_t)ncols * G * 2);
+    rb[j] = wide_rsrc((up ? biases2 : biases) + wrow * G, (int64_t)ncols * G * 2);
+  }
   const auto xr = wide_rsrc(x, (int64_t)B * Mi * K * 2);
   uint32_t wo[2], so[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int c = 64 * wave + 32 * j + lr;
+    const int c = GLU ? 32 * wave + lr : 64 * wave + 32 * j + lr;
     wo[j] = (uint32_t)(c * Kw * 4) + (uint32_t)h * 16u * WB;
     so[j] = (uint32_t)c * (uint32_t)G * 2u;
   }
@@ -110,8 +123,8 @@ __device__ __forceinline__ void thin_tile(
     const uint32_t bo = 16u * (uint32_t)(kt * BK / GS / 8);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      ns[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, so[j] + bo, 0, 0);
-      nb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, so[j] + bo, 0, 0);
+      ns[j] = __builtin_amdgcn_raw_buffer_load_b128(rs[j], so[j] + bo, 0, 0);
+      nb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb[j], so[j] + bo, 0, 0);
     }
   };
   auto xload = [&](Stage& st, int kt) {
@@ -126,11 +139,11 @@ __device__ __forceinline__ void thin_tile(
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int q = 0; q < WB; ++q)
-        st.wv[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[j] + 16u * q, k0 * BITS / 8, 0);
+        st.wv[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rw[j], wo[j] + 16u * q, k0 * BITS / 8, 0);
       if (per_step) {
         const uint32_t go = so[j] + 2u * (uint32_t)((k0 + 32 * h) / GS);
-        st.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
-        st.b[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+        st.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs[j], go, 0, 0);
+        st.b[j] = __builtin_amdgcn_raw_buffer_load_b16(rb[j], go, 0, 0);
       }
     }
   };
@@ -306,17 +319,30 @@ __device__ __forceinline__ void thin_tile(
   }
 
   // D[row][col] of a 32x32 tile: col = lane & 31, row = 8*(e/4) + 4*(lane>>5) + e%4
+  if constexpr (GLU) {
+    const int c = 32 * wave + lr;
 #pragma unroll
-  for (int i = 0; i < MB; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = 64 * wave + 32 * j + lr;
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int r = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
-        if (r < rows && c < ncols) out[(int64_t)s_orow[r] * N + n0 + c] = T::round1(acc[i][j][q]);
+        if (r < rows && c < ncols)
+          out[(int64_t)s_orow[r] * N + n0 + c] =
+              swiglu_t<DT>(T::round1(acc[i][0][q]), T::round1(acc[i][1][q]));
       }
-    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = 64 * wave + 32 * j + lr;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int r = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
+          if (r < rows && c < ncols) out[(int64_t)s_orow[r] * N + n0 + c] = T::round1(acc[i][j][q]);
+        }
+      }
+  }
 }
 
 // 1-D grid, 64 NWV threads, tiles placed by grouped_tile.  CLS2 false: the
@@ -328,14 +354,18 @@ __device__ __forceinline__ void thin_tile(
 // tile made the 64-row ones slower).  HALVES: class 1's segments run as two
 // 64-row tiles each (first and second 64 / Mi pairs, adjacent tiles), the
 // work of one-class tables, from the same two-class tables.
-template <int DT, int BITS, int GS, int PS, int NWV, bool CLS2, bool HALVES = false>
+template <int DT, int BITS, int GS, int PS, int NWV, bool CLS2, bool HALVES = false,
+          bool GLU = false>
 __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const int32_t* __restrict__ lhs, uint16_t* __restrict__ out, const int32_t* __restrict__ ws,
-    int P, int B, int Mi, int N, int K, int E, int cls) {
+    const uint32_t* __restrict__ w2, const uint16_t* __restrict__ scales2,
+    const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
+    uint16_t* __restrict__ out, const int32_t* __restrict__ ws, int P, int B, int Mi, int N,
+    int K, int E, int cls) {
   const int32_t* hdr = ws + gather_ws_header(P);
-  const int ncol = (N + 64 * NWV - 1) / (64 * NWV);
+  constexpr int BN = (GLU ? 32 : 64) * NWV;     // output columns per tile
+  const int ncol = (N + BN - 1) / BN;
   int bi = blockIdx.x;
   constexpr int H1 = HALVES ? 2 : 1;           // tiles per class-1 segment
   if constexpr (CLS2) {
@@ -351,14 +381,15 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
   int seg, col;
   if (!grouped_tile(bi, nv, ncol, seg, col)) return;
   if (CLS2 && cls == 1 && !HALVES)
-    thin_tile<DT, BITS, GS, PS, NWV, 128>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
-                                           seg + s0, col, 0);
+    thin_tile<DT, BITS, GS, PS, NWV, 128, GLU>(x, w, scales, biases, w2, scales2, biases2, lhs,
+                                                out, ws, P, B, Mi, N, K, E, seg + s0, col, 0);
   else if (CLS2 && cls == 1)
-    thin_tile<DT, BITS, GS, PS, NWV, 64>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
-                                          (seg >> 1) + s0, col, (seg & 1) * (64 / Mi));
+    thin_tile<DT, BITS, GS, PS, NWV, 64, GLU>(x, w, scales, biases, w2, scales2, biases2, lhs,
+                                               out, ws, P, B, Mi, N, K, E, (seg >> 1) + s0, col,
+                                               (seg & 1) * (64 / Mi));
   else
-    thin_tile<DT, BITS, GS, PS, NWV, 64>(x, w, scales, biases, lhs, out, ws, P, B, Mi, N, K, E,
-                                          seg + s0, col, 0);
+    thin_tile<DT, BITS, GS, PS, NWV, 64, GLU>(x, w, scales, biases, w2, scales2, biases2, lhs,
+                                               out, ws, P, B, Mi, N, K, E, seg + s0, col, 0);
 }
 
 }  // namespace mq

@@ -1,8 +1,8 @@
 // Kernel instantiations of one (dtype, bits) pair for every group size.  The
 // build compiles this file once per pair with -DMQ_INST_DT=<0|1> and
 // -DMQ_INST_BITS=<4|8>, and once more per pair with -DMQ_INST_GLU for the
-// fused gate+up and folded down + combine kernels; abi.hip calls the
-// launchers through launch.h.
+// fused gate+up kernels (decode, and prefill with SwiGLU) and the folded
+// down + combine kernel; abi.hip calls the launchers through launch.h.
 #include "launch.h"
 #include "dequant.cuh"
 #include "gather.cuh"
@@ -19,7 +19,8 @@ namespace mq {
 #define MQ_INST(GS)                                                  \
   template struct GluLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;           \
   template struct GluRouteLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;      \
-  template struct GatherFoldLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
+  template struct GatherFoldLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;   \
+  template struct SwigluTablesLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
 #else
 #define MQ_INST(GS)                                                  \
   template struct DequantLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;       \

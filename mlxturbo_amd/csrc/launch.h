@@ -94,6 +94,20 @@ struct GluRouteLaunch {
                  int* nlaunch);
 };
 
+// A prefill MoE layer's gate and up gathers and its SwiGLU pass in one launch
+// (grouped.cuh, GLU thin tiles) over the tables launch_thin_tables built for
+// this routing in `tables`: per pair row, out [P * M, N] = swiglu_t(T(x .
+// Wg^T), T(x . Wu^T)), bit for bit the two gathers over the tables followed
+// by launch_swiglu.  kStatusUnsupported where the thin kernel does not run
+// (gather_thin_path).
+template <int DT, int BITS, int GS>
+struct SwigluTablesLaunch {
+  static int run(const void* x, const uint32_t* wg, const void* sg, const void* bg,
+                 const uint32_t* wu, const void* su, const void* bu, const int32_t* lhs,
+                 void* out, int64_t P, int64_t B, int64_t M, int64_t N, int64_t K, int64_t E,
+                 const void* tables, hipStream_t st, int* nlaunch);
+};
+
 // Down projection with the MoE combine folded in (gather.cuh), decode widths:
 // x [T * top_k, K] (one row per pair), rhs and cw (float router weights)
 // [T * top_k], out [T, N] = the combine of mq_moe_combine (inv = NULL) over

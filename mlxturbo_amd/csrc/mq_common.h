@@ -86,6 +86,18 @@ template <> struct T16<kF16> {
   }
 };
 
+// SwiGLU of one gate / up pair of T values: T(T(silu(g)) * u), silu(g) =
+// g / (1 + exp(-g)) in float (mlx-lm's SwitchGLU: nn.silu on the gate
+// projection times the up projection, each step rounded to T).  The SwiGLU
+// pass (swiglu.hip) and the fused prefill gate/up gather (grouped.cuh) both
+// evaluate it here, so they give the same bits.
+template <int DT>
+__device__ __forceinline__ uint16_t swiglu_t(uint16_t g, uint16_t u) {
+  const float gf = T16<DT>::to_f32(g);
+  const float a = T16<DT>::to_f32(T16<DT>::round1(gf / (1.0f + expf(-gf))));
+  return T16<DT>::round1(a * T16<DT>::to_f32(u));
+}
+
 __device__ __forceinline__ float half_lo(uint32_t v) { return (float)bitcast<f16x2>(v).x; }
 __device__ __forceinline__ float half_hi(uint32_t v) { return (float)bitcast<f16x2>(v).y; }
 

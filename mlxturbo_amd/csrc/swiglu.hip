@@ -5,6 +5,8 @@
 // its grouped GEMM outputs, mlxturbo/fused.py:3302), each of the two steps
 // rounded to T.
 //
+// The value itself is mq_common.h's swiglu_t.
+//
 // HBM-bound: 6 bytes per value (two reads, one write).  One pass, eight
 // values per thread through 16-byte loads and stores where the three arrays
 // are 16-byte aligned, a scalar tail for the last n % 8.
@@ -19,14 +21,6 @@ namespace {
 
 constexpr int kSwigluThreads = 256;
 
-template <int DT>
-__device__ __forceinline__ uint16_t swiglu1(uint16_t g, uint16_t u) {
-  using T = T16<DT>;
-  const float gf = T::to_f32(g);
-  const float a = T::to_f32(T::round1(gf / (1.0f + expf(-gf))));
-  return T::round1(a * T::to_f32(u));
-}
-
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kSwigluThreads) void swiglu_kernel(const uint16_t* __restrict__ g,
                                                                 const uint16_t* __restrict__ u,
@@ -40,15 +34,15 @@ __global__ __launch_bounds__(kSwigluThreads) void swiglu_kernel(const uint16_t* 
     u32x4 hv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = swiglu1<DT>((uint16_t)(gv[e] & 0xffffu), (uint16_t)(uv[e] & 0xffffu));
-      const uint32_t hi = swiglu1<DT>((uint16_t)(gv[e] >> 16), (uint16_t)(uv[e] >> 16));
+      const uint32_t lo = swiglu_t<DT>((uint16_t)(gv[e] & 0xffffu), (uint16_t)(uv[e] & 0xffffu));
+      const uint32_t hi = swiglu_t<DT>((uint16_t)(gv[e] >> 16), (uint16_t)(uv[e] >> 16));
       hv[e] = lo | (hi << 16);
     }
     *reinterpret_cast<u32x4*>(h + i0) = hv;
     return;
   }
   const int64_t i1 = i0 + 8 < n ? i0 + 8 : n;
-  for (int64_t i = i0; i < i1; ++i) h[i] = swiglu1<DT>(g[i], u[i]);
+  for (int64_t i = i0; i < i1; ++i) h[i] = swiglu_t<DT>(g[i], u[i]);
 }
 
 }  // namespace

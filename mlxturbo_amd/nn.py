@@ -154,8 +154,9 @@ class SwitchGLU(torch.nn.Module):
     At prefill widths (1024+ pairs) the layer runs as the reference's prefill
     path does (fused.py:3283-3316): the segment tables are built once for
     the routing and shared by the gate, up and down gathers; the gate and up
-    gathers read x through the token of each pair (no gathered copy of x);
-    the SwiGLU is one pass; the router-weighted sum is one combine.  The
+    gathers read x through the token of each pair (no gathered copy of x)
+    and run with the SwiGLU as one launch (:func:`ops.gather_swiglu`); the
+    router-weighted sum is one combine.  The
     pairs stay in (token, expert) order throughout (the grouped kernels
     group them by expert themselves), so no sort or unsort runs.  Each step
     computes what the sort path computes, bit for bit."""
@@ -201,9 +202,15 @@ class SwitchGLU(torch.nn.Module):
         tables = ops.gather_tables(idx, E)
         if tables is None:
             return None
-        gk = g(xe, idx, tables=tables)                          # (T, k, 1, I)
-        uk = u(xe, idx, tables=tables)
-        h = ops.swiglu(gk, uk)
+        if (g.weight.shape == u.weight.shape and g.scales.dtype == u.scales.dtype
+                and (g.group_size, g.bits, g.mode) == (u.group_size, u.bits, u.mode)):
+            # gate, up and the SwiGLU in one launch where the tables' kernel
+            # takes it (each x tile read once for both banks)
+            h = ops.gather_swiglu(xe, (g.weight, g.scales, g.biases),
+                                  (u.weight, u.scales, u.biases), idx, tables,
+                                  group_size=g.group_size, bits=g.bits, mode=g.mode)
+        else:
+            h = ops.swiglu(g(xe, idx, tables=tables), u(xe, idx, tables=tables))
         y = d(h, idx, tables=tables)                            # (T, k, 1, N)
         T, top_k = idx.shape
         if scores is not None:

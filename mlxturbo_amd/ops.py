@@ -552,6 +552,39 @@ def _tables_launch(a, out, tables: GatherTables, group_size, bits) -> bool:
     return True
 
 
+def gather_swiglu(x: torch.Tensor, gate, up, rhs_indices: torch.Tensor,
+                  tables: GatherTables, transpose: bool = True, group_size: int = 64,
+                  bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """A prefill MoE layer's gate and up projections and its activation:
+    ``swiglu(gather_qmm(x, *gate, rhs_indices=rhs_indices, tables=tables),
+    gather_qmm(x, *up, ...))``, bit for bit, in one launch over the layer's
+    tables where the tables' kernel takes the call
+    (mq_gather_swiglu_tables: each gathered x tile is read once for both
+    banks), else as those three calls.  ``gate`` and ``up`` are
+    ``(w, scales, biases)`` banks of one shape; x reaches pair p through
+    batch ``p / top_k`` (no lhs table), as the tables were built.  The
+    reference runs the gate and up grouped GEMMs over its shared tables and
+    then the activation (fused.py:3294-3302)."""
+    out, a = _gather_prep(x, [tuple(gate), tuple(up)], None, rhs_indices, transpose, group_size,
+                          bits, mode)
+    if a is None:
+        return out
+    if (a["route"] == "kernel" and a["lhs"] is None
+            and (tables.P, tables.M, tables.E) == (a["P"], a["M"], a["E"])):
+        x_ = _aligned(a["x"])
+        rc = _lib.lib().mq_gather_swiglu_tables(
+            x_.data_ptr(), *[t.data_ptr() for t in a["flat"]], None, a["rhs"].data_ptr(),
+            out.data_ptr(), a["P"], a["B"], a["M"], a["N"], a["K"], a["E"], group_size, bits,
+            _DTYPE_CODE[a["x"].dtype], tables.buf.data_ptr(), tables.buf.numel(),
+            _stream_ptr(out))
+        if rc != _EUNSUPPORTED:
+            _lib.check(rc, "gather_swiglu")
+            return out
+    kw = dict(rhs_indices=rhs_indices, transpose=transpose, group_size=group_size, bits=bits,
+              mode=mode, tables=tables)
+    return swiglu(gather_qmm(x, *gate, **kw), gather_qmm(x, *up, **kw))
+
+
 def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """``T(T(silu(gate)) * up)`` elementwise, ``silu(g) = g / (1 + exp(-g))``
     in float: mlx-lm SwitchGLU's activation between a MoE layer's gate / up

@@ -1,16 +1,20 @@
 """The MoE layer at prefill widths as the reference runs it (fused.py:3283-3316):
 one table build per routing shared by the gate, up and down gathers, x read
-through each pair's token, one SwiGLU pass, one combine.
+through each pair's token, the gate and up gathers with the SwiGLU in one
+launch, one combine.
 
 Checked: the SwiGLU kernel against its torch composition bit for bit (bf16,
 fp16, ragged lengths, unaligned views); gathers over shared tables against
 the same gathers building their own, bit for bit, with hot experts (the
 two-row-class tables, whose 128-pair segments the down bank's 4-wave kernel
-runs as two 64-row tiles); the whole layer against the sort path (sorted
-gathers, torch SwiGLU, unsort or combine) bit for bit, at config-4 size
-(2048 tokens x top-8 over 512 experts, hidden 2048, intermediate 512) and
-small banks, zipf and uniform routing; each gather of the layer against the
-oracle on sampled pairs; launch counts (two table kernels per layer).
+runs as two 64-row tiles); the fused gate+up+SwiGLU launch against the two
+gathers and the SwiGLU pass, bit for bit (8- and 4-wave kernels, ragged
+column counts, fp16, 8-bit, out-of-range experts); the whole layer against
+the sort path (sorted gathers, torch SwiGLU, unsort or combine) bit for bit,
+at config-4 size (2048 tokens x top-8 over 512 experts, hidden 2048,
+intermediate 512) and small banks, zipf and uniform routing; each gather of
+the layer against the oracle on sampled pairs; launch counts (two table
+kernels per layer).
 """
 
 import numpy as np
@@ -99,6 +103,61 @@ def test_gathers_over_shared_tables(routing):
         np.testing.assert_array_equal(bits16(got), bits16(want))
 
 
+@pytest.mark.parametrize("E, T, top, H, I, routing, dtype, bits", [
+    (64, 512, 8, 2048, 512, "zipf", "bfloat16", 4),     # 8 waves, 128-row tiles
+    (64, 512, 8, 1024, 256, "uniform", "bfloat16", 4),  # 4 waves, halves
+    (48, 300, 4, 512, 200, "zipf", "bfloat16", 4),      # ragged column tile
+    (64, 512, 8, 2048, 512, "zipf", "float16", 4),
+    (64, 256, 8, 1024, 384, "uniform", "bfloat16", 8),
+])
+def test_gather_swiglu_matches_three_calls(E, T, top, H, I, routing, dtype, bits):
+    """mq_gather_swiglu_tables equals the gate and up gathers over the same
+    tables followed by the SwiGLU pass, bit for bit, in one launch."""
+    rng = np.random.default_rng(E + T + I + bits)
+    banks = []
+    for _ in range(2):
+        w, s, b = random_packed(rng, E * I, H, bits=bits, dtype=dtype)
+        banks.append((to_dev(w).view(E, I, -1), to_dev(s, dtype).view(E, I, -1),
+                      to_dev(b, dtype).view(E, I, -1)))
+    idx = zipf_routing(rng, T, top, E) if routing == "zipf" else \
+        np.stack([rng.choice(E, top, replace=False) for _ in range(T)]).astype(np.int32)
+    rhs = torch.from_numpy(idx).cuda()
+    xe = to_dev(act(rng, (T, 1, 1, H), dtype, scale=0.5), dtype)
+    tables = ops.gather_tables(rhs, E)
+    assert tables is not None
+    kw = dict(group_size=64, bits=bits)
+    before = mq.launch_count()
+    got = ops.gather_swiglu(xe, banks[0], banks[1], rhs, tables, **kw)
+    assert mq.launch_count() == before + 1
+    want = ops.swiglu(ops.gather_qmm(xe, *banks[0], rhs_indices=rhs, tables=tables, **kw),
+                      ops.gather_qmm(xe, *banks[1], rhs_indices=rhs, tables=tables, **kw))
+    assert got.shape == (T, top, 1, I)
+    np.testing.assert_array_equal(bits16(got), bits16(want))
+
+
+def test_gather_swiglu_out_of_range_experts():
+    """Pairs whose expert is outside the bank get zero rows from the fused
+    launch, as from the gathers and the SwiGLU."""
+    rng = np.random.default_rng(3)
+    E, T, top, H, I = 32, 256, 4, 1024, 256
+    banks = []
+    for _ in range(2):
+        w, s, b = random_packed(rng, E * I, H)
+        banks.append((to_dev(w).view(E, I, -1), to_dev(s, "bfloat16").view(E, I, -1),
+                      to_dev(b, "bfloat16").view(E, I, -1)))
+    idx = np.stack([rng.choice(E, top, replace=False) for _ in range(T)]).astype(np.int32)
+    idx[::7, 1] = E + 3
+    idx[::11, 2] = -1
+    rhs = torch.from_numpy(idx).cuda()
+    xe = to_dev(act(rng, (T, 1, 1, H), scale=0.5), "bfloat16")
+    tables = ops.gather_tables(rhs, E)
+    got = ops.gather_swiglu(xe, banks[0], banks[1], rhs, tables)
+    want = ops.swiglu(ops.gather_qmm(xe, *banks[0], rhs_indices=rhs, tables=tables),
+                      ops.gather_qmm(xe, *banks[1], rhs_indices=rhs, tables=tables))
+    np.testing.assert_array_equal(bits16(got), bits16(want))
+    assert not bits16(got)[::7, 1].any() and not bits16(got)[::11, 2].any()
+
+
 def _layer(rng, E, H, I, mlx=False):
     banks = [_bank(rng, E, I, H, mlx), _bank(rng, E, I, H, mlx), _bank(rng, E, H, I, mlx)]
     return [b[0] for b in banks], [b[1] for b in banks]
@@ -110,7 +169,7 @@ def _layer(rng, E, H, I, mlx=False):
     (512, 2048, 8, 2048, 512, "zipf", True),
 ])
 def test_prefill_layer_matches_sort_path(E, T, top, H, I, routing, mlx):
-    """SwitchGLU over shared tables (5 launches + combine) equals the sort
+    """SwitchGLU over shared tables (4 launches + combine) equals the sort
     path (argsorts, gathered x, sorted gathers with their own tables, torch
     SwiGLU, unsort / combine) bit for bit, with and without router scores;
     the gate gather and the down gather of the layer meet the oracle on
@@ -126,12 +185,12 @@ def test_prefill_layer_matches_sort_path(E, T, top, H, I, routing, mlx):
     scores = torch.from_numpy(rng.random((T, top)).astype(np.float32)).cuda()
     before = mq.launch_count()
     y = new(x, rhs)
-    assert mq.launch_count() == before + 6            # tables (2), gate, up, swiglu, down
+    assert mq.launch_count() == before + 4            # tables (2), gate+up+swiglu, down
     assert y.shape == (T, top, H)
     np.testing.assert_array_equal(bits16(y), bits16(old(x, rhs)))
     before = mq.launch_count()
     ys = new(x, rhs, scores)
-    assert mq.launch_count() == before + 7
+    assert mq.launch_count() == before + 5
     np.testing.assert_array_equal(bits16(ys), bits16(old(x, rhs, scores)))
     # the layer's gathers against the oracle on sampled pairs
     pairs = np.unique(rng.choice(T * top, 48, replace=False))
