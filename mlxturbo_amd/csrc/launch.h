@@ -208,10 +208,14 @@ inline int device_cu_count() {
 // costs as much as a full one (K=5120 N=17408, 68 column tiles on 256 CUs:
 // M=256 81 us with BM 128 against 112 with 256; M=512 113 with 192 against
 // 126 with 256 and 173 with 128; M=2048 362 with 192 against 406 with 256;
-// M=8192 1332 with 256 against 1515 with 192).  Splitting K serves narrow matrices, whose few column tiles leave
-// most CUs idle (K=17408 N=5120 has 20).  Partial planes are float [M, N]
-// per split, written by the tile kernel and summed in split order by a
-// reduce kernel: (8 S + 2) M N bytes at ~3.5 TB/s.
+// M=8192 1332 with 256 against 1515 with 192).  Splitting K serves narrow
+// matrices, whose few column tiles leave most CUs idle (K=17408 N=5120 has
+// 20), and one-round grids of wider ones: three splits put the 68 column
+// tiles of K=5120 N=17408 on 204 of 256 CUs (M=96 / 160 / 192 / 256: 48.9 /
+// 62.1 / 65.0 / 77.2 us against 59.4 / 74.9 / 79.3 / 86.5 with one, two or
+// four; graph-timed, one box).  Partial planes are float [M, N] per split,
+// written by the tile kernel and summed in split order by a reduce kernel:
+// (8 S + 2) M N bytes at ~3.5 TB/s.
 struct WidePlan {
   int bm = 256, splits = 1;
   double cost_us = 0.0;
@@ -224,7 +228,7 @@ inline WidePlan wide_plan(int64_t M, int64_t N, int64_t K, int cus, int max_spli
   const double tile_us[4] = {71.0, 81.0, 105.0, 119.0};   // one tile at K=5120, measured
   WidePlan best;
   bool first = true;
-  for (int sp = 1; sp <= max_splits; sp *= 2) {
+  for (int sp = 1; sp <= max_splits; sp = sp == 2 ? 3 : sp == 3 ? 4 : 2 * sp) {   // 1 2 3 4 8
     if (sp > 1 && nk / sp < 8) break;                 // at least 8 k-steps per split
     for (int i = 3; i >= 0; --i) {
       const int64_t wgs = cols * ((M + bms[i] - 1) / bms[i]) * sp;
