@@ -16,10 +16,11 @@
 // (l & 31) of each block, k = 32 h .. 32 h + 31 of the step (one 16-byte load
 // per block for 4-bit), dequantizes them exactly (mq_common.h) into the B
 // operands of four v_mfma_f32_32x32x16 (MFMA ks takes codes 8 ks .. 8 ks + 7
-// of the lane's 32; A rows use the same k order), so weights never touch
-// LDS.  Only the x tile (64 rows x 64 codes, 9 KB) is staged in LDS, double
-// buffered; 18 KB of LDS per workgroup leaves room for several workgroups
-// per CU.  Every column tile of a segment re-reads its x tile, and those
+// of the lane's 32; A rows use the same k order).  The x tile (64 rows x 64
+// codes, 9 KB) is staged in LDS, double buffered.  The 8-wave tiles load
+// their weights into registers; the 4-wave tiles of 4-bit banks take them
+// through LDS with the buffer loads' LDS form (16 columns x 64 bytes per
+// instruction, see thin_tile), 50 KB of LDS per workgroup, three per CU.  Every column tile of a segment re-reads its x tile, and those
 // re-reads cost as much as the weight stream's access shape (a load-only
 // probe: 94 us for the gate/up bank's weights, 132 with the x tiles of four
 // column tiles), so long K takes 8 waves (512 columns per x tile).  Global
@@ -55,13 +56,21 @@ __device__ __forceinline__ void thin_tile(
     const uint32_t* __restrict__ w2, const uint16_t* __restrict__ scales2,
     const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
     uint16_t* __restrict__ out, const int32_t* __restrict__ ws, int P, int B, int Mi, int N,
-    int K, int E, int seg, int col, int pofs) {
+    int K, int E, int seg, int col, int pofs, unsigned char* __restrict__ wsl0,
+    unsigned char* __restrict__ wsl1) {
   constexpr int BN = (GLU ? 32 : 64) * NWV, BK = kWideBK, LD = kWideLD, NT = 64 * NWV;
   constexpr int MB = BM / 32;                   // 32-row blocks of the tile
   static_assert(BM == 64 || BM == 128, "64- or 128-row tiles");
   constexpr int XT = BM * 8;                    // 16-byte x pieces per step
   constexpr int XI = XT >= NT ? XT / NT : 1;    // x pieces per thread per step
   constexpr int WB = BITS / 4;                  // 16-byte loads per lane per block per step
+  // 4-wave tiles (short K) take 4-bit weights into LDS by the buffer loads'
+  // LDS form (DMA), two k-steps (64 bytes) of 16 columns per load
+  // instruction, double buffered in wsl0 / wsl1 (NWV x 4 KB each); each lane
+  // then reads its 16 bytes of a step.  Config-4 down bank (K=512), one
+  // process: 166.7 / 142.9 us zipf / uniform against 170.3 / 148.1 from
+  // registers; the 8-wave gate/up tiles (K=2048) lost (308.4 against 286.7).
+  constexpr bool DMA = BITS == 4 && NWV == 4;
   static_assert(GS >= 32, "a lane's 32 codes lie in one group");
   using T = T16<DT>;
   __shared__ __align__(16) uint16_t As[2][BM * LD];
@@ -100,6 +109,31 @@ __device__ __forceinline__ void thin_tile(
     wo[j] = (uint32_t)(c * Kw * 4) + (uint32_t)h * 16u * WB;
     so[j] = (uint32_t)c * (uint32_t)G * 2u;
   }
+  // DMA: instruction q of a two-step group covers wave columns 16 q .. 16 q
+  // + 15 (block q / 2), four lanes per column; column c's 64 bytes land at
+  // LDS c * 64 with their 16-byte pieces permuted by dsw(c), so the per-step
+  // reads of 16 (or 8) lanes at consecutive columns hit distinct banks.  A
+  // group past the last one reads past the buffer range (zeros, no traffic).
+  auto dsw = [](int c) { return ((c >> 1) ^ (c >> 3)) & 3; };
+  uint32_t dmo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = 16 * q + (lane >> 2);
+    const int cr = GLU ? 32 * wave + (c & 31) : 64 * wave + c;
+    dmo[q] = (uint32_t)(cr * Kw * 4) + 16u * (uint32_t)((lane & 3) ^ dsw(c));
+  }
+  const int ngr = (nk + 1) / 2;                 // two-step groups
+  auto wdma = [&](int g, auto slotc) {
+    if constexpr (DMA) {
+      typedef __attribute__((address_space(3))) void lds_void;
+      unsigned char* base = (decltype(slotc)::value == 0 ? wsl0 : wsl1) + wave * 4096;
+      const uint32_t go = g < ngr ? (uint32_t)g * 64u : 0x80000000u;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw[q >> 1], (lds_void*)(base + 1024 * q), 16,
+                                                 dmo[q], go, 0, 0);
+    }
+  };
   // x: thread t stages rows (t >> 3) + (NT / 8) i, codes 8 (t & 7) .. +8 of
   // the step (offsets known once the segment's rows are in LDS)
   uint32_t xo[XI];
@@ -137,9 +171,12 @@ __device__ __forceinline__ void thin_tile(
     const int k0 = kt * BK;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
+      if constexpr (!DMA) {
 #pragma unroll
-      for (int q = 0; q < WB; ++q)
-        st.wv[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rw[j], wo[j] + 16u * q, k0 * BITS / 8, 0);
+        for (int q = 0; q < WB; ++q)
+          st.wv[j][q] = __builtin_amdgcn_raw_buffer_load_b128(rw[j], wo[j] + 16u * q,
+                                                              k0 * BITS / 8, 0);
+      }
       if (per_step) {
         const uint32_t go = so[j] + 2u * (uint32_t)((k0 + 32 * h) / GS);
         st.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs[j], go, 0, 0);
@@ -208,8 +245,22 @@ __device__ __forceinline__ void thin_tile(
   // One k-step: dequantize codes 8 ks .. 8 ks + 7 of the lane's 32 (B of MFMA
   // ks, per 32-column block) and multiply with the x rows in LDS buffer buf.
   // LB >= 0: step LB of an aligned block, scales from cs / cb
-  auto step = [&](const Stage& st, int buf, auto lbc) {
+  // DS: with DMA, 2 slot + step of the group (the weights' LDS copy)
+  auto step = [&](const Stage& st, int buf, auto lbc, auto dsc) {
     constexpr int LB = decltype(lbc)::value;
+    constexpr int DS = decltype(dsc)::value;
+    u32x4 wq[2];
+    if constexpr (DMA) {
+      const unsigned char* base = (DS >> 1 ? wsl1 : wsl0) + wave * 4096;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = 32 * j + lr;
+        wq[j] = *reinterpret_cast<const u32x4*>(base + 64 * c + 16 * ((2 * (DS & 1) + h) ^ dsw(c)));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) wq[j] = st.wv[j][0];
+    }
     GroupScale g[2];
     bool big = false;
 #pragma unroll
@@ -234,8 +285,8 @@ __device__ __forceinline__ void thin_tile(
       for (int j = 0; j < 2; ++j) {
         uint32_t o[4];
         if constexpr (BITS == 4) {
-          if (plain) deq_word_plain<DT, 4>(st.wv[j][0][ks], g[j], o);
-          else deq4_word<DT>(st.wv[j][0][ks], g[j], o);
+          if (plain) deq_word_plain<DT, 4>(wq[j][ks], g[j], o);
+          else deq4_word<DT>(wq[j][ks], g[j], o);
         } else {
           const u32x4 v = st.wv[j][ks / 2];
           if (plain) {
@@ -263,6 +314,8 @@ __device__ __forceinline__ void thin_tile(
       if (valid) {
 #pragma unroll
         for (int i = 0; i < PS; ++i) wload(S[i], i, false);
+        wdma(0, std::integral_constant<int, 0>{});
+        wdma(1, std::integral_constant<int, 1>{});
         bload(0);
       }
       if (!xsetup()) return;
@@ -282,7 +335,9 @@ __device__ __forceinline__ void thin_tile(
               cb[j] = nb[j];
             }
           }
-          step(S[u % PS], u & 1, uc);
+          step(S[u % PS], u & 1, uc, std::integral_constant<int, 2 * ((u >> 1) & 1) + (u & 1)>{});
+          // a group's weights are read: its slot takes the group after next
+          if constexpr (u & 1) wdma(((kt + u) >> 1) + 2, std::integral_constant<int, (u >> 1) & 1>{});
           gload(S[u % PS], min(kt + u + PS, nk - 1), false);
           if constexpr (u + PS == SPB) bload(min(kt + SPB, nk - SPB));
           store_x(S[(u + 1) % PS], (u + 1) & 1);
@@ -294,6 +349,8 @@ __device__ __forceinline__ void thin_tile(
     if (valid) {
 #pragma unroll
       for (int i = 0; i < PS; ++i) wload(S[i], min(i, nk - 1), true);
+      wdma(0, std::integral_constant<int, 0>{});
+      wdma(1, std::integral_constant<int, 1>{});
     }
     if (!xsetup()) return;
 #pragma unroll
@@ -301,20 +358,26 @@ __device__ __forceinline__ void thin_tile(
     store_x(S[0], 0);
     __syncthreads();
     // At step k: LDS buffer k & 1 holds x of step k; S[k % PS] holds step k's
-    // weights and is reloaded with step k + PS once they are multiplied;
-    // S[(k + i) % PS] holds step k + i.  The body is unrolled over lcm(PS, 2)
-    // steps so stage and buffer indices are constants; the last steps reload
-    // step nk - 1 (valid memory, unused), so the loads need no conditions.
-    constexpr int U = PS % 2 ? 2 * PS : PS;
+    // weights (with DMA: its scales; the weights are in slot (k / 2) & 1) and
+    // is reloaded with step k + PS once they are multiplied; S[(k + i) % PS]
+    // holds step k + i.  The body is unrolled over lcm(PS, 2) steps (4 with
+    // DMA) so stage, buffer and slot indices are constants; the last steps
+    // reload step nk - 1 (valid memory, unused), so the loads need no
+    // conditions.
+    constexpr int U = DMA ? 4 : PS % 2 ? 2 * PS : PS;
+    static_assert(U % PS == 0, "whole stage rounds per body");
     for (int kt = 0; kt < nk; kt += U) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (u > 0 && kt + u >= nk) break;         // uniform
-        step(S[u % PS], u & 1, std::integral_constant<int, -1>{});
-        gload(S[u % PS], min(kt + u + PS, nk - 1), true);
-        store_x(S[(u + 1) % PS], (u + 1) & 1);
-        __syncthreads();
-      }
+      static_for<0, U>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (u == 0 || kt + u < nk) {                // uniform
+          step(S[u % PS], u & 1, std::integral_constant<int, -1>{},
+               std::integral_constant<int, 2 * ((u >> 1) & 1) + (u & 1)>{});
+          if constexpr (u & 1) wdma(((kt + u) >> 1) + 2, std::integral_constant<int, (u >> 1) & 1>{});
+          gload(S[u % PS], min(kt + u + PS, nk - 1), true);
+          store_x(S[(u + 1) % PS], (u + 1) & 1);
+          __syncthreads();
+        }
+      });
     }
   }
 
@@ -363,6 +426,11 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
     const uint16_t* __restrict__ biases2, const int32_t* __restrict__ lhs,
     uint16_t* __restrict__ out, const int32_t* __restrict__ ws, int P, int B, int Mi, int N,
     int K, int E, int cls) {
+  // the 4-wave 4-bit tiles' weight slots (thin_tile's DMA), shared by both
+  // heights
+  constexpr int WSL = BITS == 4 && NWV == 4 ? NWV * 4096 : 16;
+  __shared__ __align__(16) unsigned char wsl0[WSL];
+  __shared__ __align__(16) unsigned char wsl1[WSL];
   const int32_t* hdr = ws + gather_ws_header(P);
   constexpr int BN = (GLU ? 32 : 64) * NWV;     // output columns per tile
   const int ncol = (N + BN - 1) / BN;
@@ -382,14 +450,14 @@ __global__ __launch_bounds__(64 * NWV) void qmm_grouped_thin_kernel(
   if (!grouped_tile(bi, nv, ncol, seg, col)) return;
   if (CLS2 && cls == 1 && !HALVES)
     thin_tile<DT, BITS, GS, PS, NWV, 128, GLU>(x, w, scales, biases, w2, scales2, biases2, lhs,
-                                                out, ws, P, B, Mi, N, K, E, seg + s0, col, 0);
+                                                out, ws, P, B, Mi, N, K, E, seg + s0, col, 0, wsl0, wsl1);
   else if (CLS2 && cls == 1)
     thin_tile<DT, BITS, GS, PS, NWV, 64, GLU>(x, w, scales, biases, w2, scales2, biases2, lhs,
                                                out, ws, P, B, Mi, N, K, E, (seg >> 1) + s0, col,
-                                               (seg & 1) * (64 / Mi));
+                                               (seg & 1) * (64 / Mi), wsl0, wsl1);
   else
     thin_tile<DT, BITS, GS, PS, NWV, 64, GLU>(x, w, scales, biases, w2, scales2, biases2, lhs,
-                                               out, ws, P, B, Mi, N, K, E, seg + s0, col, 0);
+                                               out, ws, P, B, Mi, N, K, E, seg + s0, col, 0, wsl0, wsl1);
 }
 
 }  // namespace mq
