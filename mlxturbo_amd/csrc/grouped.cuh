@@ -381,6 +381,9 @@ __device__ __forceinline__ void thin_tile(
     }
   }
 
+  // the last groups' loads (past the range, zeros) may still be landing in
+  // LDS: none may be in flight when the workgroup's LDS is given back
+  if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0);
   // D[row][col] of a 32x32 tile: col = lane & 31, row = 8*(e/4) + 4*(lane>>5) + e%4
   if constexpr (GLU) {
     const int c = 32 * wave + lr;
