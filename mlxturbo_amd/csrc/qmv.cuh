@@ -454,6 +454,11 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
     }
     const int kr = c * CPL;                   // lane's first code, relative to the step
     const int kt = t * STEPK + kr;            // same, absolute
+    // shared-x groups of whole tiles (qmv_shx_kernel, MT = 1): a group
+    // without tiles only stages x, and a tile past the group's rows is
+    // skipped (uniform branches)
+    constexpr bool SKIP = SHX > 1 && MT == 1;
+    if (SKIP && tl.rows[0] <= 0) return;
     if (__builtin_amdgcn_ballot_w64(big) == 0) {
 #pragma unroll
       for (int L = 0; L < NL; ++L) {
@@ -468,6 +473,7 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
           for (int mt = 0; mt < MT; ++mt) a[mt] = afrag(kr + ko, kt + ko, checked, mt);
 #pragma unroll
           for (int j = 0; j < TJ; ++j) {
+            if (SKIP && j > 0 && tl.rows[j] <= 0) continue;
             uint32_t bo[4];
             if constexpr (BITS == 4) {
               deq4_word<DT>(s.w[j][L][p], g[j], bo);
@@ -738,9 +744,11 @@ __host__ __device__ inline size_t qmv_xres_lds(int M, int K) {
 // (qmv_tile with SHX = NG): the groups stage each x slice once, so x is read
 // once per 16 NG TJ weight rows instead of once per 16 TJ; with XRES the
 // workgroup copies rows [0, M) of x into LDS once, before its first step,
-// and no step loads or stages x.  Workgroup i owns rows
-// [i N / grid, (i + 1) N / grid), group g the g-th NG-th of them as TJ tiles
-// of <= 16 rows; rows per workgroup <= 16 NG TJ.  Block 64 NW NG, dynamic
+// and no step loads or stages x.  With one A tile (MT = 1) workgroup i owns
+// the 16-row tiles [i T / grid, (i + 1) T / grid) of the T = ceil(N / 16),
+// group g TJ of them from the g TJ-th on; with two, rows [i N / grid, (i +
+// 1) N / grid), group g the g-th NG-th of them as TJ tiles of <= 16 rows;
+// rows per workgroup <= 16 NG TJ either way.  Block 64 NW NG, dynamic
 // LDS qmv_shx_lds(NW, XM) (XRES: qmv_xres_lds(M, K)) + NG TJ
 // qmv_sb_lds(K / GS) (SBL).
 template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, int NG,
@@ -753,10 +761,28 @@ __global__ __launch_bounds__(64 * NW * NG) void qmv_shx_kernel(
   __shared__ f32x4 red[NG * NW * TJ * MT][64];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = wave / NW, kw = wave - g * NW;
-  const int64_t wn0 = (int64_t)blockIdx.x * N / gridDim.x;
-  const int64_t wn1 = (int64_t)(blockIdx.x + 1) * N / gridDim.x;
-  const int n0 = (int)(wn0 + (wn1 - wn0) * g / NG);
-  const int n1 = (int)(wn0 + (wn1 - wn0) * (g + 1) / NG);
+  int n0, n1;
+  if constexpr (MT == 1) {
+    // whole 16-row tiles: workgroup i owns tiles [i T / grid, (i + 1) T /
+    // grid) of the T = ceil(N / 16), group g the TJ from the g TJ-th on
+    // (fewer or none for the last groups), so no wave dequantizes a partly
+    // empty tile: 68 rows per workgroup at K=5120 N=17408 ran as 3 x 2
+    // tiles of 11-12 rows, now as 2 + 2 + 0 or 2 + 2 + 1 whole ones (M=5 /
+    // 8 / 12 / 16: 17.8 / 17.9 / 20.4 / 20.8 -> 16.4 / 16.8 / 19.7 / 19.9
+    // us, one process; two A tiles (17-32 rows) lost 2-3% that way)
+    const int64_t nt = (N + 15) / 16;
+    const int64_t t0 = (int64_t)blockIdx.x * nt / gridDim.x;
+    const int64_t t1 = (int64_t)(blockIdx.x + 1) * nt / gridDim.x;
+    const int64_t g0 = t0 + TJ * g < t1 ? t0 + TJ * g : t1;
+    const int64_t g1 = g0 + TJ < t1 ? g0 + TJ : t1;
+    n0 = (int)(16 * g0 < N ? 16 * g0 : N);
+    n1 = (int)(16 * g1 < N ? 16 * g1 : N);
+  } else {
+    const int64_t wn0 = (int64_t)blockIdx.x * N / gridDim.x;
+    const int64_t wn1 = (int64_t)(blockIdx.x + 1) * N / gridDim.x;
+    n0 = (int)(wn0 + (wn1 - wn0) * g / NG);
+    n1 = (int)(wn0 + (wn1 - wn0) * (g + 1) / NG);
+  }
   const uint32_t rowB = (uint32_t)K * BITS / 8;
   const uint32_t sRowB = (uint32_t)(K / GS) * 2;
   QmvTiles<TJ> tl;
