@@ -767,9 +767,10 @@ __global__ __launch_bounds__(64 * NW * NG) void qmv_shx_kernel(
     // grid) of the T = ceil(N / 16), group g the TJ from the g TJ-th on
     // (fewer or none for the last groups), so no wave dequantizes a partly
     // empty tile: 68 rows per workgroup at K=5120 N=17408 ran as 3 x 2
-    // tiles of 11-12 rows, now as 2 + 2 + 0 or 2 + 2 + 1 whole ones (M=5 /
-    // 8 / 12 / 16: 17.8 / 17.9 / 20.4 / 20.8 -> 16.4 / 16.8 / 19.7 / 19.9
-    // us, one process; two A tiles (17-32 rows) lost 2-3% that way)
+    // tiles of 11-12 rows, now as 2 + 2 + 0 or 2 + 2 + 1 whole ones (two
+    // boxes, one process each: M=5 17.2-17.9 -> 16.3-16.6 us, M=8 17.6-17.9
+    // -> 16.8-17.0, M=12 / 16 0-5% faster; two A tiles (17-32 rows) lost
+    // 2-3% that way)
     const int64_t nt = (N + 15) / 16;
     const int64_t t0 = (int64_t)blockIdx.x * nt / gridDim.x;
     const int64_t t1 = (int64_t)(blockIdx.x + 1) * nt / gridDim.x;
