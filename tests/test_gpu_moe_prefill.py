@@ -135,6 +135,28 @@ def test_gather_swiglu_matches_three_calls(E, T, top, H, I, routing, dtype, bits
     np.testing.assert_array_equal(bits16(got), bits16(want))
 
 
+def test_gather_swiglu_rows_per_pair():
+    """Four x rows per pair (tables of 16-pair segments): the fused launch
+    equals the two gathers and the SwiGLU pass, bit for bit."""
+    rng = np.random.default_rng(21)
+    E, T, top, H, I, Mi = 32, 128, 4, 1024, 256, 4
+    banks = []
+    for _ in range(2):
+        w, s, b = random_packed(rng, E * I, H)
+        banks.append((to_dev(w).view(E, I, -1), to_dev(s, "bfloat16").view(E, I, -1),
+                      to_dev(b, "bfloat16").view(E, I, -1)))
+    idx = np.stack([rng.choice(E, top, replace=False) for _ in range(T)]).astype(np.int32)
+    rhs = torch.from_numpy(idx).cuda()
+    xe = to_dev(act(rng, (T, 1, Mi, H), scale=0.5), "bfloat16")
+    tables = ops.gather_tables(rhs, E, rows=Mi)
+    assert tables is not None
+    got = ops.gather_swiglu(xe, banks[0], banks[1], rhs, tables)
+    want = ops.swiglu(ops.gather_qmm(xe, *banks[0], rhs_indices=rhs, tables=tables),
+                      ops.gather_qmm(xe, *banks[1], rhs_indices=rhs, tables=tables))
+    assert got.shape == (T, top, Mi, I)
+    np.testing.assert_array_equal(bits16(got), bits16(want))
+
+
 def test_gather_swiglu_out_of_range_experts():
     """Pairs whose expert is outside the bank get zero rows from the fused
     launch, as from the gathers and the SwiGLU."""
