@@ -158,47 +158,76 @@ __global__ __launch_bounds__(64 * NW) void gather_qmv_kernel(
           if (lane == 0) ra.sgate[tok] = g;
         }
       }
-      for (int tok = wv; tok < B; tok += NW) {
-        int sel_e;
-        float sel_v;
-        route_wave_topk<8>(ra.logits + (int64_t)tok * E, E, ra.top_k, lane, sel_e, sel_v);
-        if (lane < ra.top_k) s_key[tok * ra.top_k + lane] = sel_e;
-        if (writer) {
-          const float wgt = route_wave_softmax(sel_v, lane, ra.top_k);
-          if (lane < ra.top_k) {
-            ra.idx[tok * ra.top_k + lane] = sel_e;
-            ra.w[tok * ra.top_k + lane] = wgt;
+      if (B == 1) {
+        // one token: its top_k experts are distinct, so pair r is segment r
+        // (one member), and the routing wave places the workgroup's segment
+        // itself: one barrier where the general path takes two (T=1,
+        // config-4 banks: discovery 0.8 of a 10.3 us launch)
+        if (!place(ra.top_k)) return;                // identical in every wave
+        if (wv == 0) {
+          int sel_e;
+          float sel_v;
+          route_wave_topk<8>(ra.logits, E, ra.top_k, lane, sel_e, sel_v);
+          if (writer) {
+            const float wgt = route_wave_softmax(sel_v, lane, ra.top_k);
+            if (lane < ra.top_k) {
+              ra.idx[lane] = sel_e;
+              ra.w[lane] = wgt;
+            }
+          }
+          const int es = __builtin_amdgcn_readlane(sel_e, seg);
+          if (lane < 16) {
+            s_members[lane] = lane == 0 ? seg : -1;
+            s_xbase[lane] = 0;
+          }
+          if (lane == 0) s_expert = es >= 0 ? es : E;  // a round with no expert: zeros
+        }
+        __syncthreads();
+      } else {
+        for (int tok = wv; tok < B; tok += NW) {
+          int sel_e;
+          float sel_v;
+          route_wave_topk<8>(ra.logits + (int64_t)tok * E, E, ra.top_k, lane, sel_e, sel_v);
+          if (lane < ra.top_k) s_key[tok * ra.top_k + lane] = sel_e >= 0 ? sel_e : E;
+          if (writer) {
+            const float wgt = route_wave_softmax(sel_v, lane, ra.top_k);
+            if (lane < ra.top_k) {
+              ra.idx[tok * ra.top_k + lane] = sel_e;
+              ra.w[tok * ra.top_k + lane] = wgt;
+            }
           }
         }
+        __syncthreads();
+        key = lane < P ? s_key[lane] : -1;
       }
-      __syncthreads();
-      key = lane < P ? s_key[lane] : -1;
     } else {
       key = lane < P ? key_of(lane) : -1;
     }
-    int cb = 0;
-    for (int q = 0; q < P; ++q) {
-      const int kq = __builtin_amdgcn_readlane(key, q);
-      cb += (q < lane && kq == key) ? 1 : 0;
+    if (!ROUTE || B != 1) {
+      int cb = 0;
+      for (int q = 0; q < P; ++q) {
+        const int kq = __builtin_amdgcn_readlane(key, q);
+        cb += (q < lane && kq == key) ? 1 : 0;
+      }
+      const bool lead = lane < P && (cb % R) == 0;
+      const uint64_t lmask = __builtin_amdgcn_ballot_w64(lead);
+      if (!place(__builtin_popcountll(lmask))) return;  // identical in every wave
+      const int rank = __builtin_popcountll(lmask & ((1ull << lane) - 1ull));
+      const uint64_t mine = __builtin_amdgcn_ballot_w64(lead && rank == seg);
+      const int leader = __builtin_ctzll(mine);
+      const int e = __builtin_amdgcn_readlane(key, leader);
+      const int cb0 = __builtin_amdgcn_readlane(cb, leader);
+      const int d = cb - cb0;
+      if (t < 16) s_members[t] = -1;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      if (lane < P && key == e && d >= 0 && d < R) {
+        s_members[d] = lane;
+        s_xbase[d] = ROUTE ? lane / ra.top_k : x_batch(lhs, lane, P, B);
+      }
+      if (t == 0) s_expert = e;
+      __syncthreads();
     }
-    const bool lead = lane < P && (cb % R) == 0;
-    const uint64_t lmask = __builtin_amdgcn_ballot_w64(lead);
-    if (!place(__builtin_popcountll(lmask))) return;  // identical in every wave
-    const int rank = __builtin_popcountll(lmask & ((1ull << lane) - 1ull));
-    const uint64_t mine = __builtin_amdgcn_ballot_w64(lead && rank == seg);
-    const int leader = __builtin_ctzll(mine);
-    const int e = __builtin_amdgcn_readlane(key, leader);
-    const int cb0 = __builtin_amdgcn_readlane(cb, leader);
-    const int d = cb - cb0;
-    if (t < 16) s_members[t] = -1;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    if (lane < P && key == e && d >= 0 && d < R) {
-      s_members[d] = lane;
-      s_xbase[d] = ROUTE ? lane / ra.top_k : x_batch(lhs, lane, P, B);
-    }
-    if (t == 0) s_expert = e;
-    __syncthreads();
   } else if (ws == nullptr) {
     if (t < 16) s_members[t] = -1;
     if (t == 0) {

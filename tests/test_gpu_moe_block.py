@@ -126,6 +126,38 @@ def test_routed_glu_matches_route_then_glu(E_, top, T):
     np.testing.assert_array_equal(bits16(h2), bits16(h))
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_routed_glu_rounds_without_expert(T):
+    """Logits whose order key is 0 (the all-ones NaN pattern) are never
+    chosen: with only 3 other experts, top-8 rounds 3..7 find none and
+    route to -1.  The routed launch gives those pairs zero rows, as the
+    GLU gather does for an out-of-range expert, and otherwise the same bits
+    as the routing kernel and the GLU gather."""
+    rng = np.random.default_rng(40 + T)
+    E_, top, K, N = 64, 8, 512, 256
+    def bank():
+        w, s, b = quantized(rng, E_ * N, K)
+        return (to_dev(w).view(E_, N, -1), to_dev(s, "bfloat16").view(E_, N, -1),
+                to_dev(b, "bfloat16").view(E_, N, -1))
+    gate, up = bank(), bank()
+    x = to_dev(act(rng, (T, K)), "bfloat16")
+    bits = np.full((T, E_), -1, dtype=np.int32)               # 0xffffffff: key 0
+    for t in range(T):
+        keep = rng.choice(E_, 3, replace=False)
+        bits[t, keep] = rng.standard_normal(3).astype(np.float32).view(np.int32)
+    logits = torch.from_numpy(bits.view(np.float32)).cuda()
+    got = ops._glu_routed(x, logits, top, gate, up, None, 64, 4)
+    assert got is not None
+    h2, idx2, w2, _ = got
+    idx, w, _ = ops.moe_route(logits, top)
+    assert torch.equal(idx2, idx)
+    assert (idx.cpu().numpy()[:, 3:] == -1).all() and (idx.cpu().numpy()[:, :3] >= 0).all()
+    assert torch.equal(w2.view(torch.int32), w.view(torch.int32))
+    h = ops.gather_glu(x.reshape(T, 1, 1, K), *gate, *up, rhs_indices=idx)
+    np.testing.assert_array_equal(bits16(h2), bits16(h))
+    assert not bits16(h2).reshape(T, top, N)[:, 3:].any()
+
+
 def test_routed_glu_declines_beyond_its_range():
     """More than 64 pairs or 512 experts: the block composes the launches."""
     rng = np.random.default_rng(5)
