@@ -572,13 +572,17 @@ inline int launch_thin_kernel(const void* x, const uint32_t* w, const void* s, c
                               const int32_t* lhs, void* out, int64_t P, int64_t B, int64_t M,
                               int64_t N, int64_t K, int64_t E, const void* ws, hipStream_t st) {
   const int R = (int)(kThinBM / M);
-  // 4 waves (256 columns) per workgroup at short K, 8 (512 columns, so each
-  // x tile serves twice the columns) above K = 1024: config-4 banks, 2048
-  // tokens x top-8, one process: down (K=512) 143 / 122 us zipf / uniform
-  // with 4 against 173 / 141 with 8; gate/up (K=2048) 279 / 222 with 8
-  // against 302 / 253 for the size-class wide tiles and 282 / 264 with 16
-  // waves (whose 128-register budget spills)
-  const int nwv = K <= 1024 ? 4 : 8;
+  // 4 waves (256 columns) per workgroup for 4-bit weights and at short K, 8
+  // (512 columns, so each x tile serves twice the columns) for 8-bit weights
+  // above K = 1024.  Config-4 banks, 2048 tokens x top-8, one process: down
+  // (K=512) 143 / 122 us zipf / uniform with 4 against 173 / 141 with 8.
+  // Gate/up (K=2048): 4-bit 4-wave tiles stream their weights through LDS
+  // (the DMA form in grouped.cuh) and take 275 / 241 us against 285 / 261
+  // with 8 waves; the fused SwiGLU layer 425 against 447 us zipf.  Without
+  // that stream (8-bit) 8 waves won: 279 / 222 against 302 / 253 for the
+  // size-class wide tiles and 282 / 264 with 16 waves (whose 128-register
+  // budget spills).
+  const int nwv = (K <= 1024 || BITS == 4) ? 4 : 8;
   const int64_t bn = (GLU ? 32 : 64) * nwv;     // output columns per tile
   const int64_t ncol = (N + bn - 1) / bn;
   // 8 waves: experts with more than 64 rows take 128-row tiles, which read
