@@ -17,13 +17,16 @@
 // per block for 4-bit), dequantizes them exactly (mq_common.h) into the B
 // operands of four v_mfma_f32_32x32x16 (MFMA ks takes codes 8 ks .. 8 ks + 7
 // of the lane's 32; A rows use the same k order).  The x tile (64 rows x 64
-// codes, 9 KB) is staged in LDS, double buffered.  The 8-wave tiles load
-// their weights into registers; the 4-wave tiles of 4-bit banks take them
-// through LDS with the buffer loads' LDS form (16 columns x 64 bytes per
-// instruction, see thin_tile), 50 KB of LDS per workgroup, three per CU.  Every column tile of a segment re-reads its x tile, and those
-// re-reads cost as much as the weight stream's access shape (a load-only
-// probe: 94 us for the gate/up bank's weights, 132 with the x tiles of four
-// column tiles), so long K takes 8 waves (512 columns per x tile).  Global
+// codes, 9 KB) is staged in LDS, double buffered.  The 8-wave tiles (8-bit
+// banks above K = 1024) load their weights into registers; the 4-wave tiles
+// of 4-bit banks take them through LDS with the buffer loads' LDS form (16
+// columns x 64 bytes per instruction, see thin_tile), 50 KB of LDS per
+// workgroup, three per CU.  Every column tile of a segment re-reads its x
+// tile, and those re-reads cost as much as the weight stream's access shape
+// (a load-only probe: 94 us for the gate/up bank's weights, 132 with the x
+// tiles of four column tiles), so from registers long K took 8 waves (512
+// columns per x tile); the LDS-form stream made 4 waves the faster again
+// (gate/up 272 / 241 us zipf / uniform against 285 / 261).  Global
 // loads run PS k-steps ahead in registers (two measured best: deeper
 // prefetch lowered occupancy and lost 10-15% on the down bank).  32-row
 // blocks past the segment's rows skip their MFMAs.  Measured on the
@@ -69,7 +72,8 @@ __device__ __forceinline__ void thin_tile(
   // instruction, double buffered in wsl0 / wsl1 (NWV x 4 KB each); each lane
   // then reads its 16 bytes of a step.  Config-4 down bank (K=512), one
   // process: 166.7 / 142.9 us zipf / uniform against 170.3 / 148.1 from
-  // registers; the 8-wave gate/up tiles (K=2048) lost (308.4 against 286.7).
+  // registers; 8-wave gate/up tiles (K=2048) lost with it (308.4 against
+  // 286.7), and 4-wave gate/up tiles with it beat both (272 zipf).
   constexpr bool DMA = BITS == 4 && NWV == 4;
   static_assert(GS >= 32, "a lane's 32 codes lie in one group");
   using T = T16<DT>;
