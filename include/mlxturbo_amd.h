@@ -259,6 +259,31 @@ int mq_moe_glu_route(const void* x, const float* logits, const uint32_t* w_gate,
                      void* hip_stream);
 
 /*
+ * The whole decode MoE block of one token in one launch: mq_moe_glu_route
+ * (x [K1], logits [E], gate / up banks [E, N1, K1] -> idx, weights, sgate,
+ * h [top_k, N1]) followed by mq_gather_qmm_combine(h, down bank [E, N2, N1],
+ * idx, weights, sgate, shared [N2] -> out [N2]), bit for bit.  The down
+ * projection starts behind a grid-wide arrival inside the launch (device-
+ * scope stores of h and per-workgroup flags in a static device array of the
+ * library), so calls that overlap on one GPU race; a stream's calls run in
+ * order.  The reference runs its decode route (kernels/moe_route_decode.py:
+ * 151-327), its fused decode gate/up and down (kernels/moe_decode_fused.py:
+ * 331-397) and its combine with the shared expert (moe_route_decode.py:
+ * 353-398) as separate dispatches.  sgw / sgate / shared are all given or
+ * all NULL.  One token (T = 1), top_k <= 8, E <= 512; other calls, tile
+ * configurations other than the decode gather's 4-wave gate/up tiles and
+ * one-wave down tiles, or a grid that does not fit the device at once
+ * return MQ_EUNSUPPORTED, and the caller makes the two calls.
+ */
+int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
+                 const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
+                 const void* scales_up, const void* biases_up, const uint32_t* w_down,
+                 const void* scales_down, const void* biases_down, const void* sgw,
+                 const void* shared, int32_t* idx, float* weights, void* sgate, void* h,
+                 void* out, int64_t T, int64_t top_k, int64_t N1, int64_t K1, int64_t N2,
+                 int64_t E, int group_size, int bits, int dtype, void* hip_stream);
+
+/*
  * out[i] = T(T(silu(gate[i])) * up[i]) for i < n, silu(g) = g / (1 + exp(-g))
  * in float, dtype bf16 or fp16: mlx-lm SwitchGLU's activation between the
  * gate / up and down gathers (`act = switch_mlp.activation(x_up, x_gate)` in

@@ -1,9 +1,11 @@
 // Kernel instantiations of one (dtype, bits) pair for every group size.  The
 // build compiles this file once per pair with -DMQ_INST_DT=<0|1> and
 // -DMQ_INST_BITS=<4|8>, and once more per pair with -DMQ_INST_GLU for the
-// fused gate+up kernels (decode, and prefill with SwiGLU) and the folded
-// down + combine kernel; abi.hip calls the launchers through launch.h.
+// fused gate+up kernels (decode, and prefill with SwiGLU), the folded
+// down + combine kernel and the one-launch decode block; abi.hip calls the
+// launchers through launch.h.
 #include "launch.h"
+#include "block.cuh"
 #include "dequant.cuh"
 #include "gather.cuh"
 #include "qmm_wide.cuh"
@@ -20,7 +22,8 @@ namespace mq {
   template struct GluLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;           \
   template struct GluRouteLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;      \
   template struct GatherFoldLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;   \
-  template struct SwigluTablesLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
+  template struct SwigluTablesLaunch<MQ_INST_DT, MQ_INST_BITS, GS>; \
+  template struct MoeBlockLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;
 #else
 #define MQ_INST(GS)                                                  \
   template struct DequantLaunch<MQ_INST_DT, MQ_INST_BITS, GS>;       \

@@ -125,6 +125,22 @@ struct GatherFoldLaunch {
                  hipStream_t st, int* nlaunch);
 };
 
+// The decode MoE block of one token in one launch (block.cuh): the routing
+// of logits [E], the fused gate+up+SiLU gather into h [top_k, N1], the down
+// projection [E, N2, N1] with the router-weighted combine and, with shared /
+// ra.sgw, the shared-expert merge into out [N2]; the same bits as
+// GluRouteLaunch followed by GatherFoldLaunch.  kStatusUnsupported where its
+// tile configuration does not apply or its grid does not fit the device at
+// once (the caller then runs those two launches).
+template <int DT, int BITS, int GS>
+struct MoeBlockLaunch {
+  static int run(const void* x, const uint32_t* wg, const void* sg, const void* bg,
+                 const uint32_t* wu, const void* su, const void* bu, const uint32_t* wd,
+                 const void* sd, const void* bd, const void* shared, void* h, void* out,
+                 int64_t N1, int64_t K1, int64_t N2, int64_t E, const RouteArgs& ra,
+                 hipStream_t st, int* nlaunch);
+};
+
 // MoE routing (route.hip): per row of float logits [rows, E] the top_k
 // experts (descending, equal values by smaller index) into idx and their
 // softmax weights into w; with x ([rows, H]) and sgw ([H]) non-null (dtype

@@ -60,6 +60,7 @@
 //    each output row is bit-identical for every M (the property the
 //    reference tests for its small-M kernel: bench/test_qmm_smallm.py:70-85).
 #pragma once
+#include <type_traits>
 #include "launch.h"
 
 namespace mq {
@@ -179,6 +180,17 @@ inline bool qmv_sb_fits(int64_t G, int NW, int TJ, const void* scales, const voi
 // row m from x) and either store(m, nn, v) of a rounded 16-bit output
 // (kCombine false) or store_combined(m, nn, v[TJ]) of the float sums of all
 // tiles of the call (kCombine true).
+// A Rows type may also give kXAux, the cache-policy bits of its x loads
+// (0 when absent).
+template <class R, class = void>
+struct RowsXAux {
+  static constexpr int value = 0;
+};
+template <class R>
+struct RowsXAux<R, std::void_t<decltype(R::kXAux)>> {
+  static constexpr int value = R::kXAux;
+};
+
 // Dense: A row m is x row m; output (m, column n0 + nn).
 struct DenseRows {
   static constexpr bool kCombine = false;
@@ -258,6 +270,8 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   constexpr int XPL = XM ? (XM * XPR + 63) / 64 : 1;      // pieces per lane per step
   constexpr int XSR = 2 * STEPK + 16;                     // LDS bytes per x row (padded)
   static_assert(SHX == 1 || XM > 0, "shared x slices stream through LDS");
+  constexpr int XAUX = RowsXAux<Rows>::value;
+  static_assert(XAUX == 0 || XM > 0, "x loads with cache-policy bits are buffer loads");
   // pieces this wave loads: q-th of them is piece q * SHX + grp
   constexpr int XPW = XRES ? 1 : (XPL + SHX - 1) / SHX;
   static_assert(!XRES || (XM > 0 && SBL), "resident x is filled with the scale copy");
@@ -334,7 +348,7 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
                                 live ? src.x_nrec - xstep : 0u);
 #pragma unroll
       for (int q = 0; q < XPW; ++q)
-        s.xq[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, xvo[q], 0, 0);
+        s.xq[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, xvo[q], 0, XAUX);
     }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -561,7 +575,7 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
 #pragma unroll
     for (int u = 0; u < XRU; ++u) {
       uint32_t lo;
-      xrq[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, xres_piece(xtid + u * xnt, lo), 0, 0);
+      xrq[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, xres_piece(xtid + u * xnt, lo), 0, XAUX);
     }
   }
   // ---- main loop: PF-stage pipeline over the unchecked steps --------------
@@ -579,7 +593,7 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
     for (int i = xtid + XRU * xnt; i < xtot; i += xnt) {
       uint32_t lo;
       const uint32_t go = xres_piece(i, lo);
-      *(lds_u32x4*)((lds_u8*)xsh + lo) = __builtin_amdgcn_raw_buffer_load_b128(rx, go, 0, 0);
+      *(lds_u32x4*)((lds_u8*)xsh + lo) = __builtin_amdgcn_raw_buffer_load_b128(rx, go, 0, XAUX);
     }
   }
   if constexpr (SBL) {
@@ -672,6 +686,15 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
     // the next tile of this workgroup reuses red and the LDS copies
     __syncthreads();
   }
+}
+
+// Workgroup barriers one qmv_tile call executes without shared x slices,
+// resident x or stacked A tiles (SHX = 1, XRES off, MT = 1): the scale
+// copy's, and the two of the cross-wave sum when NW > 1.  Waves of a
+// workgroup that sit a call out execute as many.
+template <int NW, bool SBL>
+constexpr int qmv_tile_barriers() {
+  return (SBL ? 1 : 0) + (NW > 1 ? 2 : 0);
 }
 
 // Workgroups of the skinny kernel.  By default one per 16 TJ rows.  When the

@@ -952,10 +952,16 @@ def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
     are ``(w, scales, biases)`` banks.  Returns ``(T, H_out)``: the same
     bits as calling the three steps one by one.  Up to 64 (token, expert)
     pairs over up to 512 experts the routing runs inside the gate+up
-    launch (mq_moe_glu_route), one launch less on the dependent chain."""
+    launch (mq_moe_glu_route), one launch less on the dependent chain; one
+    token runs the whole block as one launch (mq_moe_block) where its tile
+    configuration applies."""
     if (sgw is None) != (shared is None):
         raise ValueError("sgw and shared are given together")
     T, H = x.shape
+    if T == 1:
+        out = _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits)
+        if out is not None:
+            return out
     routed = _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits)
     if routed is not None:
         h, idx, wts, sg = routed
@@ -968,9 +974,51 @@ def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
                               sgate=sg, shared=shared)
 
 
-def _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits):
-    """Routing and the fused gate+up+SiLU in one launch (mq_moe_glu_route:
-    the same bits as moe_route then gather_glu), or None where that launch
+def _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits):
+    """The block of one token in one launch (mq_moe_block: the same bits as
+    the routed gate+up launch followed by the folded down projection, the
+    down tiles starting behind a grid-wide arrival inside the launch), or
+    None where that launch does not apply."""
+    (wd, sd, bd) = down
+    E = logits.shape[-1]
+    if (wd.ndim != 3 or wd.shape[0] != E or bd is None or sd.dtype != x.dtype
+            or wd.dtype not in (torch.uint32, torch.int32)):
+        return None
+    routed_ok = _glu_routed_args(x, logits, top_k, gate, up, sgw, group_size, bits)
+    if routed_ok is None:
+        return None
+    N1, K1 = routed_ok
+    N2 = wd.shape[1]
+    if _check_quant(wd, sd, bd, group_size, bits) != N1:
+        raise ValueError(f"down bank K={wd.shape[-1] * 32 // bits} does not match the gate/up "
+                         f"rows N={N1}")
+    if shared is not None and (tuple(shared.shape) != (1, N2) or shared.dtype != x.dtype):
+        raise ValueError(f"shared must be (1, {N2}) of x's dtype")
+    _require_gpu(wd, sd, bd, shared)
+    dev = x.device
+    idx = torch.empty((1, top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((1, top_k), dtype=torch.float32, device=dev)
+    sgate = torch.empty((1, 1), dtype=x.dtype, device=dev) if sgw is not None else None
+    h = torch.empty((1, top_k, 1, N1), dtype=x.dtype, device=dev)
+    out = torch.empty((1, N2), dtype=x.dtype, device=dev)
+    x_ = _aligned(x.contiguous())
+    lg = logits.contiguous()
+    g_ = sgw.reshape(-1).contiguous() if sgw is not None else None
+    sh_ = shared.contiguous() if shared is not None else None
+    (wg, sg_, bg), (wu, su, bu) = gate, up
+    banks = [_aligned(t) for t in (wg, sg_, bg, wu, su, bu, wd, sd, bd)]
+    rc = _lib.lib().mq_moe_block(x_.data_ptr(), lg.data_ptr(), *[t.data_ptr() for t in banks],
+                                 _ptr(g_), _ptr(sh_), idx.data_ptr(), wts.data_ptr(),
+                                 _ptr(sgate), h.data_ptr(), out.data_ptr(), 1, top_k, N1, K1,
+                                 N2, E, group_size, bits, _DTYPE_CODE[x.dtype], _stream_ptr(out))
+    if rc == _EUNSUPPORTED:
+        return None
+    _lib.check(rc, "moe_block")
+    return out
+
+
+def _glu_routed_args(x, logits, top_k, gate, up, sgw, group_size, bits):
+    """(N, K) of the routed gate+up launch's banks, or None where that launch
     does not apply (more than 64 pairs or 512 experts, other formats)."""
     T, H = x.shape
     (wg, sg_, bg), (wu, su, bu) = gate, up
@@ -983,11 +1031,24 @@ def _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits):
             or (sgw is not None and sgw.dtype != x.dtype)):
         return None
     _require_gpu(x, logits, wg, sg_, bg, wu, su, bu, sgw)
-    N = wg.shape[1]
     K = _check_quant(wg, sg_, bg, group_size, bits)
     _check_quant(wu, su, bu, group_size, bits)
     if K != H:
         raise ValueError(f"x last dimension {H} does not match the quantized weight K={K}")
+    return wg.shape[1], K
+
+
+def _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits):
+    """Routing and the fused gate+up+SiLU in one launch (mq_moe_glu_route:
+    the same bits as moe_route then gather_glu), or None where that launch
+    does not apply (more than 64 pairs or 512 experts, other formats)."""
+    T, H = x.shape
+    (wg, sg_, bg), (wu, su, bu) = gate, up
+    E = logits.shape[-1]
+    nk = _glu_routed_args(x, logits, top_k, gate, up, sgw, group_size, bits)
+    if nk is None:
+        return None
+    N, K = nk
     dev = x.device
     idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
     wts = torch.empty((T, top_k), dtype=torch.float32, device=dev)

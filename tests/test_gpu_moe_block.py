@@ -11,8 +11,10 @@ steps called one by one, bit for bit; the routing equals the oracle's
 exactly; each step meets the oracle on the previous step's GPU output (the
 GLU and the down projection at the matmul tolerance, the combine with the
 shared merge bit for bit); the routing inside the gate+up launch gives the
-routing kernel's and the GLU gather's bits; launch counts (2 launches at
-T <= 2, 3 above).
+routing kernel's and the GLU gather's bits; the one-launch block of one
+token (mq_moe_block) gives the two launches' bits on fresh routings, in
+graph replays and across calls of other shapes; launch counts (1 launch at
+T = 1, 2 at T = 2, 3 above).
 """
 
 import numpy as np
@@ -20,7 +22,7 @@ import pytest
 import torch
 
 import mlxturbo_amd as mq
-from mlxturbo_amd import ops
+from mlxturbo_amd import _lib, ops
 from oracle import oracle as O
 from qmm_helpers import act, bits16, from_dev, quantized, to_dev
 
@@ -58,9 +60,10 @@ def test_moe_block(banks, T, with_shared):
     before = mq.launch_count()
     out = ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
     launches = mq.launch_count() - before
-    # routing inside the gate+up launch, then the folded down (T <= 2) or
-    # the down gather and the combine
-    assert launches == (2 if T * TOP <= 16 else 3)
+    # one token: the whole block in one launch; else routing inside the
+    # gate+up launch, then the folded down (T <= 2) or the down gather and
+    # the combine
+    assert launches == (1 if T == 1 else 2 if T * TOP <= 16 else 3)
     assert out.shape == (T, H)
 
     # the three steps one by one
@@ -168,3 +171,180 @@ def test_routed_glu_declines_beyond_its_range():
     x = to_dev(act(rng, (2, K)), "bfloat16")
     logits = torch.from_numpy(rng.standard_normal((2, E_)).astype(np.float32)).cuda()
     assert ops._glu_routed(x, logits, 8, bank, bank, None, 64, 4) is None
+
+
+def _two_launch_block(x, logits, top, gate, up, down, sgw, shared, gs=64, bits=4):
+    """The block of one token as the routed gate+up launch and the folded
+    down launch (what mq_moe_block fuses)."""
+    h, idx, w, sg = ops._glu_routed(x, logits, top, gate, up, sgw, gs, bits)
+    return ops.gather_qmm_combine(h, *down, idx, w, group_size=gs, bits=bits, sgate=sg,
+                                  shared=shared), idx, w, sg, h
+
+
+def _block_launch(x, logits, top, gate, up, down, sgw, shared, bits=4, gs=64):
+    before = mq.launch_count()
+    out = ops.moe_block(x, logits, top, gate, up, down, sgw=sgw, shared=shared, bits=bits,
+                        group_size=gs)
+    assert mq.launch_count() - before == 1
+    return out
+
+
+def test_block_one_launch_fresh_routings(banks):
+    """One token, 24 calls in a row with fresh logits (normal, zipf-skewed,
+    and quantized to quarters so that ties occur), with and without the
+    shared expert: the one-launch block equals the two launches bit for
+    bit every time (each call's arrival flags follow the last call's)."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(2024)
+    for i in range(24):
+        with_shared = i % 2 == 0
+        x = to_dev(act(rng, (1, H)), "bfloat16")
+        lg = rng.standard_normal((1, E)).astype(np.float32)
+        if i % 3 == 1:
+            lg = lg - 0.5 * np.log(np.arange(1, E + 1, dtype=np.float32))
+        elif i % 3 == 2:
+            lg = np.round(lg * 4) / 4
+        logits = torch.from_numpy(lg).cuda()
+        sgw = to_dev(act(rng, (H,), scale=0.02), "bfloat16") if with_shared else None
+        shared = to_dev(act(rng, (1, H), scale=0.1), "bfloat16") if with_shared else None
+        out = _block_launch(x, logits, TOP, gate, up, down, sgw, shared)
+        want = _two_launch_block(x, logits, TOP, gate, up, down, sgw, shared)[0]
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"call {i}")
+
+
+def test_block_one_launch_outputs(banks):
+    """The launch's routing, gate and h outputs are the two launches' bits."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(8)
+    x = to_dev(act(rng, (1, H)), "bfloat16")
+    logits = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+    sgw = to_dev(act(rng, (H,), scale=0.02), "bfloat16")
+    shared = to_dev(act(rng, (1, H), scale=0.1), "bfloat16")
+    want, idx, w, sg, h = _two_launch_block(x, logits, TOP, gate, up, down, sgw, shared)
+    (wg, sg_, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
+    idx2 = torch.empty_like(idx)
+    w2 = torch.empty_like(w)
+    sg2 = torch.empty_like(sg)
+    h2 = torch.empty_like(h)
+    out = torch.empty_like(want)
+    lib = _lib.lib()
+    rc = lib.mq_moe_block(x.data_ptr(), logits.data_ptr(),
+                          *[t.data_ptr() for t in (wg, sg_, bg, wu, su, bu, wd, sd, bd)],
+                          sgw.data_ptr(), shared.data_ptr(), idx2.data_ptr(), w2.data_ptr(),
+                          sg2.data_ptr(), h2.data_ptr(), out.data_ptr(), 1, TOP, I, H, H, E,
+                          64, 4, 0, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "moe_block")
+    torch.cuda.synchronize()
+    assert torch.equal(idx2, idx) and torch.equal(w2, w)
+    np.testing.assert_array_equal(bits16(sg2), bits16(sg))
+    np.testing.assert_array_equal(bits16(h2), bits16(h))
+    np.testing.assert_array_equal(bits16(out), bits16(want))
+
+
+def test_block_one_launch_graph_replays(banks):
+    """A captured one-token block replayed 6 times with new logits and x
+    copied in between (eager two-launch blocks run between the replays):
+    every replay equals the two launches on its inputs."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(99)
+    x = to_dev(act(rng, (1, H)), "bfloat16")
+    logits = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+    sgw = to_dev(act(rng, (H,), scale=0.02), "bfloat16")
+    shared = to_dev(act(rng, (1, H), scale=0.1), "bfloat16")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
+    for r in range(6):
+        x.copy_(to_dev(act(rng, (1, H)), "bfloat16"))
+        logits.copy_(torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        want = _two_launch_block(x, logits, TOP, gate, up, down, sgw, shared)[0]
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"replay {r}")
+
+
+@pytest.mark.parametrize("dtype,bits,gs,E_,top,H_,I_", [
+    ("float16", 4, 64, 128, 8, 1024, 512),
+    ("bfloat16", 8, 64, 64, 4, 1024, 384),
+    ("bfloat16", 4, 64, 96, 6, 1536, 320),
+    ("bfloat16", 4, 128, 64, 4, 2048, 1024),
+])
+def test_block_one_launch_other_shapes(banks, dtype, bits, gs, E_, top, H_, I_):
+    """Other dtypes, bit widths, group sizes, expert counts and widths
+    (grids of 96-256 workgroups), each call followed by a call of the
+    config-4 block (a grid of another size over the same arrival flags):
+    both equal the two launches bit for bit."""
+    (_, gate4), (_, up4), (_, down4) = banks
+    rng = np.random.default_rng(E_ + top + bits)
+
+    def bank(N, K):
+        w, s_, b = quantized(rng, E_ * N, K, gs=gs, bits=bits, dtype=dtype)
+        return (to_dev(w).view(E_, N, -1), to_dev(s_, dtype).view(E_, N, -1),
+                to_dev(b, dtype).view(E_, N, -1))
+
+    gate, up, down = bank(I_, H_), bank(I_, H_), bank(H_, I_)
+    for i in range(3):
+        x = to_dev(act(rng, (1, H_), dtype), dtype)
+        logits = torch.from_numpy(rng.standard_normal((1, E_)).astype(np.float32)).cuda()
+        sgw = to_dev(act(rng, (H_,), dtype, scale=0.02), dtype)
+        shared = to_dev(act(rng, (1, H_), dtype, scale=0.1), dtype)
+        out = _block_launch(x, logits, top, gate, up, down, sgw, shared, bits, gs)
+        want = _two_launch_block(x, logits, top, gate, up, down, sgw, shared, gs, bits)[0]
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"call {i}")
+        x4 = to_dev(act(rng, (1, H)), "bfloat16")
+        lg4 = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+        out4 = _block_launch(x4, lg4, TOP, gate4, up4, down4, None, None)
+        want4 = _two_launch_block(x4, lg4, TOP, gate4, up4, down4, None, None)[0]
+        np.testing.assert_array_equal(bits16(out4), bits16(want4), err_msg=f"config-4 call {i}")
+
+
+def test_block_one_launch_rounds_without_expert():
+    """One token whose logits leave only 3 choosable experts: top-8 rounds
+    3..7 route to -1, their pairs contribute zero rows, and the one-launch
+    block equals the two launches bit for bit."""
+    rng = np.random.default_rng(41)
+    E_, top, H_, I_ = 64, 8, 1024, 512
+
+    def bank(N, K):
+        w, s_, b = quantized(rng, E_ * N, K)
+        return (to_dev(w).view(E_, N, -1), to_dev(s_, "bfloat16").view(E_, N, -1),
+                to_dev(b, "bfloat16").view(E_, N, -1))
+
+    gate, up, down = bank(I_, H_), bank(I_, H_), bank(H_, I_)
+    x = to_dev(act(rng, (1, H_)), "bfloat16")
+    lb = np.full((1, E_), -1, dtype=np.int32)                # 0xffffffff: key 0
+    keep = rng.choice(E_, 3, replace=False)
+    lb[0, keep] = rng.standard_normal(3).astype(np.float32).view(np.int32)
+    logits = torch.from_numpy(lb.view(np.float32)).cuda()
+    out = _block_launch(x, logits, top, gate, up, down, None, None)
+    want, idx, _, _, _ = _two_launch_block(x, logits, top, gate, up, down, None, None)
+    assert (idx.cpu().numpy()[:, 3:] == -1).all()
+    np.testing.assert_array_equal(bits16(out), bits16(want))
+
+
+@pytest.mark.parametrize("E_,top,H_,I_,gs", [(32, 4, 512, 256, 64), (64, 8, 2048, 1024, 128)])
+def test_block_one_launch_declines(E_, top, H_, I_, gs):
+    """Shapes outside the one-launch kernel's tiles (gate/up K whose tiles
+    split over fewer than 4 waves) or grid (more than 256 workgroups):
+    moe_block runs the two launches."""
+    rng = np.random.default_rng(6)
+
+    def bank(N, K):
+        w, s_, b = quantized(rng, E_ * N, K, gs=gs)
+        return (to_dev(w).view(E_, N, -1), to_dev(s_, "bfloat16").view(E_, N, -1),
+                to_dev(b, "bfloat16").view(E_, N, -1))
+
+    gate, up, down = bank(I_, H_), bank(I_, H_), bank(H_, I_)
+    x = to_dev(act(rng, (1, H_)), "bfloat16")
+    logits = torch.from_numpy(rng.standard_normal((1, E_)).astype(np.float32)).cuda()
+    before = mq.launch_count()
+    out = ops.moe_block(x, logits, top, gate, up, down, group_size=gs)
+    assert mq.launch_count() - before == 2
+    want = _two_launch_block(x, logits, top, gate, up, down, None, None, gs)[0]
+    np.testing.assert_array_equal(bits16(out), bits16(want))
