@@ -9,7 +9,10 @@
 // (gather.cuh) as two dependent launches.
 //
 // CDNA4 design.  Phase 1 is the routed GLU gather at one token: every
-// workgroup routes the token on wave 0 (route.cuh), and workgroup i computes
+// workgroup routes the token with all its waves (route.cuh route_block_topk,
+// ranks instead of rounds: routed 3.3 us into the launch, against 3.8 with
+// one wave's sorted rounds and 4.2 with rounds on 8 waves), and workgroup i
+// computes
 // the 16 h columns (i mod nsl) of the (i / nsl)-th selected expert.  The
 // down projection needs every h value, so phase 2 starts behind a grid-wide
 // arrival: the h tiles are stored with device-scope stores (sc1, written
@@ -88,6 +91,7 @@ __global__ __launch_bounds__(64 * NW) void moe_block1_kernel(
   using C = QmvConf<BITS, GS>;
   using T = T16<DT>;
   constexpr int NPOLL = NW < 4 ? NW : 4;       // waves polling the arrival flags
+  static_assert(NW == 8 && NWT < NW, "8 waves: routing over 512 experts, a free wave per tile");
   __shared__ f32x4 red[NW * 2][64];
   __shared__ uint16_t s_y[8][16];
   __shared__ int s_sel[8];
@@ -102,30 +106,37 @@ __global__ __launch_bounds__(64 * NW) void moe_block1_kernel(
   const int seg = blockIdx.x / nsl, slot = blockIdx.x - seg * nsl;
   const int ngrid = gridDim.x;
   if (t == 0) s_ep = __hip_atomic_load(&g_block_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // the shared gate beside the top-k, in workgroup 0 (phase 2 reads it
-  // after the arrival)
-  if (SH && blockIdx.x == 0 && wv == NW / 2) {
+  // routing by the workgroup's waves (route_block_topk, one barrier), then
+  // the softmax on wave 0
+  __shared__ uint64_t s_c[64 * NW];
+  __shared__ uint32_t s_ck[64];
+  __shared__ int s_ce[64];
+  {
+    int sel_e;
+    float sel_v;
+    route_block_topk<NW>(ra.logits, E, top_k, wv, lane, s_c, s_ck, s_ce, sel_e, sel_v);
+    if (wv == 0) {
+      const float wgt = route_wave_softmax(sel_v, lane, top_k);
+      if (blockIdx.x == 0 && lane < top_k) {
+        ra.idx[lane] = sel_e;
+        ra.w[lane] = wgt;
+      }
+      if (lane < top_k) {
+        s_sel[lane] = sel_e >= 0 ? sel_e : E;    // a round with no expert: zeros
+        s_w[lane] = wgt;
+      }
+      const int es = __builtin_amdgcn_readlane(sel_e, seg < top_k ? seg : 0);
+      if (lane == 0) s_expert = es >= 0 ? es : E;
+    }
+  }
+  __syncthreads();
+  // the shared gate in workgroup 0 on its last wave, which the phase-1 tile
+  // leaves free (phase 2 reads the gate after the arrival)
+  if (SH && blockIdx.x == 0 && wv == NW - 1) {
     const uint16_t gsh = route_wave_shared_gate<DT>(x, ra.sgw, K1, lane);
     if (lane == 0)
       __hip_atomic_store(ra.sgate, gsh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (wv == 0) {
-    int sel_e;
-    float sel_v;
-    route_wave_topk<8>(ra.logits, E, top_k, lane, sel_e, sel_v);
-    const float wgt = route_wave_softmax(sel_v, lane, top_k);
-    if (blockIdx.x == 0 && lane < top_k) {
-      ra.idx[lane] = sel_e;
-      ra.w[lane] = wgt;
-    }
-    if (lane < top_k) {
-      s_sel[lane] = sel_e >= 0 ? sel_e : E;      // a round with no expert: zeros
-      s_w[lane] = wgt;
-    }
-    const int es = __builtin_amdgcn_readlane(sel_e, seg < top_k ? seg : 0);
-    if (lane == 0) s_expert = es >= 0 ? es : E;
-  }
-  __syncthreads();
 
   // ---- phase 1: 16 columns of h for pair seg, on waves 0 .. NWT-1 ---------
   {

@@ -18,28 +18,34 @@ namespace mq {
 // experts per lane: E <= 64 kRouteMaxPerLane
 constexpr int kRouteMaxPerLane = 16;
 
-#define MQ_DPP_STEP(x, OP, CTRL, ROWS)                                                        \
-  x = OP(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROWS, 0xf, false))
-// Largest / smallest uint32 over the 64 lanes, returned to every lane:
-// inclusive row scans (row_shr 1, 2, 4, 8), the row ends broadcast into the
-// following rows (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2
-// and 3), the total read from lane 63.  Lanes without a source keep their
-// own value (bound_ctrl off, old = x).  (v_max_u32 / v_min_u32 directly: a
-// compare-and-select lets the compiler re-run the DPP move under a partial
-// exec mask, where disabled source lanes read as out of range.)
-template <bool MAX>
-__device__ __forceinline__ uint32_t route_wave_reduce_u32(uint32_t x) {
-#define MQ_OP(a, b) (MAX ? __builtin_elementwise_max(a, b) : __builtin_elementwise_min(a, b))
-  MQ_DPP_STEP(x, MQ_OP, 0x111, 0xf);
-  MQ_DPP_STEP(x, MQ_OP, 0x112, 0xf);
-  MQ_DPP_STEP(x, MQ_OP, 0x114, 0xf);
-  MQ_DPP_STEP(x, MQ_OP, 0x118, 0xf);
-  MQ_DPP_STEP(x, MQ_OP, 0x142, 0xa);
-  MQ_DPP_STEP(x, MQ_OP, 0x143, 0xc);
-#undef MQ_OP
+// Largest uint32 over the 64 lanes (all lanes active), returned to every
+// lane: inclusive row scans (row_shr 1, 2, 4, 8), the row ends broadcast
+// into the following rows (row_bcast 15 into rows 1 and 3, row_bcast 31 into
+// rows 2 and 3), the total read from lane 63.  Each step is one v_max_u32
+// with the DPP source in place: a lane without a source lane (bound_ctrl
+// off) or outside the row mask is not written and keeps its own value.
+// Two wait states before each DPP read of the previous step's result.  (As
+// a DPP move and a separate max the compiler took four instructions per
+// step; as a compare-and-select it re-ran a DPP move under a partial exec
+// mask, where disabled source lanes read as out of range.)
+__device__ __forceinline__ uint32_t route_wave_max_u32(uint32_t x) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:1 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:2 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(x));
   return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
 }
-#undef MQ_DPP_STEP
 
 // Sum over the 64 lanes (lanes without a source add 0), returned to every lane.
 __device__ __forceinline__ float route_wave_sum_f32(float x) {
@@ -136,7 +142,7 @@ __device__ __forceinline__ void route_wave_topk(const float* __restrict__ lr, in
   sel_e = 0;
   for (int r = 0; r < top_k; ++r) {
     // the lane's head is its best remaining expert (ties: smaller expert)
-    const uint32_t mk = route_wave_reduce_u32<true>(key[0]);
+    const uint32_t mk = route_wave_max_u32(key[0]);
     const uint64_t held = __builtin_amdgcn_ballot_w64(key[0] == mk && mk != 0u);
     int win = -1;
     if (held != 0) {
@@ -154,6 +160,83 @@ __device__ __forceinline__ void route_wave_topk(const float* __restrict__ lr, in
     if (lane == r) {
       sel_v = route_from_key(mk);
       sel_e = win;
+    }
+  }
+}
+
+// The same selection by NWV waves of a workgroup (E <= 64 NWV, top_k <= 8,
+// NWV * top_k <= 64), as ranks instead of rounds: wave w keys experts
+// 64 w + lane, one per lane, as c = key * 64 + (63 - lane) (unique; larger c
+// first, so equal keys go by the smaller expert), and each lane's rank is
+// the number of c in its wave above its own (LDS broadcast reads, 64
+// independent compares: no dependent chain of wave reductions).  Ranks
+// below top_k (with key != 0) are the wave's candidates in round order, at
+// LDS slot top_k w + rank; after a workgroup barrier wave 0 ranks the
+// NWV top_k candidates the same way by key and slot (slot order keeps
+// equal keys in expert order: waves hold increasing experts, and a wave's
+// candidates take equal keys by increasing expert).  Every wave of the
+// workgroup calls it (one barrier); lane r < top_k of wave 0 gets round
+// r's expert and logit, as route_wave_topk gives them (expert -1 and the
+// logit of key 0 for a round with no expert).  LDS: s_c [64 NWV], s_ck /
+// s_ce [64].
+template <int NWV>
+__device__ __forceinline__ void route_block_topk(const float* __restrict__ lr, int E, int top_k,
+                                                 int wv, int lane, uint64_t* s_c, uint32_t* s_ck,
+                                                 int* s_ce, int& sel_e, float& sel_v) {
+  static_assert(NWV * 8 <= 64, "the candidates fit one wave");
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // rank of c among the 64 values at base (c itself counts 0)
+  auto rank_of = [](const uint64_t* base, uint64_t c) {
+    int rk = 0;
+#pragma unroll
+    for (int d = 0; d < 64; ++d) rk += base[d] > c ? 1 : 0;
+    return rk;
+  };
+  const int e = 64 * wv + lane;
+  const uint32_t k = e < E ? route_order_key(lr[e]) : 0u;
+  const uint64_t c = ((uint64_t)k << 6) | (uint64_t)(63 - lane);
+  s_c[64 * wv + lane] = c;
+  if (lane < top_k) {
+    s_ck[top_k * wv + lane] = 0u;
+    s_ce[top_k * wv + lane] = -1;
+  }
+  wave_sync();
+  const int rk = rank_of(s_c + 64 * wv, c);
+  if (k != 0u && rk < top_k) {
+    s_ck[top_k * wv + rk] = k;
+    s_ce[top_k * wv + rk] = e;
+  }
+  __syncthreads();
+  sel_v = 0.0f;
+  sel_e = 0;
+  if (wv == 0) {
+    const uint32_t k2 = lane < NWV * top_k ? s_ck[lane] : 0u;
+    const int e2 = lane < NWV * top_k ? s_ce[lane] : -1;
+    const uint64_t c2 = ((uint64_t)k2 << 6) | (uint64_t)(63 - lane);
+    s_c[lane] = c2;                               // stage 1's values are read
+    wave_sync();
+    const int rk2 = rank_of(s_c, c2);
+    wave_sync();
+    // round r's key and expert, at s_c / s_ce slots 64 + r (key 0, -1: none)
+    uint32_t* ok = reinterpret_cast<uint32_t*>(s_c + 64);
+    int* oe = reinterpret_cast<int*>(s_c + 64) + 8;
+    if (lane < top_k) {
+      ok[lane] = 0u;
+      oe[lane] = -1;
+    }
+    wave_sync();
+    if (k2 != 0u && rk2 < top_k) {
+      ok[rk2] = k2;
+      oe[rk2] = e2;
+    }
+    wave_sync();
+    if (lane < top_k) {
+      sel_v = route_from_key(ok[lane]);
+      sel_e = oe[lane];
     }
   }
 }
