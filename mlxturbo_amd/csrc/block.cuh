@@ -12,14 +12,14 @@
 // workgroup routes the token with all its waves (route.cuh route_block_topk,
 // ranks instead of rounds: routed 3.3 us into the launch, against 3.8 with
 // one wave's sorted rounds and 4.2 with rounds on 8 waves), and workgroup i
-// computes
-// the 16 h columns (i mod nsl) of the (i / nsl)-th selected expert.  The
-// down projection needs every h value, so phase 2 starts behind a grid-wide
-// arrival: the h tiles are stored with device-scope stores (sc1, written
-// through to the point of coherence of all XCDs), each workgroup waits for
-// its stores to complete and then sets its arrival flag to the call's epoch
-// + 1, and the first ceil(N2 / 16) workgroups, which run phase 2, poll the
-// flags with device-scope loads and read h the same way.  No L2 write-back
+// computes the 16 h columns (i mod nsl) of the (i / nsl)-th selected
+// expert.  The down projection needs every h value, so phase 2 starts
+// behind a grid-wide arrival: the h tiles are stored with device-scope
+// stores (sc1, written through to the point of coherence of all XCDs), each
+// workgroup waits for its stores to complete and then sets its arrival flag
+// to the call's epoch + 1, and the first ceil(N2 / 16) workgroups, which
+// run phase 2, poll the flags with device-scope loads and read h the same
+// way.  No L2 write-back
 // or invalidate runs (a device-scope release per workgroup cost more than
 // the launch it would save, since it writes back the XCD's whole L2).
 //
