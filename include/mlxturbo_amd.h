@@ -284,6 +284,27 @@ int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
                  int64_t E, int group_size, int bits, int dtype, void* hip_stream);
 
 /*
+ * The decode MoE layer of one token with its routing given, in one launch:
+ * mq_gather_glu(x [1, 1, K1], gate bank, up bank, lhs NULL, rhs idx [top_k],
+ * h [top_k, N1], P = top_k, B = 1, M = 1, ...) followed by
+ * mq_gather_qmm_combine(h, down bank [E, N2, N1], idx, weights [top_k]
+ * (float router weights), no shared expert -> out [N2]), bit for bit, with
+ * mq_moe_block's grid-wide arrival (calls that overlap on one GPU race).
+ * The reference's decode layer runs its fused gate/up and its down kernel
+ * with the combine as separate dispatches (kernels/moe_decode_fused.py:
+ * 331-397, kernels/moe_combine.py:160-195; fused.py:2456-2492).  An expert
+ * outside [0, E) gives a zero row.  T = 1, top_k <= 8, E <= 512 and
+ * mq_moe_block's tile and grid limits, else MQ_EUNSUPPORTED and the caller
+ * makes the two calls.
+ */
+int mq_moe_layer(const void* x, const int32_t* idx, const float* weights, const uint32_t* w_gate,
+                 const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
+                 const void* scales_up, const void* biases_up, const uint32_t* w_down,
+                 const void* scales_down, const void* biases_down, void* h, void* out,
+                 int64_t T, int64_t top_k, int64_t N1, int64_t K1, int64_t N2, int64_t E,
+                 int group_size, int bits, int dtype, void* hip_stream);
+
+/*
  * out[i] = T(T(silu(gate[i])) * up[i]) for i < n, silu(g) = g / (1 + exp(-g))
  * in float, dtype bf16 or fp16: mlx-lm SwitchGLU's activation between the
  * gate / up and down gathers (`act = switch_mlp.activation(x_up, x_gate)` in

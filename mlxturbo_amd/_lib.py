@@ -41,6 +41,7 @@ EXPORTED = (
     "mq_swiglu",
     "mq_moe_glu_route",
     "mq_moe_block",
+    "mq_moe_layer",
     "mq_gather_glu",
     "mq_gather_qmm_combine",
     "mq_moe_combine",
@@ -102,6 +103,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mq_moe_glu_route.argtypes = [_vp] * 13 + [_i64] * 5 + [_int, _int, _int, _vp]
     lib.mq_moe_block.restype = _int
     lib.mq_moe_block.argtypes = [_vp] * 18 + [_i64] * 6 + [_int, _int, _int, _vp]
+    lib.mq_moe_layer.restype = _int
+    lib.mq_moe_layer.argtypes = [_vp] * 14 + [_i64] * 6 + [_int, _int, _int, _vp]
     lib.mq_swiglu.restype = _int
     lib.mq_swiglu.argtypes = [_vp, _vp, _vp, _i64, _int, _vp]
     lib.mq_moe_combine_shared.restype = _int

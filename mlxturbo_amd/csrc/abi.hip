@@ -147,7 +147,7 @@ int moe_combine_checked(const void* y, int64_t y_rows, const int32_t* inv, const
 
 extern "C" {
 
-int mq_version(void) { return 7; }
+int mq_version(void) { return 8; }
 
 const char* mq_last_error(void) { return g_last_error.c_str(); }
 
@@ -511,6 +511,47 @@ int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail((int)e, "moe_block: launch failed: %s", hipGetErrorString(e));
+  g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
+  return MQ_OK;
+}
+
+int mq_moe_layer(const void* x, const int32_t* idx, const float* weights, const uint32_t* w_gate,
+                 const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
+                 const void* scales_up, const void* biases_up, const uint32_t* w_down,
+                 const void* scales_down, const void* biases_down, void* h, void* out,
+                 int64_t T, int64_t top_k, int64_t N1, int64_t K1, int64_t N2, int64_t E,
+                 int group_size, int bits, int dtype, void* hip_stream) {
+  int rc = check_common(w_gate, scales_gate, biases_gate, N1, K1, group_size, bits, dtype);
+  if (rc) return rc;
+  rc = check_common(w_up, scales_up, biases_up, N1, K1, group_size, bits, dtype);
+  if (rc) return rc;
+  rc = check_common(w_down, scales_down, biases_down, N2, N1, group_size, bits, dtype);
+  if (rc) return rc;
+  if (!x || !idx || !weights || !h || !out)
+    return fail(MQ_EINVAL, "x, idx, weights, h and out must be non-null");
+  if (T < 0 || E < 1 || top_k < 1)
+    return fail(MQ_EINVAL, "invalid sizes T=%lld E=%lld top_k=%lld", (long long)T, (long long)E,
+                (long long)top_k);
+  if (dtype == MQ_FLOAT32)
+    return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
+  if (!aligned16(x) || !aligned16(h)) return fail(MQ_EINVAL, "x and h must be 16-byte aligned");
+  if (T != 1 || top_k > 8 || top_k > E || E > 512 || N1 > INT32_MAX || K1 > INT32_MAX ||
+      N2 > INT32_MAX || N1 == 0 || N2 == 0)
+    return fail(MQ_EUNSUPPORTED,
+                "moe_layer runs one token, top_k <= 8, E <= 512 (T=%lld top_k=%lld E=%lld)",
+                (long long)T, (long long)top_k, (long long)E);
+  mq::RouteArgs ra;
+  ra.idx = const_cast<int32_t*>(idx);
+  ra.w = const_cast<float*>(weights);
+  ra.top_k = (int)top_k;
+  int nl = 0;
+  rc = dispatch_16<mq::MoeBlockLaunch>(dtype, bits, group_size, x, w_gate, scales_gate,
+                                       biases_gate, w_up, scales_up, biases_up, w_down,
+                                       scales_down, biases_down, nullptr, h, out, N1, K1, N2, E,
+                                       ra, reinterpret_cast<hipStream_t>(hip_stream), &nl);
+  if (rc) return fail(rc, "moe_layer: no one-launch kernel for this configuration");
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail((int)e, "moe_layer: launch failed: %s", hipGetErrorString(e));
   g_launches.fetch_add((uint64_t)nl, std::memory_order_relaxed);
   return MQ_OK;
 }

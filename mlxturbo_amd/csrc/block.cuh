@@ -76,9 +76,12 @@ struct BlockFoldRows {
 // wait), the phase-2 tiles one per wave and round; x [K1], logits [E]
 // (E <= 512),
 // gate / up banks [E, N1, K1], down bank [E, N2, K2 = N1], h [top_k, N1],
-// out [N2]; ra.idx / ra.w / ra.sgate get the routing as mq_moe_route writes
-// it.  SH: shared [N2] merged with the gate sigmoid(T(x . ra.sgw)).
-template <int DT, int BITS, int GS, int NW, int NWT, bool SH>
+// out [N2].  ROUTE: logits [E] in ra.logits, and ra.idx / ra.w / ra.sgate
+// get the routing as mq_moe_route writes it; else the pairs' experts and
+// router weights are given in ra.idx / ra.w (an expert outside [0, E)
+// gives a zero row, as in the gather).  SH (with ROUTE): shared [N2] merged
+// with the gate sigmoid(T(x . ra.sgw)).
+template <int DT, int BITS, int GS, int NW, int NWT, bool ROUTE, bool SH>
 __global__ __launch_bounds__(64 * NW) void moe_block1_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wg,
     const uint16_t* __restrict__ sg, const uint16_t* __restrict__ bg,
@@ -92,6 +95,7 @@ __global__ __launch_bounds__(64 * NW) void moe_block1_kernel(
   using T = T16<DT>;
   constexpr int NPOLL = NW < 4 ? NW : 4;       // waves polling the arrival flags
   static_assert(NW == 8 && NWT < NW, "8 waves: routing over 512 experts, a free wave per tile");
+  static_assert(ROUTE || !SH, "the shared expert's gate comes with the routing");
   __shared__ f32x4 red[NW * 2][64];
   __shared__ uint16_t s_y[8][16];
   __shared__ int s_sel[8];
@@ -107,11 +111,11 @@ __global__ __launch_bounds__(64 * NW) void moe_block1_kernel(
   const int ngrid = gridDim.x;
   if (t == 0) s_ep = __hip_atomic_load(&g_block_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // routing by the workgroup's waves (route_block_topk, one barrier), then
-  // the softmax on wave 0
-  __shared__ uint64_t s_c[64 * NW];
-  __shared__ uint32_t s_ck[64];
-  __shared__ int s_ce[64];
-  {
+  // the softmax on wave 0; or the given experts and weights
+  if constexpr (ROUTE) {
+    __shared__ uint64_t s_c[64 * NW];
+    __shared__ uint32_t s_ck[64];
+    __shared__ int s_ce[64];
     int sel_e;
     float sel_v;
     route_block_topk<NW>(ra.logits, E, top_k, wv, lane, s_c, s_ck, s_ce, sel_e, sel_v);
@@ -128,6 +132,15 @@ __global__ __launch_bounds__(64 * NW) void moe_block1_kernel(
       const int es = __builtin_amdgcn_readlane(sel_e, seg < top_k ? seg : 0);
       if (lane == 0) s_expert = es >= 0 ? es : E;
     }
+  } else if (wv == 0) {
+    const int ei = lane < top_k ? ra.idx[lane] : 0;
+    const int ek = (unsigned)ei < (unsigned)E ? ei : E;
+    if (lane < top_k) {
+      s_sel[lane] = ek;
+      s_w[lane] = ra.w[lane];
+    }
+    const int es = __builtin_amdgcn_readlane(ek, seg < top_k ? seg : 0);
+    if (lane == 0) s_expert = es;
   }
   __syncthreads();
   // the shared gate in workgroup 0 on its last wave, which the phase-1 tile
@@ -294,14 +307,16 @@ int MoeBlockLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const v
   const size_t lds1 = gather_group_lds<BITS, GS, C::GPL>(4, 1, false, (int)(K1 / GS), 2);
   const size_t lds2 = NW * gather_group_lds<BITS, GS, C::GPL>(1, 1, false, (int)(N1 / GS), 1);
   const size_t lds = lds1 > lds2 ? lds1 : lds2;
-  const bool sh = shared != nullptr;
+  const bool sh = shared != nullptr, route = ra.logits != nullptr;
+  if (sh && !route) return kStatusUnsupported;
   const void* kern =
-      sh ? reinterpret_cast<const void*>(&moe_block1_kernel<DT, BITS, GS, NW, 4, true>)
-         : reinterpret_cast<const void*>(&moe_block1_kernel<DT, BITS, GS, NW, 4, false>);
+      !route ? reinterpret_cast<const void*>(&moe_block1_kernel<DT, BITS, GS, NW, 4, false, false>)
+      : sh   ? reinterpret_cast<const void*>(&moe_block1_kernel<DT, BITS, GS, NW, 4, true, true>)
+             : reinterpret_cast<const void*>(&moe_block1_kernel<DT, BITS, GS, NW, 4, true, false>);
   // every workgroup resident at once (the arrival waits for all of them);
   // the occupancy query is kept per kernel and LDS size
-  static std::atomic<uint64_t> occ[2];
-  const int ki = sh;
+  static std::atomic<uint64_t> occ[3];
+  const int ki = route ? 1 + sh : 0;
   const uint64_t key = (uint64_t)lds << 32;
   uint64_t got = occ[ki].load(std::memory_order_relaxed);
   if ((got & ~0xffffffffull) != key || got == 0) {
@@ -313,15 +328,16 @@ int MoeBlockLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* wg, const v
   }
   const int64_t per_cu = (int64_t)(got & 0xffffffffull) - 1;
   if (per_cu * device_cu_count() < grid) return kStatusUnsupported;
-#define MQ_BLK(SH)                                                                              \
-  hipLaunchKernelGGL((moe_block1_kernel<DT, BITS, GS, NW, 4, SH>), dim3((unsigned)grid),       \
+#define MQ_BLK(RT, SH)                                                                          \
+  hipLaunchKernelGGL((moe_block1_kernel<DT, BITS, GS, NW, 4, RT, SH>), dim3((unsigned)grid),   \
                      dim3(64 * NW), lds, st, (const uint16_t*)x, wg, (const uint16_t*)sg,       \
                      (const uint16_t*)bg, wu, (const uint16_t*)su, (const uint16_t*)bu, wd,     \
                      (const uint16_t*)sd, (const uint16_t*)bd, (const uint16_t*)shared,         \
                      (uint16_t*)h, (uint16_t*)out, (int)N1, (int)K1, (int)N2, (int)E, (int)n2, \
                      ra)
-  if (sh) MQ_BLK(true);
-  else MQ_BLK(false);
+  if (!route) MQ_BLK(false, false);
+  else if (sh) MQ_BLK(true, true);
+  else MQ_BLK(true, false);
 #undef MQ_BLK
   *nlaunch += 1;
   return 0;

@@ -129,7 +129,9 @@ struct GatherFoldLaunch {
 // of logits [E], the fused gate+up+SiLU gather into h [top_k, N1], the down
 // projection [E, N2, N1] with the router-weighted combine and, with shared /
 // ra.sgw, the shared-expert merge into out [N2]; the same bits as
-// GluRouteLaunch followed by GatherFoldLaunch.  kStatusUnsupported where its
+// GluRouteLaunch followed by GatherFoldLaunch.  With ra.logits NULL the
+// experts and router weights are given in ra.idx / ra.w (the decode layer:
+// GluLaunch followed by GatherFoldLaunch).  kStatusUnsupported where its
 // tile configuration does not apply or its grid does not fit the device at
 // once (the caller then runs those two launches).
 template <int DT, int BITS, int GS>

@@ -246,6 +246,16 @@ class SwitchGLU(torch.nn.Module):
         idx = indices.reshape(-1, top_k)
         if self._fused(idx.numel()):
             g, u = self.gate_proj, self.up_proj
+            d = self.down_proj
+            if (idx.shape[0] == 1 and scores is not None and d.bias is None and g.mode == "affine"
+                    and (d.group_size, d.bits, d.mode) == (g.group_size, g.bits, g.mode)):
+                # one token: the whole layer in one launch where it applies
+                out = ops._layer_one(x.reshape(1, -1), idx, scores,
+                                     (g.weight, g.scales, g.biases),
+                                     (u.weight, u.scales, u.biases),
+                                     (d.weight, d.scales, d.biases), g.group_size, g.bits)
+                if out is not None:
+                    return out.reshape(*lead, out.shape[-1])
             h = ops.gather_glu(xe, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases,
                                rhs_indices=idx, group_size=g.group_size, bits=g.bits,
                                mode=g.mode)                        # (T, k, 1, I)

@@ -1017,6 +1017,65 @@ def _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits):
     return out
 
 
+def moe_layer(x: torch.Tensor, rhs_indices: torch.Tensor, weights: torch.Tensor, gate, up,
+              down, group_size: int = 64, bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """A decode MoE layer after its routing (the reference's fused decode
+    route, kernels/moe_decode_fused.py:331-397 with the combine of
+    kernels/moe_combine.py:160-195): ``gather_glu(x, gate, up, rhs_indices)``
+    then ``gather_qmm_combine(h, down, rhs_indices, weights)``.  ``x`` is
+    ``(T, K)``, ``rhs_indices`` and the router ``weights`` ``(T, top_k)``;
+    ``gate``, ``up``, ``down`` are ``(w, scales, biases)`` banks.  Returns
+    ``(T, N)``, the bits of the two calls; one token runs both in one launch
+    (mq_moe_layer) where its tile configuration applies."""
+    T, K = x.shape
+    idx = rhs_indices.reshape(T, -1)
+    if T == 1 and mode == "affine":
+        out = _layer_one(x, idx, weights, gate, up, down, group_size, bits)
+        if out is not None:
+            return out
+    h = gather_glu(x.reshape(T, 1, 1, K), *gate, *up, rhs_indices=idx, group_size=group_size,
+                   bits=bits, mode=mode)
+    return gather_qmm_combine(h, *down, idx, weights.reshape(idx.shape), group_size=group_size,
+                              bits=bits, mode=mode)
+
+
+def _layer_one(x, idx, weights, gate, up, down, group_size, bits):
+    """One token's layer in one launch (mq_moe_layer), or None where that
+    launch does not apply."""
+    (wg, sg_, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
+    top_k = idx.shape[-1]
+    if (x.dtype not in (torch.bfloat16, torch.float16) or bits not in (4, 8)
+            or bg is None or bu is None or bd is None or wg.ndim != 3 or wg.shape != wu.shape
+            or wd.ndim != 3 or wd.shape[0] != wg.shape[0] or top_k > 8 or weights.numel() != top_k
+            or sg_.dtype != x.dtype or su.dtype != x.dtype or sd.dtype != x.dtype
+            or any(w.dtype not in (torch.uint32, torch.int32) for w in (wg, wu, wd))):
+        return None
+    dev = _require_gpu(x, idx, weights, wg, sg_, bg, wu, su, bu, wd, sd, bd)
+    E, N1 = wg.shape[0], wg.shape[1]
+    K1 = _check_quant(wg, sg_, bg, group_size, bits)
+    _check_quant(wu, su, bu, group_size, bits)
+    if K1 != x.shape[-1]:
+        raise ValueError(f"x last dimension {x.shape[-1]} does not match the quantized weight "
+                         f"K={K1}")
+    if _check_quant(wd, sd, bd, group_size, bits) != N1:
+        return None
+    N2 = wd.shape[1]
+    h = torch.empty((1, top_k, 1, N1), dtype=x.dtype, device=dev)
+    out = torch.empty((1, N2), dtype=x.dtype, device=dev)
+    x_ = _aligned(x.contiguous())
+    idx_ = idx.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+    w_ = weights.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    banks = [_aligned(t) for t in (wg, sg_, bg, wu, su, bu, wd, sd, bd)]
+    rc = _lib.lib().mq_moe_layer(x_.data_ptr(), idx_.data_ptr(), w_.data_ptr(),
+                                 *[t.data_ptr() for t in banks], h.data_ptr(), out.data_ptr(), 1,
+                                 top_k, N1, K1, N2, E, group_size, bits, _DTYPE_CODE[x.dtype],
+                                 _stream_ptr(out))
+    if rc == _EUNSUPPORTED:
+        return None
+    _lib.check(rc, "moe_layer")
+    return out
+
+
 def _glu_routed_args(x, logits, top_k, gate, up, sgw, group_size, bits):
     """(N, K) of the routed gate+up launch's banks, or None where that launch
     does not apply (more than 64 pairs or 512 experts, other formats)."""

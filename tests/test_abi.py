@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version(lib):
-    assert lib.mq_version() == 7
+    assert lib.mq_version() == 8
 
 
 FAKE = 256  # aligned, never dereferenced: validation fails before any HIP call

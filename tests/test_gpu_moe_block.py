@@ -348,3 +348,75 @@ def test_block_one_launch_declines(E_, top, H_, I_, gs):
     assert mq.launch_count() - before == 2
     want = _two_launch_block(x, logits, top, gate, up, down, None, None, gs)[0]
     np.testing.assert_array_equal(bits16(out), bits16(want))
+
+
+def _two_launch_layer(x, idx, w, gate, up, down, gs=64, bits=4):
+    h = ops.gather_glu(x.reshape(1, 1, 1, -1), *gate, *up, rhs_indices=idx, group_size=gs,
+                       bits=bits)
+    return ops.gather_qmm_combine(h, *down, idx, w, group_size=gs, bits=bits)
+
+
+def test_layer_one_launch(banks):
+    """The decode layer of one token with its routing given (mq_moe_layer):
+    24 calls with fresh experts (distinct, repeated, out of range) and
+    router weights, interleaved with routed one-launch blocks (the same
+    arrival flags): each equals gather_glu then gather_qmm_combine bit for
+    bit, in one launch; nn.SwitchGLU(fuse_gate_up=True) takes it at T = 1."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(55)
+    for i in range(24):
+        x = to_dev(act(rng, (1, H)), "bfloat16")
+        e = rng.choice(E, TOP, replace=False).astype(np.int32)
+        if i % 4 == 1:
+            e[3] = e[1]                                  # a repeated expert
+        elif i % 4 == 2:
+            e[5] = E + 7                                 # out of range: a zero row
+        idx = torch.from_numpy(e.reshape(1, TOP)).cuda()
+        w = torch.softmax(torch.from_numpy(rng.standard_normal((1, TOP)).astype(np.float32)),
+                          -1).cuda()
+        before = mq.launch_count()
+        out = ops.moe_layer(x, idx, w, gate, up, down)
+        assert mq.launch_count() - before == 1
+        want = _two_launch_layer(x, idx, w, gate, up, down)
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"call {i}")
+        if i % 3 == 0:
+            lg = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+            ob = _block_launch(x, lg, TOP, gate, up, down, None, None)
+            np.testing.assert_array_equal(
+                bits16(ob), bits16(_two_launch_block(x, lg, TOP, gate, up, down, None, None)[0]))
+    from mlxturbo_amd import nn as mqnn
+    layer = mqnn.SwitchGLU(mqnn.QuantizedSwitchLinear(*gate), mqnn.QuantizedSwitchLinear(*up),
+                           mqnn.QuantizedSwitchLinear(*down), fuse_gate_up=True)
+    before = mq.launch_count()
+    out = layer(x, idx, w)
+    assert mq.launch_count() - before == 1
+    np.testing.assert_array_equal(bits16(out), bits16(_two_launch_layer(x, idx, w, gate, up, down)))
+
+
+def test_layer_one_launch_graph_replays(banks):
+    """A captured one-token layer replayed 5 times with new experts,
+    weights and x copied in between: every replay equals the two calls."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(7)
+    x = to_dev(act(rng, (1, H)), "bfloat16")
+    idx = torch.from_numpy(rng.choice(E, TOP, replace=False).astype(np.int32).reshape(1, TOP)).cuda()
+    w = torch.full((1, TOP), 1.0 / TOP, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            ops.moe_layer(x, idx, w, gate, up, down)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ops.moe_layer(x, idx, w, gate, up, down)
+    for r in range(5):
+        x.copy_(to_dev(act(rng, (1, H)), "bfloat16"))
+        idx.copy_(torch.from_numpy(rng.choice(E, TOP, replace=False).astype(np.int32)
+                                   .reshape(1, TOP)).cuda())
+        w.copy_(torch.softmax(torch.from_numpy(rng.standard_normal((1, TOP))
+                                               .astype(np.float32)), -1).cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        want = _two_launch_layer(x, idx, w, gate, up, down)
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"replay {r}")
