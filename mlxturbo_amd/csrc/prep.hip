@@ -12,6 +12,9 @@ namespace {
 // Pairs whose keys the counting sort stages in LDS (larger P reads them from
 // memory on each pass).
 constexpr int kPrepLdsKeys = 24576;
+// Dynamic LDS limit of the table kernel: the CU's 160 KiB less room for its
+// static arrays.
+constexpr int kPrepLdsMax = 159 * 1024;
 constexpr int kPrepThreads = 1024;
 // Experts per thread of the table kernel (E + 1 keys over its threads).
 constexpr int kPrepPer = (kGatherPrepMaxE + 1 + kPrepThreads - 1) / kPrepThreads;
@@ -22,18 +25,48 @@ constexpr int kPrepPer = (kGatherPrepMaxE + 1 + kPrepThreads - 1) / kPrepThreads
 constexpr int kRunThreads = 256;
 constexpr int kRunPer = kPrepChunk / kRunThreads;
 
-// Dynamic LDS of the table kernel: counting-sort tables (4 (E + 1) ints) and
-// the staged keys.
+// Dynamic LDS of the table kernel: counting-sort tables (4 (E + 1) ints and
+// a spare counter), the staged keys, and where the whole fits the CU's
+// 160 KiB the sorted pair order (prep_lds_perm), written to memory in one
+// coalesced pass instead of as scattered 4-byte stores.
+__host__ __device__ inline bool prep_lds_perm(int64_t P, int64_t E) {
+  return P <= kPrepLdsKeys && 4 * (4 * (E + 1) + 1 + 2 * P) <= kPrepLdsMax;
+}
 inline size_t gather_prep_lds(int64_t P, int64_t E) {
-  return sizeof(int) * (size_t)(4 * (E + 1) + (P <= kPrepLdsKeys ? P : 0));
+  return sizeof(int) * (size_t)(4 * (E + 1) + 1 + (P <= kPrepLdsKeys ? P : 0) +
+                                (prep_lds_perm(P, E) ? P : 0));
 }
 
-// key of pair p: its expert, or E when the expert or the x index is invalid
+// key of pair p: its expert, or E when the expert or the x index is invalid.
+// Without lhs the x index p / (P / B) is in range exactly when p < (P / B) B
+// (no division per pair).
 __device__ __forceinline__ int prep_key(const int32_t* rhs, const int32_t* lhs, int p, int P,
                                         int E, int B) {
   const int e = rhs[p];
-  const int xb = x_batch(lhs, p, P, B);
-  return (e >= 0 && e < E && xb >= 0 && xb < B) ? e : E;
+  bool xok;
+  if (lhs) {
+    const int xb = lhs[p];
+    xok = xb >= 0 && xb < B;
+  } else {
+    xok = B > 0 && p < (P / B) * B;
+  }
+  return (e >= 0 && e < E && xok) ? e : E;
+}
+
+// Inclusive sum over the 64 lanes (all active): row scans by row_shr 1, 2,
+// 4, 8, then the row ends broadcast into the following rows (row_bcast 15
+// into rows 1 and 3, row_bcast 31 into rows 2 and 3); lanes without a
+// source add 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+#define MQ_SCAN_STEP(CTRL, ROWS) x += __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, false)
+  MQ_SCAN_STEP(0x111, 0xf);
+  MQ_SCAN_STEP(0x112, 0xf);
+  MQ_SCAN_STEP(0x114, 0xf);
+  MQ_SCAN_STEP(0x118, 0xf);
+  MQ_SCAN_STEP(0x142, 0xa);
+  MQ_SCAN_STEP(0x143, 0xc);
+#undef MQ_SCAN_STEP
+  return x;
 }
 
 // First of the two prep kernels, one workgroup per chunk of kPrepChunk
@@ -101,7 +134,7 @@ __global__ __launch_bounds__(kPrepThreads) void gather_prep_kernel(
     int R0, int R1, int C1, int R2, int C2, int32_t* __restrict__ ws) {
   extern __shared__ int sh[];
   const int NE = E + 1;  // bucket E collects out-of-range experts
-  __shared__ int wtot[3][16];
+  __shared__ int wtot[4][16];
   __shared__ int ctot[3];
   auto cls_of = [&](int c) { return (R2 > 0 && c >= C2) ? 2 : (R1 > 0 && c >= C1) ? 1 : 0; };
   auto r_of = [&](int k) { return k == 2 ? R2 : k == 1 ? R1 : R0; };
@@ -115,43 +148,32 @@ __global__ __launch_bounds__(kPrepThreads) void gather_prep_kernel(
   int32_t* hdr = ws + gather_ws_header(P);
   const int32_t* lower = ws + gather_ws_lower(P);
   const int32_t* order = ws + gather_ws_order(P);
-  // exclusive workgroup scan of three ints per thread: wave scans with
-  // cross-lane reads, then one wave over the wave totals
-  auto wg_scan3 = [&](const int (&v)[3], int (&excl)[3]) {
-    int x[3], below[3];
+  // exclusive workgroup scan of four ints per thread: DPP wave scans, then
+  // one wave over the wave totals
+  auto wg_scan4 = [&](const int (&v)[4], int (&excl)[4]) {
+    int x[4];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      x[i] = v[i];
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x[i], d, 64);
-        if (lane >= d) x[i] += y;
-      }
-      below[i] = __shfl_up(x[i], 1, 64);
+    for (int i = 0; i < 4; ++i) {
+      x[i] = wave_incl_scan(v[i]);
       if (lane == 63) wtot[i][wv] = x[i];
     }
     __syncthreads();
     if (wv == 0) {
 #pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        int z = lane < nw ? wtot[i][lane] : 0;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-          const int y = __shfl_up(z, d, 64);
-          if (lane >= d) z += y;
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int z = wave_incl_scan(lane < nw ? wtot[i][lane] : 0);
         if (lane < nw) wtot[i][lane] = z;
       }
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 3; ++i) excl[i] = (wv ? wtot[i][wv - 1] : 0) + (lane ? below[i] : 0);
+    for (int i = 0; i < 4; ++i) excl[i] = (wv ? wtot[i][wv - 1] : 0) + x[i] - v[i];
   };
-  // Segment numbering by class: thread-chunk counts ss[k] -> first segment
-  // id of the chunk in each class, in table order (class 2, 1, 0); the last
-  // thread writes the header and the total.
+  // Segment numbering by class: thread-chunk counts ss[k] and their
+  // exclusive scans sid[k] -> first segment id of the chunk in each class,
+  // in table order (class 2, 1, 0); the last thread writes the header and
+  // the total.
   auto class_ids = [&](const int (&ss)[3], int (&sid)[3]) {
-    wg_scan3(ss, sid);
     if (t == nt - 1) {
 #pragma unroll
       for (int k = 0; k < 3; ++k) ctot[k] = sid[k] + ss[k];
@@ -189,7 +211,10 @@ __global__ __launch_bounds__(kPrepThreads) void gather_prep_kernel(
           ss[k] += (c + R - 1) / R;
         }
       }
-      int sid[3];
+      const int v4[4] = {ss[0], ss[1], ss[2], 0};
+      int ex[4];
+      wg_scan4(v4, ex);
+      int sid[3] = {ex[0], ex[1], ex[2]};
       class_ids(ss, sid);
 #pragma unroll
       for (int i = 0; i < kPrepPer; ++i) {
@@ -208,17 +233,22 @@ __global__ __launch_bounds__(kPrepThreads) void gather_prep_kernel(
   }
 
   // ---- any order: counting sort by key ------------------------------------
+  // Keys staged with every load of a thread issued before the first store
+  // (clamped indices, no branch around the loads); the histogram and the
+  // scatter take 16 pairs per thread and round, their LDS atomics
+  // independent (the scatter's 16 returns in flight at once, pairs past P
+  // counting into the spare counter cur[NE]).
   int* cnt = sh;
   int* base = sh + NE;
   int* segb = sh + 2 * NE;
-  int* cur = sh + 3 * NE;
-  int* skey = sh + 4 * NE;
+  int* cur = sh + 3 * NE;                        // NE + 1 counters
+  int* skey = sh + 4 * NE + 1;
   const bool staged = P <= kPrepLdsKeys;
   if (staged) {
     for (int p0 = t; p0 < P; p0 += 16 * nt) {
       int k[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) k[i] = p0 + i * nt < P ? prep_key(rhs, lhs, p0 + i * nt, P, E, B) : 0;
+      for (int i = 0; i < 16; ++i) k[i] = prep_key(rhs, lhs, min(p0 + i * nt, P - 1), P, E, B);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int q = p0 + i * nt;
@@ -227,29 +257,35 @@ __global__ __launch_bounds__(kPrepThreads) void gather_prep_kernel(
     }
   }
   auto key_at = [&](int p) { return staged ? skey[p] : prep_key(rhs, lhs, p, P, E, B); };
-  for (int e = t; e < NE; e += nt) {
-    cnt[e] = 0;
+  for (int e = t; e <= NE; e += nt) {
+    if (e < NE) cnt[e] = 0;
     cur[e] = 0;
   }
   __syncthreads();
-  for (int p = t; p < P; p += nt) atomicAdd(&cnt[key_at(p)], 1);
+  for (int p0 = t; p0 < P; p0 += 16 * nt) {
+    int k[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) k[i] = key_at(min(p0 + i * nt, P - 1));
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (p0 + i * nt < P) atomicAdd(&cnt[k[i]], 1);
+  }
   __syncthreads();
-  // exclusive scans of cnt and of each class's segments over contiguous key
-  // chunks
+  // one scan: the keys' counts and each class's segments over contiguous
+  // key chunks
   int sc = 0, ss[3] = {0, 0, 0};
   for (int e = e0; e < e1; ++e) {
     sc += cnt[e];
     const int k = cls_of(cnt[e]), R = r_of(k);
     ss[k] += (cnt[e] + R - 1) / R;
   }
-  int rc3[3];
+  int ex[4];
   {
-    const int v[3] = {sc, 0, 0};
-    wg_scan3(v, rc3);
-    __syncthreads();                        // wtot is reused by the next scan
+    const int v4[4] = {ss[0], ss[1], ss[2], sc};
+    wg_scan4(v4, ex);
   }
-  int rc = rc3[0];
-  int rs[3];
+  int rc = ex[3];
+  int rs[3] = {ex[0], ex[1], ex[2]};
   class_ids(ss, rs);
   for (int e = e0; e < e1; ++e) {
     const int k = cls_of(cnt[e]), R = r_of(k);
@@ -259,9 +295,27 @@ __global__ __launch_bounds__(kPrepThreads) void gather_prep_kernel(
     rs[k] += (cnt[e] + R - 1) / R;
   }
   __syncthreads();
-  for (int p = t; p < P; p += nt) {
-    const int k = key_at(p);
-    perm[base[k] + atomicAdd(&cur[k], 1)] = p;
+  // the pair order: into LDS and then to memory in one coalesced pass
+  // (scattered 4-byte stores from this one CU took 5-8 us at 16384 pairs)
+  const bool lperm = prep_lds_perm(P, E);
+  int* sperm = skey + P;
+  for (int p0 = t; p0 < P; p0 += 16 * nt) {
+    int k[16], pos[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) k[i] = p0 + i * nt < P ? key_at(p0 + i * nt) : NE;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pos[i] = atomicAdd(&cur[k[i]], 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = p0 + i * nt;
+      if (q >= P) continue;
+      if (lperm) sperm[base[k[i]] + pos[i]] = q;
+      else perm[base[k[i]] + pos[i]] = q;
+    }
+  }
+  if (lperm) {
+    __syncthreads();
+    for (int i = t; i < P; i += nt) perm[i] = sperm[i];
   }
   for (int e = t; e < NE; e += nt) {
     const int c = cnt[e];
@@ -284,7 +338,7 @@ int launch_prep(const int32_t* rhs, const int32_t* lhs, int64_t P, int64_t E, in
   if (E < 0 || E > kGatherPrepMaxE || P < 1 || P > INT32_MAX / 4) return kStatusUnsupported;
   static std::atomic<uint64_t> lds_set{0};
   if (hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(&gather_prep_kernel),
-                                      (int)gather_prep_lds(kPrepLdsKeys, kGatherPrepMaxE), lds_set))
+                                      kPrepLdsMax, lds_set))
     return (int)e;
   const int64_t nch = (P + kPrepChunk - 1) / kPrepChunk;
   hipLaunchKernelGGL(prep_runs_kernel, dim3((unsigned)nch), dim3(kRunThreads), 0, st, rhs, lhs,
