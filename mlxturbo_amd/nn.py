@@ -284,8 +284,12 @@ class SwitchGLU(torch.nn.Module):
         g = self.gate_proj(xe, idx_use, sorted_indices=do_sort)
         u = self.up_proj(xe, idx_use, sorted_indices=do_sort)
         # SwiGLU in T as MLX evaluates it: each op in float, rounded to T
-        act = torch.nn.functional.silu(g.float()).to(g.dtype)
-        h = (act.float() * u.float()).to(g.dtype)
+        # (one kernel pass for bf16 / fp16)
+        if g.dtype in (torch.bfloat16, torch.float16) and g.dtype == u.dtype:
+            h = ops.swiglu(g, u)
+        else:
+            act = torch.nn.functional.silu(g.float()).to(g.dtype)
+            h = (act.float() * u.float()).to(g.dtype)
         if scores is not None and not do_sort and self.down_proj.bias is None:
             out = self._down_combine(h, idx, scores)
             return out.reshape(*lead, out.shape[-1])
