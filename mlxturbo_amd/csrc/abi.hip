@@ -490,9 +490,10 @@ int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
   if (dtype == MQ_FLOAT32)
     return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
   if (!aligned16(x) || !aligned16(h)) return fail(MQ_EINVAL, "x and h must be 16-byte aligned");
-  if (T != 1 || top_k > 8 || E > 512 || N1 > INT32_MAX || K1 > INT32_MAX || N2 > INT32_MAX)
+  if (T < 1 || T > 8 || top_k > 8 || T * top_k > 64 || E > 512 || N1 > INT32_MAX ||
+      K1 > INT32_MAX || N2 > INT32_MAX)
     return fail(MQ_EUNSUPPORTED,
-                "moe_block runs one token, top_k <= 8, E <= 512 (T=%lld top_k=%lld E=%lld)",
+                "moe_block runs 1-8 tokens, top_k <= 8, E <= 512 (T=%lld top_k=%lld E=%lld)",
                 (long long)T, (long long)top_k, (long long)E);
   if (N1 == 0 || N2 == 0) return fail(MQ_EUNSUPPORTED, "moe_block: empty projection");
   mq::RouteArgs ra;
@@ -505,8 +506,8 @@ int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
   int nl = 0;
   rc = dispatch_16<mq::MoeBlockLaunch>(dtype, bits, group_size, x, w_gate, scales_gate,
                                        biases_gate, w_up, scales_up, biases_up, w_down,
-                                       scales_down, biases_down, shared, h, out, N1, K1, N2, E,
-                                       ra, reinterpret_cast<hipStream_t>(hip_stream), &nl);
+                                       scales_down, biases_down, shared, h, out, T, N1, K1, N2,
+                                       E, ra, reinterpret_cast<hipStream_t>(hip_stream), &nl);
   if (rc) return fail(rc, "moe_block: no one-launch kernel for this configuration");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -535,10 +536,10 @@ int mq_moe_layer(const void* x, const int32_t* idx, const float* weights, const 
   if (dtype == MQ_FLOAT32)
     return fail(MQ_EUNSUPPORTED, "float32 activations are not implemented on this path");
   if (!aligned16(x) || !aligned16(h)) return fail(MQ_EINVAL, "x and h must be 16-byte aligned");
-  if (T != 1 || top_k > 8 || top_k > E || E > 512 || N1 > INT32_MAX || K1 > INT32_MAX ||
-      N2 > INT32_MAX || N1 == 0 || N2 == 0)
+  if (T < 1 || T > 8 || top_k > 8 || T * top_k > 64 || top_k > E || E > 512 ||
+      N1 > INT32_MAX || K1 > INT32_MAX || N2 > INT32_MAX || N1 == 0 || N2 == 0)
     return fail(MQ_EUNSUPPORTED,
-                "moe_layer runs one token, top_k <= 8, E <= 512 (T=%lld top_k=%lld E=%lld)",
+                "moe_layer runs 1-8 tokens, top_k <= 8, E <= 512 (T=%lld top_k=%lld E=%lld)",
                 (long long)T, (long long)top_k, (long long)E);
   mq::RouteArgs ra;
   ra.idx = const_cast<int32_t*>(idx);
@@ -547,8 +548,8 @@ int mq_moe_layer(const void* x, const int32_t* idx, const float* weights, const 
   int nl = 0;
   rc = dispatch_16<mq::MoeBlockLaunch>(dtype, bits, group_size, x, w_gate, scales_gate,
                                        biases_gate, w_up, scales_up, biases_up, w_down,
-                                       scales_down, biases_down, nullptr, h, out, N1, K1, N2, E,
-                                       ra, reinterpret_cast<hipStream_t>(hip_stream), &nl);
+                                       scales_down, biases_down, nullptr, h, out, T, N1, K1, N2,
+                                       E, ra, reinterpret_cast<hipStream_t>(hip_stream), &nl);
   if (rc) return fail(rc, "moe_layer: no one-launch kernel for this configuration");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail((int)e, "moe_layer: launch failed: %s", hipGetErrorString(e));

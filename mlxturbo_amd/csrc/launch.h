@@ -125,10 +125,11 @@ struct GatherFoldLaunch {
                  hipStream_t st, int* nlaunch);
 };
 
-// The decode MoE block of one token in one launch (block.cuh): the routing
-// of logits [E], the fused gate+up+SiLU gather into h [top_k, N1], the down
-// projection [E, N2, N1] with the router-weighted combine and, with shared /
-// ra.sgw, the shared-expert merge into out [N2]; the same bits as
+// The decode MoE block of T <= 8 tokens in one launch (block.cuh): the
+// routing of logits [T, E], the fused gate+up+SiLU gather into h
+// [T * top_k, N1], the down projection [E, N2, N1] with the router-weighted
+// combine and, with shared / ra.sgw, the shared-expert merge into out
+// [T, N2]; the same bits as
 // GluRouteLaunch followed by GatherFoldLaunch.  With ra.logits NULL the
 // experts and router weights are given in ra.idx / ra.w (the decode layer:
 // GluLaunch followed by GatherFoldLaunch).  kStatusUnsupported where its
@@ -139,7 +140,7 @@ struct MoeBlockLaunch {
   static int run(const void* x, const uint32_t* wg, const void* sg, const void* bg,
                  const uint32_t* wu, const void* su, const void* bu, const uint32_t* wd,
                  const void* sd, const void* bd, const void* shared, void* h, void* out,
-                 int64_t N1, int64_t K1, int64_t N2, int64_t E, const RouteArgs& ra,
+                 int64_t T, int64_t N1, int64_t K1, int64_t N2, int64_t E, const RouteArgs& ra,
                  hipStream_t st, int* nlaunch);
 };
 

@@ -247,10 +247,11 @@ class SwitchGLU(torch.nn.Module):
         if self._fused(idx.numel()):
             g, u = self.gate_proj, self.up_proj
             d = self.down_proj
-            if (idx.shape[0] == 1 and scores is not None and d.bias is None and g.mode == "affine"
+            if (idx.shape[0] <= ops._BLOCK_MAX_T and scores is not None and d.bias is None
+                    and g.mode == "affine"
                     and (d.group_size, d.bits, d.mode) == (g.group_size, g.bits, g.mode)):
-                # one token: the whole layer in one launch where it applies
-                out = ops._layer_one(x.reshape(1, -1), idx, scores,
+                # up to 8 tokens: the whole layer in one launch where it applies
+                out = ops._layer_fused(x.reshape(idx.shape[0], -1), idx, scores,
                                      (g.weight, g.scales, g.biases),
                                      (u.weight, u.scales, u.biases),
                                      (d.weight, d.scales, d.biases), g.group_size, g.bits)

@@ -958,8 +958,8 @@ def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
     if (sgw is None) != (shared is None):
         raise ValueError("sgw and shared are given together")
     T, H = x.shape
-    if T == 1:
-        out = _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits)
+    if 1 <= T <= _BLOCK_MAX_T:
+        out = _block_fused(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits)
         if out is not None:
             return out
     routed = _glu_routed(x, logits, top_k, gate, up, sgw, group_size, bits)
@@ -974,11 +974,16 @@ def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
                               sgate=sg, shared=shared)
 
 
-def _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits):
-    """The block of one token in one launch (mq_moe_block: the same bits as
-    the routed gate+up launch followed by the folded down projection, the
-    down tiles starting behind a grid-wide arrival inside the launch), or
-    None where that launch does not apply."""
+# mq_moe_block / mq_moe_layer take up to this many tokens
+_BLOCK_MAX_T = 8
+
+
+def _block_fused(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits):
+    """The block of T <= 8 tokens in one launch (mq_moe_block: the same bits
+    as the routed gate+up launch followed by the down projection and the
+    combine, the down tiles starting behind a grid-wide arrival inside the
+    launch), or None where that launch does not apply."""
+    T = x.shape[0]
     (wd, sd, bd) = down
     E = logits.shape[-1]
     if (wd.ndim != 3 or wd.shape[0] != E or bd is None or sd.dtype != x.dtype
@@ -992,15 +997,15 @@ def _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits):
     if _check_quant(wd, sd, bd, group_size, bits) != N1:
         raise ValueError(f"down bank K={wd.shape[-1] * 32 // bits} does not match the gate/up "
                          f"rows N={N1}")
-    if shared is not None and (tuple(shared.shape) != (1, N2) or shared.dtype != x.dtype):
-        raise ValueError(f"shared must be (1, {N2}) of x's dtype")
+    if shared is not None and (tuple(shared.shape) != (T, N2) or shared.dtype != x.dtype):
+        raise ValueError(f"shared must be ({T}, {N2}) of x's dtype")
     _require_gpu(wd, sd, bd, shared)
     dev = x.device
-    idx = torch.empty((1, top_k), dtype=torch.int32, device=dev)
-    wts = torch.empty((1, top_k), dtype=torch.float32, device=dev)
-    sgate = torch.empty((1, 1), dtype=x.dtype, device=dev) if sgw is not None else None
-    h = torch.empty((1, top_k, 1, N1), dtype=x.dtype, device=dev)
-    out = torch.empty((1, N2), dtype=x.dtype, device=dev)
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    sgate = torch.empty((T, 1), dtype=x.dtype, device=dev) if sgw is not None else None
+    h = torch.empty((T, top_k, 1, N1), dtype=x.dtype, device=dev)
+    out = torch.empty((T, N2), dtype=x.dtype, device=dev)
     x_ = _aligned(x.contiguous())
     lg = logits.contiguous()
     g_ = sgw.reshape(-1).contiguous() if sgw is not None else None
@@ -1009,7 +1014,7 @@ def _block_one(x, logits, top_k, gate, up, down, sgw, shared, group_size, bits):
     banks = [_aligned(t) for t in (wg, sg_, bg, wu, su, bu, wd, sd, bd)]
     rc = _lib.lib().mq_moe_block(x_.data_ptr(), lg.data_ptr(), *[t.data_ptr() for t in banks],
                                  _ptr(g_), _ptr(sh_), idx.data_ptr(), wts.data_ptr(),
-                                 _ptr(sgate), h.data_ptr(), out.data_ptr(), 1, top_k, N1, K1,
+                                 _ptr(sgate), h.data_ptr(), out.data_ptr(), T, top_k, N1, K1,
                                  N2, E, group_size, bits, _DTYPE_CODE[x.dtype], _stream_ptr(out))
     if rc == _EUNSUPPORTED:
         return None
@@ -1029,8 +1034,8 @@ def moe_layer(x: torch.Tensor, rhs_indices: torch.Tensor, weights: torch.Tensor,
     (mq_moe_layer) where its tile configuration applies."""
     T, K = x.shape
     idx = rhs_indices.reshape(T, -1)
-    if T == 1 and mode == "affine":
-        out = _layer_one(x, idx, weights, gate, up, down, group_size, bits)
+    if 1 <= T <= _BLOCK_MAX_T and mode == "affine":
+        out = _layer_fused(x, idx, weights, gate, up, down, group_size, bits)
         if out is not None:
             return out
     h = gather_glu(x.reshape(T, 1, 1, K), *gate, *up, rhs_indices=idx, group_size=group_size,
@@ -1039,14 +1044,15 @@ def moe_layer(x: torch.Tensor, rhs_indices: torch.Tensor, weights: torch.Tensor,
                               bits=bits, mode=mode)
 
 
-def _layer_one(x, idx, weights, gate, up, down, group_size, bits):
-    """One token's layer in one launch (mq_moe_layer), or None where that
-    launch does not apply."""
+def _layer_fused(x, idx, weights, gate, up, down, group_size, bits):
+    """The layer of T <= 8 tokens in one launch (mq_moe_layer), or None where
+    that launch does not apply."""
     (wg, sg_, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
-    top_k = idx.shape[-1]
+    T, top_k = x.shape[0], idx.shape[-1]
     if (x.dtype not in (torch.bfloat16, torch.float16) or bits not in (4, 8)
             or bg is None or bu is None or bd is None or wg.ndim != 3 or wg.shape != wu.shape
-            or wd.ndim != 3 or wd.shape[0] != wg.shape[0] or top_k > 8 or weights.numel() != top_k
+            or wd.ndim != 3 or wd.shape[0] != wg.shape[0] or top_k > 8 or T > _BLOCK_MAX_T
+            or T * top_k > 64 or idx.numel() != T * top_k or weights.numel() != T * top_k
             or sg_.dtype != x.dtype or su.dtype != x.dtype or sd.dtype != x.dtype
             or any(w.dtype not in (torch.uint32, torch.int32) for w in (wg, wu, wd))):
         return None
@@ -1060,14 +1066,14 @@ def _layer_one(x, idx, weights, gate, up, down, group_size, bits):
     if _check_quant(wd, sd, bd, group_size, bits) != N1:
         return None
     N2 = wd.shape[1]
-    h = torch.empty((1, top_k, 1, N1), dtype=x.dtype, device=dev)
-    out = torch.empty((1, N2), dtype=x.dtype, device=dev)
+    h = torch.empty((T, top_k, 1, N1), dtype=x.dtype, device=dev)
+    out = torch.empty((T, N2), dtype=x.dtype, device=dev)
     x_ = _aligned(x.contiguous())
     idx_ = idx.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
     w_ = weights.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
     banks = [_aligned(t) for t in (wg, sg_, bg, wu, su, bu, wd, sd, bd)]
     rc = _lib.lib().mq_moe_layer(x_.data_ptr(), idx_.data_ptr(), w_.data_ptr(),
-                                 *[t.data_ptr() for t in banks], h.data_ptr(), out.data_ptr(), 1,
+                                 *[t.data_ptr() for t in banks], h.data_ptr(), out.data_ptr(), T,
                                  top_k, N1, K1, N2, E, group_size, bits, _DTYPE_CODE[x.dtype],
                                  _stream_ptr(out))
     if rc == _EUNSUPPORTED:

@@ -13,8 +13,9 @@ GLU and the down projection at the matmul tolerance, the combine with the
 shared merge bit for bit); the routing inside the gate+up launch gives the
 routing kernel's and the GLU gather's bits; the one-launch block of one
 token (mq_moe_block) gives the two launches' bits on fresh routings, in
-graph replays and across calls of other shapes; launch counts (1 launch at
-T = 1, 2 at T = 2, 3 above).
+graph replays and across calls of other shapes, and so does the one-launch
+block of 2-8 tokens over the gather launches' tile configurations; launch
+counts (1 launch up to 8 tokens).
 """
 
 import numpy as np
@@ -60,10 +61,8 @@ def test_moe_block(banks, T, with_shared):
     before = mq.launch_count()
     out = ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
     launches = mq.launch_count() - before
-    # one token: the whole block in one launch; else routing inside the
-    # gate+up launch, then the folded down (T <= 2) or the down gather and
-    # the combine
-    assert launches == (1 if T == 1 else 2 if T * TOP <= 16 else 3)
+    # up to 8 tokens: the whole block in one launch
+    assert launches == 1
     assert out.shape == (T, H)
 
     # the three steps one by one
@@ -351,8 +350,8 @@ def test_block_one_launch_declines(E_, top, H_, I_, gs):
 
 
 def _two_launch_layer(x, idx, w, gate, up, down, gs=64, bits=4):
-    h = ops.gather_glu(x.reshape(1, 1, 1, -1), *gate, *up, rhs_indices=idx, group_size=gs,
-                       bits=bits)
+    h = ops.gather_glu(x.reshape(x.shape[0], 1, 1, -1), *gate, *up, rhs_indices=idx,
+                       group_size=gs, bits=bits)
     return ops.gather_qmm_combine(h, *down, idx, w, group_size=gs, bits=bits)
 
 
@@ -420,3 +419,112 @@ def test_layer_one_launch_graph_replays(banks):
         torch.cuda.synchronize()
         want = _two_launch_layer(x, idx, w, gate, up, down)
         np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"replay {r}")
+
+
+@pytest.mark.parametrize("T", [2, 3, 4, 5, 8])
+def test_block_multi_token(banks, T):
+    """2-8 tokens in one launch (segments of pairs sharing an expert, the
+    gather launches' tile configurations: gate/up over 4 waves at T = 2, 2
+    waves with the scale copy at T = 3-4, 1 wave at T = 5-8): 6 calls with
+    fresh zipf-skewed and tied logits, with and without the shared expert,
+    each equal to the routed gate+up launch then the down projection and the
+    combine, bit for bit."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(300 + T)
+    for i in range(6):
+        with_shared = i % 2 == 0
+        x = to_dev(act(rng, (T, H)), "bfloat16")
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        lg = lg - 0.5 * np.log(np.arange(1, E + 1, dtype=np.float32)) if i % 3 == 1 else lg
+        lg = np.round(lg * 4) / 4 if i % 3 == 2 else lg
+        logits = torch.from_numpy(lg).cuda()
+        sgw = to_dev(act(rng, (H,), scale=0.02), "bfloat16") if with_shared else None
+        shared = to_dev(act(rng, (T, H), scale=0.1), "bfloat16") if with_shared else None
+        out = _block_launch(x, logits, TOP, gate, up, down, sgw, shared)
+        want = _two_launch_block(x, logits, TOP, gate, up, down, sgw, shared)[0]
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"T={T} call {i}")
+
+
+@pytest.mark.parametrize("T", [2, 4, 7])
+def test_layer_multi_token(banks, T):
+    """The layer of 2-8 tokens with the routing given, in one launch: repeated
+    experts across tokens (shared segments), an out-of-range expert, equal to
+    gather_glu then gather_qmm_combine bit for bit; interleaved with blocks
+    of other token counts over the same arrival flags."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(400 + T)
+    for i in range(5):
+        x = to_dev(act(rng, (T, H)), "bfloat16")
+        e = np.stack([rng.choice(E, TOP, replace=False) for _ in range(T)]).astype(np.int32)
+        if i % 2 == 1:
+            e[1:, 0] = e[0, 0]                           # one expert in every token
+        if i == 3:
+            e[0, 5] = E + 3                              # out of range: a zero row
+        idx = torch.from_numpy(e).cuda()
+        w = torch.softmax(torch.from_numpy(rng.standard_normal((T, TOP)).astype(np.float32)),
+                          -1).cuda()
+        before = mq.launch_count()
+        out = ops.moe_layer(x, idx, w, gate, up, down)
+        assert mq.launch_count() - before == 1
+        np.testing.assert_array_equal(bits16(out),
+                                      bits16(_two_launch_layer(x, idx, w, gate, up, down)),
+                                      err_msg=f"T={T} call {i}")
+        T2 = 1 + (T + i) % 8
+        x2 = to_dev(act(rng, (T2, H)), "bfloat16")
+        lg = torch.from_numpy(rng.standard_normal((T2, E)).astype(np.float32)).cuda()
+        ob = _block_launch(x2, lg, TOP, gate, up, down, None, None)
+        np.testing.assert_array_equal(
+            bits16(ob), bits16(_two_launch_block(x2, lg, TOP, gate, up, down, None, None)[0]))
+
+
+def test_block_multi_token_graph_replays(banks):
+    """A captured 4-token block replayed 4 times with new logits and x."""
+    (_, gate), (_, up), (_, down) = banks
+    rng = np.random.default_rng(17)
+    T = 4
+    x = to_dev(act(rng, (T, H)), "bfloat16")
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
+    sgw = to_dev(act(rng, (H,), scale=0.02), "bfloat16")
+    shared = to_dev(act(rng, (T, H), scale=0.1), "bfloat16")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ops.moe_block(x, logits, TOP, gate, up, down, sgw=sgw, shared=shared)
+    for r in range(4):
+        x.copy_(to_dev(act(rng, (T, H)), "bfloat16"))
+        logits.copy_(torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        want = _two_launch_block(x, logits, TOP, gate, up, down, sgw, shared)[0]
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"replay {r}")
+
+
+def test_block_multi_token_rounds_without_expert():
+    """Three tokens whose logits leave 3 choosable experts each (rounds 3..7
+    route to -1, zero rows), then two tokens (the 4-wave configuration), on
+    a 64-expert bank: the one-launch blocks equal the two launches."""
+    rng = np.random.default_rng(43)
+    E_, top, H_, I_ = 64, 8, 2048, 512
+
+    def bank(N, K):
+        w, s_, b = quantized(rng, E_ * N, K)
+        return (to_dev(w).view(E_, N, -1), to_dev(s_, "bfloat16").view(E_, N, -1),
+                to_dev(b, "bfloat16").view(E_, N, -1))
+
+    gate, up, down = bank(I_, H_), bank(I_, H_), bank(H_, I_)
+    for T in (3, 2):
+        x = to_dev(act(rng, (T, H_)), "bfloat16")
+        lb = np.full((T, E_), -1, dtype=np.int32)
+        for t in range(T):
+            keep = rng.choice(E_, 3, replace=False)
+            lb[t, keep] = rng.standard_normal(3).astype(np.float32).view(np.int32)
+        logits = torch.from_numpy(lb.view(np.float32)).cuda()
+        out = _block_launch(x, logits, top, gate, up, down, None, None)
+        want, idx, _, _, _ = _two_launch_block(x, logits, top, gate, up, down, None, None)
+        assert (idx.cpu().numpy()[:, 3:] == -1).all()
+        np.testing.assert_array_equal(bits16(out), bits16(want), err_msg=f"T={T}")
