@@ -259,10 +259,11 @@ int mq_moe_glu_route(const void* x, const float* logits, const uint32_t* w_gate,
                      void* hip_stream);
 
 /*
- * The whole decode MoE block of one token in one launch: mq_moe_glu_route
- * (x [K1], logits [E], gate / up banks [E, N1, K1] -> idx, weights, sgate,
- * h [top_k, N1]) followed by mq_gather_qmm_combine(h, down bank [E, N2, N1],
- * idx, weights, sgate, shared [N2] -> out [N2]), bit for bit.  The down
+ * The whole decode MoE block of T <= 8 tokens in one launch:
+ * mq_moe_glu_route (x [T, K1], logits [T, E], gate / up banks [E, N1, K1]
+ * -> idx, weights, sgate, h [T * top_k, N1]) followed by
+ * mq_gather_qmm_combine(h, down bank [E, N2, N1], idx, weights, sgate,
+ * shared [T, N2] -> out [T, N2]), bit for bit.  The down
  * projection starts behind a grid-wide arrival inside the launch (device-
  * scope stores of h and per-workgroup flags in a static device array of the
  * library), so calls that overlap on one GPU race; a stream's calls run in
@@ -270,10 +271,11 @@ int mq_moe_glu_route(const void* x, const float* logits, const uint32_t* w_gate,
  * 151-327), its fused decode gate/up and down (kernels/moe_decode_fused.py:
  * 331-397) and its combine with the shared expert (moe_route_decode.py:
  * 353-398) as separate dispatches.  sgw / sgate / shared are all given or
- * all NULL.  One token (T = 1), top_k <= 8, E <= 512; other calls, tile
- * configurations other than the decode gather's 4-wave gate/up tiles and
- * one-wave down tiles, or a grid that does not fit the device at once
- * return MQ_EUNSUPPORTED, and the caller makes the two calls.
+ * all NULL.  T = 1 .. 8, top_k <= 8, T * top_k <= 64, E <= 512; other
+ * calls, tile configurations other than the decode gathers' (gate/up tiles
+ * over 4 waves, or over 2 or 1 with the scale copy; down tiles on one
+ * wave), or a grid that does not fit the device at once return
+ * MQ_EUNSUPPORTED, and the caller makes the two calls.
  */
 int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
                  const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
@@ -284,18 +286,19 @@ int mq_moe_block(const void* x, const float* logits, const uint32_t* w_gate,
                  int64_t E, int group_size, int bits, int dtype, void* hip_stream);
 
 /*
- * The decode MoE layer of one token with its routing given, in one launch:
- * mq_gather_glu(x [1, 1, K1], gate bank, up bank, lhs NULL, rhs idx [top_k],
- * h [top_k, N1], P = top_k, B = 1, M = 1, ...) followed by
- * mq_gather_qmm_combine(h, down bank [E, N2, N1], idx, weights [top_k]
- * (float router weights), no shared expert -> out [N2]), bit for bit, with
- * mq_moe_block's grid-wide arrival (calls that overlap on one GPU race).
+ * The decode MoE layer of T <= 8 tokens with its routing given, in one
+ * launch: mq_gather_glu(x [T, 1, K1], gate bank, up bank, lhs NULL, rhs idx
+ * [T, top_k], h [T * top_k, N1], P = T * top_k, B = T, M = 1, ...) followed
+ * by mq_gather_qmm_combine(h, down bank [E, N2, N1], idx, weights
+ * [T, top_k] (float router weights), no shared expert -> out [T, N2]), bit
+ * for bit, with mq_moe_block's grid-wide arrival (calls that overlap on
+ * one GPU race).
  * The reference's decode layer runs its fused gate/up and its down kernel
  * with the combine as separate dispatches (kernels/moe_decode_fused.py:
  * 331-397, kernels/moe_combine.py:160-195; fused.py:2456-2492).  An expert
- * outside [0, E) gives a zero row.  T = 1, top_k <= 8, E <= 512 and
- * mq_moe_block's tile and grid limits, else MQ_EUNSUPPORTED and the caller
- * makes the two calls.
+ * outside [0, E) gives a zero row.  mq_moe_block's limits (T <= 8,
+ * top_k <= 8, T * top_k <= 64, E <= 512, tiles, grid), else
+ * MQ_EUNSUPPORTED and the caller makes the two calls.
  */
 int mq_moe_layer(const void* x, const int32_t* idx, const float* weights, const uint32_t* w_gate,
                  const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
