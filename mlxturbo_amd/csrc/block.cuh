@@ -1,4 +1,4 @@
-// The decode MoE block of one token in one launch: routing, the fused
+// The decode MoE block of 1-8 tokens in one launch: routing, the fused
 // gate+up+SiLU gather, and the down projection with the router-weighted
 // combine and the shared-expert merge.
 //
@@ -22,6 +22,13 @@
 // way.  No L2 write-back
 // or invalidate runs (a device-scope release per workgroup cost more than
 // the launch it would save, since it writes back the XCD's whole L2).
+//
+// Two to eight tokens (moe_blockn_kernel) take the same two phases with
+// the tile configurations the separate gather launches pick for those
+// shapes: token t is routed on wave t, the pairs are grouped into segments
+// of up to min(8, T) pairs sharing an expert (one dequantized tile serves
+// them all), phase-1 units are (segment, 16 columns) per wave group, and
+// phase 2 deals (16-column block, token group) units.
 //
 // The epoch (a device word) is read by every workgroup at its start and
 // advanced by workgroup 0 once every flag holds epoch + 1, that is once

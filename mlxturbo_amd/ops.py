@@ -952,8 +952,8 @@ def moe_block(x: torch.Tensor, logits: torch.Tensor, top_k: int, gate, up, down,
     are ``(w, scales, biases)`` banks.  Returns ``(T, H_out)``: the same
     bits as calling the three steps one by one.  Up to 64 (token, expert)
     pairs over up to 512 experts the routing runs inside the gate+up
-    launch (mq_moe_glu_route), one launch less on the dependent chain; one
-    token runs the whole block as one launch (mq_moe_block) where its tile
+    launch (mq_moe_glu_route), one launch less on the dependent chain; up to
+    8 tokens run the whole block as one launch (mq_moe_block) where its tile
     configuration applies."""
     if (sgw is None) != (shared is None):
         raise ValueError("sgw and shared are given together")
@@ -1030,8 +1030,8 @@ def moe_layer(x: torch.Tensor, rhs_indices: torch.Tensor, weights: torch.Tensor,
     then ``gather_qmm_combine(h, down, rhs_indices, weights)``.  ``x`` is
     ``(T, K)``, ``rhs_indices`` and the router ``weights`` ``(T, top_k)``;
     ``gate``, ``up``, ``down`` are ``(w, scales, biases)`` banks.  Returns
-    ``(T, N)``, the bits of the two calls; one token runs both in one launch
-    (mq_moe_layer) where its tile configuration applies."""
+    ``(T, N)``, the bits of the two calls; up to 8 tokens run both in one
+    launch (mq_moe_layer) where its tile configurations apply."""
     T, K = x.shape
     idx = rhs_indices.reshape(T, -1)
     if 1 <= T <= _BLOCK_MAX_T and mode == "affine":
