@@ -257,7 +257,8 @@ int mq_quantized_matmul_ws(const void* x, const uint32_t* w, const void* scales,
                   hipGetErrorString((hipError_t)rc));
   }
   rc = dispatch_16<mq::SkinnyLaunch>(dtype, bits, group_size, x, w, scales, biases, out, M, N, K,
-                                     st, &nl);
+                                     split_ok ? workspace : nullptr,
+                                     split_ok ? workspace_bytes : (size_t)0, st, &nl);
   if (rc) return fail(rc, "quantized_matmul: no kernel for dtype=%d bits=%d group_size=%d", dtype,
                       bits, group_size);
   hipError_t e = hipGetLastError();

@@ -18,11 +18,15 @@ struct DequantLaunch {
 };
 
 // quantized_matmul for M rows, in launches of up to 16 rows, or 32 on the
-// shared-x workgroups (qmv.cuh); *nlaunch counts the kernels enqueued.
+// shared-x workgroups (qmv.cuh); with a workspace (ws, ws_bytes; may be
+// NULL) of skinny_split_bytes(...) bytes, launches of 5-16 rows on
+// matrices of few tiles run their K slices on separate workgroups (same
+// bits).  *nlaunch counts the kernels enqueued.
 template <int DT, int BITS, int GS>
 struct SkinnyLaunch {
   static int run(const void* x, const uint32_t* w, const void* s, const void* b, void* out,
-                 int64_t M, int64_t N, int64_t K, hipStream_t st, int* nlaunch);
+                 int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, hipStream_t st,
+                 int* nlaunch);
 };
 
 // quantized_matmul of one row on the quad kernel (qmv_quad.cuh, its own
@@ -347,8 +351,31 @@ inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cu
 
 // Workspace bytes of quantized_matmul (K splits of the wide kernel), 0 when
 // the chosen plan needs none.
+// K slices (the waves of the one-workgroup launch, 8 on matrices of fewer
+// than 640 16-row tiles) that a skinny launch of m rows runs on separate
+// workgroups (qmv.cuh qmv_split_kernel), or 0: 5-16 rows (16 streamed x
+// rows: steps of at most 256 codes), 8 slices, K whole steps.  K=17408
+// N=5120, one box: M=8 / 9 / 16 20.9-21.2 / 21.4 / 21.6 us against
+// 21.6-21.8 / 23.0-23.2 / 24.1-24.5 on one workgroup per tile group; 2 and
+// 4 rows lost (20.6-21.1 against 17.9-19.4).
+inline int skinny_split_slices(int64_t m, int64_t N, int64_t K, int bits, int gs) {
+  const int64_t stepg = (bits == 4 && gs == 32) ? 8 : 4;   // groups per step
+  if (m < 5 || m > 16 || (N + 15) / 16 >= 640 || stepg * gs > 256 || (K / gs) % stepg) return 0;
+  return 8;
+}
+
+// Float partial planes of the split skinny launches of an M-row call.
+inline size_t skinny_split_bytes(int64_t M, int64_t N, int64_t K, int bits, int gs) {
+  int64_t most = 0;                                 // rows of the largest split launch
+  for (int64_t r = M; r > 0; r -= 16) {
+    const int64_t mt = r < 16 ? r : 16;
+    if (skinny_split_slices(mt, N, K, bits, gs)) most = mt > most ? mt : most;
+  }
+  return (size_t)most * N * 8 * sizeof(float);
+}
+
 inline size_t qmm_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits, int gs, int cus) {
-  if (!wide_route(M, N, K, bits, gs, cus, true)) return 0;
+  if (!wide_route(M, N, K, bits, gs, cus, true)) return skinny_split_bytes(M, N, K, bits, gs);
   return wide_workspace_bytes(wide_plan(M, N, K, cus), M, N);
 }
 

@@ -49,6 +49,10 @@
 //    weight fragment with two 16-row A tiles (x staged in one buffer per
 //    slice, a barrier before and after).  Each group's arithmetic is that of
 //    the one-group launch.
+//  * Given a workspace, 5-16 rows on matrices of fewer than 640 tiles (K=17408
+//    N=5120) run each tile's K slices on separate workgroups, one slice per
+//    workgroup over ten whole tiles, and a second kernel adds the float
+//    slices in order: the same arithmetic as the one-workgroup launch.
 //  * Dequantization is the exact fma_mix trick of mq_common.h, rounded to T
 //    per weight (bit-exact MLX dequantization); the packed T pairs are the
 //    B operand of v_mfma_f32_16x16x32 (32 k x 16 rows).  A and B use the same
@@ -256,11 +260,14 @@ __host__ __device__ inline size_t qmv_shx_lds(int NW, int XM) {
 // rows (group grp of them); the x slices live in the qmv_shx_lds(NW, XM)
 // bytes at xsh, shared by the groups, and qmv_smem then only holds the
 // group's scale copy.  Each group's arithmetic is the SHX = 1 arithmetic.
+// SPLIT (NW = 1): the wave runs K slice ksl of nsl (the slice wave ksl of
+// an nsl-wave group runs) and hands its float tiles to a combining Rows.
 template <int DT, int BITS, int GS, int GPL, int NW, int PF, int XM, bool SBL, int TJ, int SHX = 1,
-          bool XRES = false, int MT = 1, class Rows>
+          bool XRES = false, int MT = 1, bool SPLIT = false, class Rows>
 __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, const Rows& src,
                                          unsigned char* qmv_smem, f32x4 (*red)[64], int kw,
-                                         int gt, unsigned char* xsh = nullptr, int grp = 0) {
+                                         int gt, unsigned char* xsh = nullptr, int grp = 0,
+                                         int ksl = 0, int nsl = 1) {
   using Gm = QmvGeom<BITS, GS, GPL>;
   constexpr int STEPG = Gm::STEPG, STEPB = Gm::STEPB, STEPK = Gm::STEPK, NSV = Gm::NSV;
   constexpr int NL = Gm::NL, CPL = Gm::CPL, MPL = Gm::MPL, SH = Gm::SH;
@@ -277,6 +284,7 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   static_assert(!XRES || (XM > 0 && SBL), "resident x is filled with the scale copy");
   static_assert(MT == 1 || (SHX > 1 && !XRES && XM == 16 * MT && NW > 1),
                 "16-row A tiles beyond the first share staged x slices");
+  static_assert(!SPLIT || (NW == 1 && Rows::kCombine), "a split slice hands floats on");
   using T = T16<DT>;
   struct Stage {
     u32x4 w[TJ][NL];
@@ -305,8 +313,9 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
 
   const int nsteps = (G + STEPG - 1) / STEPG;
   const int full = G / STEPG;                 // steps with every group inside K
-  const int sb = (int)((int64_t)nsteps * wave / NW);
-  const int se = (int)((int64_t)nsteps * (wave + 1) / NW);
+  const int sw = SPLIT ? ksl : wave, swn = SPLIT ? nsl : NW;   // K slice of this wave
+  const int sb = (int)((int64_t)nsteps * sw / swn);
+  const int se = (int)((int64_t)nsteps * (sw + 1) / swn);
   const int fe = se < full ? se : full;      // pipelined (unchecked) steps: [sb, fe)
 
   const int xr = min(r, M - 1);              // A row of this lane (rows >= M repeat row M-1)
@@ -614,8 +623,8 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   if constexpr (SHX > 1 && !XRES) {
     // every wave takes as many steps as the longest slice (each step's
     // staging ends with a workgroup barrier); steps past its own are dead
-    int nmax = 0;
-    for (int w2 = 0; w2 < NW; ++w2) {
+    int nmax = SPLIT ? fe - sb : 0;          // SPLIT: every group runs the one slice
+    for (int w2 = 0; w2 < (SPLIT ? 0 : NW); ++w2) {
       const int b2 = (int)((int64_t)nsteps * w2 / NW);
       const int e2 = min((int)((int64_t)nsteps * (w2 + 1) / NW), full);
       nmax = max(nmax, e2 - b2);
@@ -829,6 +838,101 @@ __global__ __launch_bounds__(64 * NW * NG) void qmv_shx_kernel(
       tl, M, K, src, gsm, red + g * NW * TJ * MT, kw, threadIdx.x - 64 * NW * g, qmv_smem, g);
 }
 
+// Float tiles of one K slice: A row m, column n of [n0, n1) to part[m N + n].
+struct SplitRows {
+  static constexpr bool kCombine = true;
+  const uint16_t* x;
+  uint32_t x_nrec;
+  float* part;
+  int64_t ldx;
+  int N, n0, n1;
+  __device__ __forceinline__ int64_t xoff(int m) const { return (int64_t)m * ldx; }
+  template <int TJ>
+  __device__ __forceinline__ void store_combined(int m, int nn, const float (&v)[TJ]) const {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      if (n0 + 16 * j + nn < n1) part[(int64_t)m * N + n0 + 16 * j + nn] = v[j];
+  }
+};
+
+// The K slices of a skinny launch over separate workgroups (5-16 rows on
+// matrices of few tiles).  The one-workgroup launch runs a tile's nsl K
+// slices on the nsl waves of one workgroup, so every workgroup streams all
+// of x (16 x 17408 x 2 B = 557 KB per workgroup at K=17408, three times the
+// weight bytes of the call) and 20 rows per CU run as a 16- and a 4-row
+// tile.  Here workgroup i runs K slice i % nsl (launch order deals
+// consecutive workgroups to the 8 XCDs, so each XCD's L2 serves one slice of
+// x) over the whole 16-row tiles [b T / B, (b + 1) T / B) of the T =
+// ceil(N / 16), b = i / nsl, B = grid / nsl, on NG one-wave groups of TJ
+// tiles that stage each step's x slice once for the workgroup.  Each wave's
+// arithmetic is that of wave i % nsl of the one-workgroup launch (same
+// steps, same accumulator); its float tile goes to part[i % nsl], and
+// qmv_split_sum_kernel adds the nsl planes in slice order and rounds once,
+// as that launch's cross-wave sum does, so the bits are the same.  K must be
+// whole steps.  Block 64 NG, dynamic LDS qmv_shx_lds(1, 16).
+template <int DT, int BITS, int GS, int GPL, int PF, int TJ, int NG>
+__global__ __launch_bounds__(64 * NG) void qmv_split_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    float* __restrict__ part, int M, int N, int K, int64_t ldx, int nsl) {
+  extern __shared__ __align__(16) unsigned char qmv_smem[];
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = (int)(blockIdx.x % (unsigned)nsl);
+  const int64_t blk = blockIdx.x / (unsigned)nsl, nblk = gridDim.x / (unsigned)nsl;
+  const int64_t nt = (N + 15) / 16;
+  const int64_t t0 = blk * nt / nblk, t1 = (blk + 1) * nt / nblk;
+  const int64_t g0 = t0 + TJ * g < t1 ? t0 + TJ * g : t1;
+  const int64_t g1 = g0 + TJ < t1 ? g0 + TJ : t1;
+  const int n0 = (int)(16 * g0 < N ? 16 * g0 : N);
+  const int n1 = (int)(16 * g1 < N ? 16 * g1 : N);
+  const uint32_t rowB = (uint32_t)K * BITS / 8;
+  const uint32_t sRowB = (uint32_t)(K / GS) * 2;
+  QmvTiles<TJ> tl;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int nj = n0 + 16 * j;
+    const int rj = min(16, n1 - nj);
+    const int64_t base = rj > 0 ? nj : 0;
+    tl.w[j] = reinterpret_cast<const char*>(w) + base * rowB;
+    tl.s[j] = reinterpret_cast<const char*>(scales) + base * sRowB;
+    tl.b[j] = reinterpret_cast<const char*>(biases) + base * sRowB;
+    tl.rows[j] = rj;
+  }
+  const SplitRows src{x,  (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2),
+                      part + (int64_t)ks * M * N, ldx, N, n0, n1};
+  qmv_tile<DT, BITS, GS, GPL, 1, PF, 16, false, TJ, NG, false, 1, true>(
+      tl, M, K, src, qmv_smem, nullptr, 0, threadIdx.x & 63, qmv_smem, g, ks, nsl);
+}
+
+// out[i] = round(part[0][i] + part[1][i] + ... + part[NSL - 1][i]), the
+// planes added in slice order (the order of the one-workgroup launch's
+// cross-wave sum); mn = M N outputs, rows of N contiguous.  The NSL loads
+// are issued together (a loop over a run-time count waited for each in
+// turn: 4.6 us per call at M=16 N=5120).
+template <int DT, int NSL>
+__global__ __launch_bounds__(256) void qmv_split_sum_kernel(const float* __restrict__ part,
+                                                            uint16_t* __restrict__ out,
+                                                            int64_t mn) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= mn) return;
+  float p[NSL];
+#pragma unroll
+  for (int q = 0; q < NSL; ++q) p[q] = part[q * mn + i];
+  float v = p[0];
+#pragma unroll
+  for (int q = 1; q < NSL; ++q) v += p[q];
+  out[i] = T16<DT>::round1(v);
+}
+
+// One-wave groups per split workgroup and tiles per group.  K=17408 N=5120
+// (320 tiles x 8 slices, one box, graph-timed): 10 x 1 on 256 workgroups
+// M=16 22.9-23.1 us, M=9 22.2-22.3, against 24.1-24.5 / 23.0-23.2 for the
+// one-workgroup launch; 5 x 1 on 512 23.95-24.0, 5 x 2 26.4-26.5, 2 x 1 on
+// 1280 26.9.  Deeper prefetch lost (10 x 1, M=16: 3 / 4 / 6 / 8 stages
+// 24.5 / 25.6 / 27.8 / 29.8 us against 23.1 with 2).
+constexpr int kQmvSplitNG = 10;
+constexpr int kQmvSplitTJ = 1;
+
 // Wave groups per shared-x workgroup and tiles per group (K=5120 N=17408
 // M=16, one process: 3 x 2 19.4 us, 2 x 3 20.5, 4 x 2 21.6, against 21.4
 // for one group of two tiles on three workgroups per CU).
@@ -908,10 +1012,31 @@ inline int skinny_launch_shx(int xm, const uint16_t* x, const uint32_t* w, const
   return kStatusUnsupported;
 }
 
+// One split launch (qmv_split_kernel then qmv_split_sum_kernel) of M <= 16
+// rows: nsl float planes of M x N in part.
+template <int DT, int BITS, int GS>
+inline int skinny_launch_split(const uint16_t* x, const uint32_t* w, const void* s, const void* b,
+                               uint16_t* out, int M, int64_t N, int64_t K, float* part, int nsl,
+                               hipStream_t st) {
+  using C = QmvConf<BITS, GS>;
+  if (nsl != 8) return kStatusUnsupported;            // the sum kernel adds 8 planes
+  constexpr int per = kQmvSplitNG * kQmvSplitTJ;
+  const int64_t nblk = ((N + 15) / 16 + per - 1) / per;
+  const size_t lds = qmv_shx_lds<BITS, GS, C::GPL>(1, 16);
+  hipLaunchKernelGGL((qmv_split_kernel<DT, BITS, GS, C::GPL, C::PF, kQmvSplitTJ, kQmvSplitNG>),
+                     dim3((unsigned)(nblk * nsl)), dim3(64 * kQmvSplitNG), lds, st, x, w,
+                     (const uint16_t*)s, (const uint16_t*)b, part, M, (int)N, (int)K,
+                     (int64_t)K, nsl);
+  const int64_t mn = (int64_t)M * N;
+  hipLaunchKernelGGL((qmv_split_sum_kernel<DT, 8>), dim3((unsigned)((mn + 255) / 256)), dim3(256),
+                     0, st, part, out, mn);
+  return 0;
+}
+
 template <int DT, int BITS, int GS, int NW>
 inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, const void* b,
-                            void* out, int64_t M, int64_t N, int64_t K, hipStream_t st,
-                            int* nlaunch) {
+                            void* out, int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes,
+                            hipStream_t st, int* nlaunch) {
   using C = QmvConf<BITS, GS>;
   const int G = (int)(K / GS);
   for (int64_t m0 = 0, step = 16; m0 < M; m0 += step, ++*nlaunch) {
@@ -919,6 +1044,18 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
     const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
     const uint16_t* xp = (const uint16_t*)x + m0 * K;
     uint16_t* op = (uint16_t*)out + m0 * N;
+    // 5-16 rows on matrices of few tiles, with the caller's workspace: the
+    // K slices on separate workgroups (same bits)
+    if (ws && skinny_split_slices(mt, N, K, BITS, GS) == NW &&
+        ws_bytes >= (size_t)mt * N * NW * sizeof(float) && (int64_t)mt * K * 2 < ((int64_t)1 << 31)) {
+      if constexpr (QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
+        if (int rc = skinny_launch_split<DT, BITS, GS>(xp, w, s, b, op, mt, N, K, (float*)ws, NW,
+                                                       st))
+          return rc;
+        ++*nlaunch;
+        continue;
+      }
+    }
     if constexpr (NW == 4 && QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
       // 17-32 rows: one shared-x launch whose groups multiply every weight
       // fragment with two 16-row A tiles (x staged once per step, in one
@@ -994,10 +1131,10 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
 template <int DT, int BITS, int GS>
 int SkinnyLaunch<DT, BITS, GS>::run(const void* x, const uint32_t* w, const void* s,
                                     const void* b, void* out, int64_t M, int64_t N, int64_t K,
-                                    hipStream_t st, int* nlaunch) {
+                                    void* ws, size_t ws_bytes, hipStream_t st, int* nlaunch) {
   if (qmv_nw_for(N) == 8)
-    return skinny_launch_nw<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, st, nlaunch);
-  return skinny_launch_nw<DT, BITS, GS, 4>(x, w, s, b, out, M, N, K, st, nlaunch);
+    return skinny_launch_nw<DT, BITS, GS, 8>(x, w, s, b, out, M, N, K, ws, ws_bytes, st, nlaunch);
+  return skinny_launch_nw<DT, BITS, GS, 4>(x, w, s, b, out, M, N, K, ws, ws_bytes, st, nlaunch);
 }
 
 }  // namespace mq

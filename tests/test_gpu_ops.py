@@ -281,6 +281,42 @@ def test_qmv_shared_x_groups(bits, gs, dtype, N, K):
     np.testing.assert_array_equal(ob[14:16], pair)
 
 
+@pytest.mark.parametrize("bits, gs, dtype, N, K", [
+    (4, 64, "bfloat16", 5120, 17408),    # the down-proj shape: 320 tiles, 8 K slices
+    (4, 32, "float16", 1000, 4096),      # ragged last tile
+    (8, 64, "bfloat16", 2056, 4096),
+    (8, 32, "bfloat16", 640, 2048),
+])
+def test_qmv_split_k_slices(bits, gs, dtype, N, K):
+    """5-16 rows on matrices of fewer than 640 16-row tiles, given the
+    workspace (the operator passes one), run the K slices of the
+    one-workgroup launch on separate workgroups and add the float planes in
+    slice order in a second kernel: the bits of the plain entry point (no
+    workspace, one workgroup per tile group) and of the two-row launches,
+    and the oracle on a column sample."""
+    rng = np.random.default_rng(N + K + bits + gs + 7)
+    w, s, b = random_packed(rng, N, K, gs, bits, dtype)
+    x = act(rng, (16, K), dtype, scale=0.1)
+    args = (to_dev(w), to_dev(s, dtype), to_dev(b, dtype))
+    xd = to_dev(x, dtype)
+    lib = _lib.lib()
+    two = bits16(mq.quantized_matmul(xd[:2], *args, group_size=gs, bits=bits))
+    cols = np.concatenate([np.arange(0, 24), np.arange(N - 24, N), rng.choice(N, 64, False)])
+    colt = torch.from_numpy(cols).cuda()
+    assert lib.mq_quantized_matmul_workspace_size(4, N, K, gs, bits) == 0
+    for M in (5, 8, 9, 12, 16):
+        assert lib.mq_quantized_matmul_workspace_size(M, N, K, gs, bits) == M * N * 32
+        n0 = mq.launch_count()
+        out = mq.quantized_matmul(xd[:M], *args, group_size=gs, bits=bits)
+        assert mq.launch_count() - n0 == 2
+        ob = bits16(out)
+        np.testing.assert_array_equal(ob[:2], two)
+        plain = bits16(_qmm_abi(xd[:M], *args, M, N, K, gs, bits))
+        np.testing.assert_array_equal(ob, plain)
+        ref = O.quantized_matmul_ref(x[:M], w[cols], s[cols], b[cols], gs, bits, dtype)
+        _check(out[:, colt], ref, dtype)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_qmv_two_tiles_tall_matrix(bits):
     """3-4 rows on matrices of 256+ rows per CU run two tiles per x slice;
@@ -434,8 +470,11 @@ def test_skinny_launches_above_16_rows(cfg2_weights, shape, M):
     out = mq.quantized_matmul(xd, *dev)
     launches, m0 = 0, 0
     while m0 < M:
-        m0 += 32 if N == 17408 and M - m0 > 16 else 16
-        launches += 1
+        step = 32 if N == 17408 and M - m0 > 16 else 16
+        # 5-16 rows on the narrow matrix: K slices on separate workgroups,
+        # then the sum kernel
+        launches += 2 if N == 5120 and 5 <= min(step, M - m0) <= 16 else 1
+        m0 += step
     assert mq.launch_count() - n0 == launches
     ob = bits16(out)
     for m0 in range(0, M, 16):
