@@ -49,10 +49,11 @@
 //    weight fragment with two 16-row A tiles (x staged in one buffer per
 //    slice, a barrier before and after).  Each group's arithmetic is that of
 //    the one-group launch.
-//  * Given a workspace, 5-16 rows on matrices of fewer than 640 tiles (K=17408
+//  * Given a workspace, 5-32 rows on matrices of fewer than 640 tiles (K=17408
 //    N=5120) run each tile's K slices on separate workgroups, one slice per
-//    workgroup over ten whole tiles, and a second kernel adds the float
-//    slices in order: the same arithmetic as the one-workgroup launch.
+//    workgroup over ten whole tiles (17-32 rows as two 16-row A tiles), and
+//    a second kernel adds the float slices in order: the same arithmetic as
+//    the one-workgroup launch of each 16 rows.
 //  * Dequantization is the exact fma_mix trick of mq_common.h, rounded to T
 //    per weight (bit-exact MLX dequantization); the packed T pairs are the
 //    B operand of v_mfma_f32_16x16x32 (32 k x 16 rows).  A and B use the same
@@ -282,7 +283,7 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   // pieces this wave loads: q-th of them is piece q * SHX + grp
   constexpr int XPW = XRES ? 1 : (XPL + SHX - 1) / SHX;
   static_assert(!XRES || (XM > 0 && SBL), "resident x is filled with the scale copy");
-  static_assert(MT == 1 || (SHX > 1 && !XRES && XM == 16 * MT && NW > 1),
+  static_assert(MT == 1 || (SHX > 1 && !XRES && XM == 16 * MT && (NW > 1 || SPLIT)),
                 "16-row A tiles beyond the first share staged x slices");
   static_assert(!SPLIT || (NW == 1 && Rows::kCombine), "a split slice hands floats on");
   using T = T16<DT>;
@@ -666,13 +667,15 @@ __device__ __forceinline__ void qmv_tile(const QmvTiles<TJ>& tl, int M, int K, c
   // lane l holds D[4*(l>>4)+v][l&15]: output row 4c+v, column r of the tile
   if constexpr (NW == 1) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int m = 4 * c + v;
-      float val[TJ];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) val[j] = acc[j][0][v];
-      if (m < M) rows_put_tiles<T, TJ>(src, m, r, val, tl.rows);
-    }
+      for (int v = 0; v < 4; ++v) {
+        const int m = 16 * mt + 4 * c + v;
+        float val[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) val[j] = acc[j][mt][v];
+        if (m < M) rows_put_tiles<T, TJ>(src, m, r, val, tl.rows);
+      }
   } else {
 #pragma unroll
     for (int j = 0; j < TJ; ++j)
@@ -855,7 +858,7 @@ struct SplitRows {
   }
 };
 
-// The K slices of a skinny launch over separate workgroups (5-16 rows on
+// The K slices of a skinny launch over separate workgroups (5-32 rows on
 // matrices of few tiles).  The one-workgroup launch runs a tile's nsl K
 // slices on the nsl waves of one workgroup, so every workgroup streams all
 // of x (16 x 17408 x 2 B = 557 KB per workgroup at K=17408, three times the
@@ -869,8 +872,11 @@ struct SplitRows {
 // steps, same accumulator); its float tile goes to part[i % nsl], and
 // qmv_split_sum_kernel adds the nsl planes in slice order and rounds once,
 // as that launch's cross-wave sum does, so the bits are the same.  K must be
-// whole steps.  Block 64 NG, dynamic LDS qmv_shx_lds(1, 16).
-template <int DT, int BITS, int GS, int GPL, int PF, int TJ, int NG>
+// whole steps.  With MT = 2 (17-32 rows) every dequantized weight fragment
+// meets two 16-row A tiles, each with its own accumulator (the arithmetic
+// of a 16-row launch for each), x slices of 32 rows staged in one buffer.
+// Block 64 NG, dynamic LDS qmv_shx_lds(1, 16) (MT = 1) or qmv_x_lds(1, 32).
+template <int DT, int BITS, int GS, int GPL, int PF, int TJ, int NG, int MT = 1>
 __global__ __launch_bounds__(64 * NG) void qmv_split_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
@@ -900,7 +906,7 @@ __global__ __launch_bounds__(64 * NG) void qmv_split_kernel(
   }
   const SplitRows src{x,  (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2),
                       part + (int64_t)ks * M * N, ldx, N, n0, n1};
-  qmv_tile<DT, BITS, GS, GPL, 1, PF, 16, false, TJ, NG, false, 1, true>(
+  qmv_tile<DT, BITS, GS, GPL, 1, PF, 16 * MT, false, TJ, NG, false, MT, true>(
       tl, M, K, src, qmv_smem, nullptr, 0, threadIdx.x & 63, qmv_smem, g, ks, nsl);
 }
 
@@ -1012,7 +1018,7 @@ inline int skinny_launch_shx(int xm, const uint16_t* x, const uint32_t* w, const
   return kStatusUnsupported;
 }
 
-// One split launch (qmv_split_kernel then qmv_split_sum_kernel) of M <= 16
+// One split launch (qmv_split_kernel then qmv_split_sum_kernel) of M <= 32
 // rows: nsl float planes of M x N in part.
 template <int DT, int BITS, int GS>
 inline int skinny_launch_split(const uint16_t* x, const uint32_t* w, const void* s, const void* b,
@@ -1022,11 +1028,19 @@ inline int skinny_launch_split(const uint16_t* x, const uint32_t* w, const void*
   if (nsl != 8) return kStatusUnsupported;            // the sum kernel adds 8 planes
   constexpr int per = kQmvSplitNG * kQmvSplitTJ;
   const int64_t nblk = ((N + 15) / 16 + per - 1) / per;
-  const size_t lds = qmv_shx_lds<BITS, GS, C::GPL>(1, 16);
-  hipLaunchKernelGGL((qmv_split_kernel<DT, BITS, GS, C::GPL, C::PF, kQmvSplitTJ, kQmvSplitNG>),
-                     dim3((unsigned)(nblk * nsl)), dim3(64 * kQmvSplitNG), lds, st, x, w,
-                     (const uint16_t*)s, (const uint16_t*)b, part, M, (int)N, (int)K,
-                     (int64_t)K, nsl);
+  if (M > 16) {
+    const size_t lds = qmv_x_lds<BITS, GS, C::GPL>(1, 32);
+    hipLaunchKernelGGL((qmv_split_kernel<DT, BITS, GS, C::GPL, C::PF, kQmvSplitTJ, kQmvSplitNG, 2>),
+                       dim3((unsigned)(nblk * nsl)), dim3(64 * kQmvSplitNG), lds, st, x, w,
+                       (const uint16_t*)s, (const uint16_t*)b, part, M, (int)N, (int)K,
+                       (int64_t)K, nsl);
+  } else {
+    const size_t lds = qmv_shx_lds<BITS, GS, C::GPL>(1, 16);
+    hipLaunchKernelGGL((qmv_split_kernel<DT, BITS, GS, C::GPL, C::PF, kQmvSplitTJ, kQmvSplitNG>),
+                       dim3((unsigned)(nblk * nsl)), dim3(64 * kQmvSplitNG), lds, st, x, w,
+                       (const uint16_t*)s, (const uint16_t*)b, part, M, (int)N, (int)K,
+                       (int64_t)K, nsl);
+  }
   const int64_t mn = (int64_t)M * N;
   hipLaunchKernelGGL((qmv_split_sum_kernel<DT, 8>), dim3((unsigned)((mn + 255) / 256)), dim3(256),
                      0, st, part, out, mn);
@@ -1044,15 +1058,17 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
     const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
     const uint16_t* xp = (const uint16_t*)x + m0 * K;
     uint16_t* op = (uint16_t*)out + m0 * N;
-    // 5-16 rows on matrices of few tiles, with the caller's workspace: the
-    // K slices on separate workgroups (same bits)
-    if (ws && skinny_split_slices(mt, N, K, BITS, GS) == NW &&
-        ws_bytes >= (size_t)mt * N * NW * sizeof(float) && (int64_t)mt * K * 2 < ((int64_t)1 << 31)) {
+    // 5-32 rows on matrices of few tiles, with the caller's workspace: the
+    // K slices on separate workgroups, up to 32 rows per launch (same bits)
+    const int ms = (int)((M - m0) < 32 ? (M - m0) : 32);
+    if (ws && skinny_split_slices(ms, N, K, BITS, GS) == NW &&
+        ws_bytes >= (size_t)ms * N * NW * sizeof(float) && (int64_t)ms * K * 2 < ((int64_t)1 << 31)) {
       if constexpr (QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {
-        if (int rc = skinny_launch_split<DT, BITS, GS>(xp, w, s, b, op, mt, N, K, (float*)ws, NW,
+        if (int rc = skinny_launch_split<DT, BITS, GS>(xp, w, s, b, op, ms, N, K, (float*)ws, NW,
                                                        st))
           return rc;
         ++*nlaunch;
+        step = ms;
         continue;
       }
     }
