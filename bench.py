@@ -779,7 +779,7 @@ def main():
     sweep = {}
     if not args.no_sweep:
         for (KK, NN, bits, Ms) in ((4096, 4096, 4, (1,)), (5120, 17408, 4, (2, 4, 8, 16)),
-                                   (17408, 5120, 4, (1, 2, 4, 8, 16, 32)),
+                                   (17408, 5120, 4, (1, 2, 4, 8, 16, 32, 48)),
                                    (5120, 248320, 8, (1, 2, 4))):
             for M in Ms:
                 r = measure_qmm(torch, mq, M, NN, KK, bits, 100, 5)

@@ -117,7 +117,7 @@ int mq_quantized_matmul(const void* x, const uint32_t* w, const void* scales,
 /*
  * Bytes of device workspace mq_quantized_matmul_ws can use for an M x N x K
  * problem (float partial sums when the K range is split over workgroups:
- * narrow matrices at prefill widths and at 5-32 rows), 0 when the chosen
+ * narrow matrices at prefill widths and at 5-64 rows), 0 when the chosen
  * plan needs none.
  * No counterpart in the reference (MLX allocates its own temporaries); it
  * is the sizing call of the entry point below.
@@ -130,10 +130,10 @@ size_t mq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int g
  * workspace_bytes bytes (16-byte aligned, may be NULL): when it holds
  * mq_quantized_matmul_workspace_size(M, N, K, group_size, bits) bytes, wide
  * problems may split K over workgroups and reduce the partials in a second
- * kernel (same results up to the order of the float sums), and 5-32 rows on
+ * kernel (same results up to the order of the float sums), and 5-64 rows on
  * matrices of fewer than 640 16-row tiles run their K slices on separate
- * workgroups and add them in a second kernel (the same bits as without the
- * workspace).  Replaces the
+ * workgroups and add them in a second kernel (every 16 rows get the bits of
+ * a 16-row call without the workspace).  Replaces the
  * same mx.quantized_matmul call as mq_quantized_matmul; calls sharing a
  * workspace must be ordered (one stream).
  */

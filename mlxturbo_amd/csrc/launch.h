@@ -324,25 +324,26 @@ inline bool skinny_resident_x_fits(int64_t m, int64_t K, int bits, int gs) {
 
 // K slices (the waves of the one-workgroup launch, 8 on matrices of fewer
 // than 640 16-row tiles) that a skinny launch of m rows runs on separate
-// workgroups (qmv.cuh qmv_split_kernel), or 0: 5-32 rows (16 or 32
+// workgroups (qmv.cuh qmv_split_kernel), or 0: 5-64 rows (16, 32 or 64
 // streamed x rows: steps of at most 256 codes), 8 slices, K whole steps.  K=17408
 // N=5120, one box: M=8 / 9 / 16 20.9-21.2 / 21.4 / 21.6 us against
 // 21.6-21.8 / 23.0-23.2 / 24.1-24.5 on one workgroup per tile group, M=20 /
 // 24 / 32 25.7 / 26.0 / 26.6 us against ~40-43 as a 16-row launch and a
-// remainder (or ~49 on the wide tile at 32); 2 and 4 rows lost (20.6-21.1
+// remainder (or ~49 on the wide tile at 32), M=40 / 48 / 64 32.2 / 32.8 /
+// 35.2 us against 43.1 / 43.1 / 47-49; 2 and 4 rows lost (20.6-21.1
 // against 17.9-19.4).
 inline int skinny_split_slices(int64_t m, int64_t N, int64_t K, int bits, int gs) {
   const int64_t stepg = (bits == 4 && gs == 32) ? 8 : 4;   // groups per step
-  if (m < 5 || m > 32 || (N + 15) / 16 >= 640 || stepg * gs > 256 || (K / gs) % stepg) return 0;
+  if (m < 5 || m > 64 || (N + 15) / 16 >= 640 || stepg * gs > 256 || (K / gs) % stepg) return 0;
   return 8;
 }
 
 // Float partial planes of the split skinny launches of an M-row call (the
-// launch loop of qmv.cuh: up to 32 rows per split launch, 16 otherwise).
+// launch loop of qmv.cuh: up to 64 rows per split launch, 16 otherwise).
 inline size_t skinny_split_bytes(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   int64_t most = 0;                                 // rows of the largest split launch
   for (int64_t r = M; r > 0;) {
-    const int64_t ms = r < 32 ? r : 32;
+    const int64_t ms = r < 64 ? r : 64;
     const int64_t step = skinny_split_slices(ms, N, K, bits, gs) ? ms : (r < 16 ? r : 16);
     if (skinny_split_slices(step, N, K, bits, gs)) most = step > most ? step : most;
     r -= step;
@@ -365,13 +366,13 @@ inline bool wide_route(int64_t M, int64_t N, int64_t K, int bits, int gs, int cu
   const bool shared_x = sx > 0;
   double skinny_us = 0.0;
   for (int64_t m0 = 0, step = 16; m0 < M; m0 += step) {
-    // with the workspace, 5-32 rows on matrices of few tiles run as one
-    // split launch (K=17408 N=5120: 16 / 32 rows 21.7 / 26.6 us = 1.4 / 1.7
-    // x one; M=48 43.1 us as 32 + 16, M=64 on the wide tile 47-48.5)
-    const int64_t ms = M - m0 < 32 ? M - m0 : 32;
+    // with the workspace, 5-64 rows on matrices of few tiles run as one
+    // split launch (K=17408 N=5120: 16 / 32 / 64 rows 21.7 / 26.0-26.6 /
+    // 35.2 us = 1.4 / 1.7 / 2.3 x one; from 96 rows the wide tile, 55.6 us)
+    const int64_t ms = M - m0 < 64 ? M - m0 : 64;
     if (split_ok && skinny_split_slices(ms, N, K, bits, gs)) {
       step = ms;
-      skinny_us += one * (ms > 16 ? 1.7 : 1.4);
+      skinny_us += one * (ms > 32 ? 2.3 : ms > 16 ? 1.7 : 1.4);
       continue;
     }
     step = sx == 32 && M - m0 > 16 ? 32 : 16;

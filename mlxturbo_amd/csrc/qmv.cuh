@@ -49,9 +49,9 @@
 //    weight fragment with two 16-row A tiles (x staged in one buffer per
 //    slice, a barrier before and after).  Each group's arithmetic is that of
 //    the one-group launch.
-//  * Given a workspace, 5-32 rows on matrices of fewer than 640 tiles (K=17408
+//  * Given a workspace, 5-64 rows on matrices of fewer than 640 tiles (K=17408
 //    N=5120) run each tile's K slices on separate workgroups, one slice per
-//    workgroup over ten whole tiles (17-32 rows as two 16-row A tiles), and
+//    workgroup over ten whole tiles (17-64 rows as 2 or 4 16-row A tiles), and
 //    a second kernel adds the float slices in order: the same arithmetic as
 //    the one-workgroup launch of each 16 rows.
 //  * Dequantization is the exact fma_mix trick of mq_common.h, rounded to T
@@ -858,7 +858,7 @@ struct SplitRows {
   }
 };
 
-// The K slices of a skinny launch over separate workgroups (5-32 rows on
+// The K slices of a skinny launch over separate workgroups (5-64 rows on
 // matrices of few tiles).  The one-workgroup launch runs a tile's nsl K
 // slices on the nsl waves of one workgroup, so every workgroup streams all
 // of x (16 x 17408 x 2 B = 557 KB per workgroup at K=17408, three times the
@@ -872,10 +872,11 @@ struct SplitRows {
 // steps, same accumulator); its float tile goes to part[i % nsl], and
 // qmv_split_sum_kernel adds the nsl planes in slice order and rounds once,
 // as that launch's cross-wave sum does, so the bits are the same.  K must be
-// whole steps.  With MT = 2 (17-32 rows) every dequantized weight fragment
-// meets two 16-row A tiles, each with its own accumulator (the arithmetic
-// of a 16-row launch for each), x slices of 32 rows staged in one buffer.
-// Block 64 NG, dynamic LDS qmv_shx_lds(1, 16) (MT = 1) or qmv_x_lds(1, 32).
+// whole steps.  With MT = 2 or 4 (17-32 or 33-64 rows) every dequantized
+// weight fragment meets MT 16-row A tiles, each with its own accumulator
+// (the arithmetic of a 16-row launch for each), x slices of 16 MT rows
+// staged in one buffer.  Block 64 NG, dynamic LDS qmv_shx_lds(1, 16) (MT =
+// 1) or qmv_x_lds(1, 16 MT).
 template <int DT, int BITS, int GS, int GPL, int PF, int TJ, int NG, int MT = 1>
 __global__ __launch_bounds__(64 * NG) void qmv_split_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
@@ -1018,7 +1019,7 @@ inline int skinny_launch_shx(int xm, const uint16_t* x, const uint32_t* w, const
   return kStatusUnsupported;
 }
 
-// One split launch (qmv_split_kernel then qmv_split_sum_kernel) of M <= 32
+// One split launch (qmv_split_kernel then qmv_split_sum_kernel) of M <= 64
 // rows: nsl float planes of M x N in part.
 template <int DT, int BITS, int GS>
 inline int skinny_launch_split(const uint16_t* x, const uint32_t* w, const void* s, const void* b,
@@ -1028,7 +1029,13 @@ inline int skinny_launch_split(const uint16_t* x, const uint32_t* w, const void*
   if (nsl != 8) return kStatusUnsupported;            // the sum kernel adds 8 planes
   constexpr int per = kQmvSplitNG * kQmvSplitTJ;
   const int64_t nblk = ((N + 15) / 16 + per - 1) / per;
-  if (M > 16) {
+  if (M > 32) {
+    const size_t lds = qmv_x_lds<BITS, GS, C::GPL>(1, 64);
+    hipLaunchKernelGGL((qmv_split_kernel<DT, BITS, GS, C::GPL, C::PF, kQmvSplitTJ, kQmvSplitNG, 4>),
+                       dim3((unsigned)(nblk * nsl)), dim3(64 * kQmvSplitNG), lds, st, x, w,
+                       (const uint16_t*)s, (const uint16_t*)b, part, M, (int)N, (int)K,
+                       (int64_t)K, nsl);
+  } else if (M > 16) {
     const size_t lds = qmv_x_lds<BITS, GS, C::GPL>(1, 32);
     hipLaunchKernelGGL((qmv_split_kernel<DT, BITS, GS, C::GPL, C::PF, kQmvSplitTJ, kQmvSplitNG, 2>),
                        dim3((unsigned)(nblk * nsl)), dim3(64 * kQmvSplitNG), lds, st, x, w,
@@ -1058,9 +1065,9 @@ inline int skinny_launch_nw(const void* x, const uint32_t* w, const void* s, con
     const int mt = (int)((M - m0) < 16 ? (M - m0) : 16);
     const uint16_t* xp = (const uint16_t*)x + m0 * K;
     uint16_t* op = (uint16_t*)out + m0 * N;
-    // 5-32 rows on matrices of few tiles, with the caller's workspace: the
-    // K slices on separate workgroups, up to 32 rows per launch (same bits)
-    const int ms = (int)((M - m0) < 32 ? (M - m0) : 32);
+    // 5-64 rows on matrices of few tiles, with the caller's workspace: the
+    // K slices on separate workgroups, up to 64 rows per launch (same bits)
+    const int ms = (int)((M - m0) < 64 ? (M - m0) : 64);
     if (ws && skinny_split_slices(ms, N, K, BITS, GS) == NW &&
         ws_bytes >= (size_t)ms * N * NW * sizeof(float) && (int64_t)ms * K * 2 < ((int64_t)1 << 31)) {
       if constexpr (QmvGeom<BITS, GS, C::GPL>::STEPK <= 256) {

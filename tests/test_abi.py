@@ -96,16 +96,16 @@ def test_qmm_workspace_sizing(lib):
 def test_qmm_route_by_workspace(lib):
     """The wide/skinny route model as the workspace sizing sees it (wide
     tiles that split K ask for float partials; skinny launches need none,
-    but those of 5-32 rows on matrices of few tiles split their 8 K slices
-    over workgroups into float planes, up to 32 rows per launch): on
-    K=17408 N=5120 up to 48 rows run as split skinny launches; on K=5120
+    but those of 5-64 rows on matrices of few tiles split their 8 K slices
+    over workgroups into float planes, up to 64 rows per launch): on
+    K=17408 N=5120 at least 48 rows run as one split skinny launch; on K=5120
     N=17408 up to ~70 rows as 32-row shared-x launches."""
     narrow = lambda M: lib.mq_quantized_matmul_workspace_size(M, 5120, 17408, 64, 4)  # noqa: E731
     tall = lambda M: lib.mq_quantized_matmul_workspace_size(M, 17408, 5120, 64, 4)  # noqa: E731
     planes = lambda m: m * 5120 * 8 * 4  # noqa: E731
     assert narrow(4) == 0 and narrow(5) == planes(5) and narrow(16) == planes(16)
-    assert narrow(17) == planes(17) and narrow(32) == planes(32) and narrow(48) == planes(32)
-    assert narrow(1024) > 0 and narrow(1024) != planes(32)
+    assert narrow(17) == planes(17) and narrow(32) == planes(32) and narrow(48) == planes(48)
+    assert narrow(1024) > 0 and narrow(1024) != planes(64)
     assert tall(32) == 0 and tall(64) == 0 and tall(96) > 0
 
 

@@ -296,7 +296,7 @@ def test_qmv_split_k_slices(bits, gs, dtype, N, K):
     and the oracle on a column sample."""
     rng = np.random.default_rng(N + K + bits + gs + 7)
     w, s, b = random_packed(rng, N, K, gs, bits, dtype)
-    x = act(rng, (32, K), dtype, scale=0.1)
+    x = act(rng, (64, K), dtype, scale=0.1)
     args = (to_dev(w), to_dev(s, dtype), to_dev(b, dtype))
     xd = to_dev(x, dtype)
     lib = _lib.lib()
@@ -304,7 +304,7 @@ def test_qmv_split_k_slices(bits, gs, dtype, N, K):
     cols = np.concatenate([np.arange(0, 24), np.arange(N - 24, N), rng.choice(N, 64, False)])
     colt = torch.from_numpy(cols).cuda()
     assert lib.mq_quantized_matmul_workspace_size(4, N, K, gs, bits) == 0
-    for M in (5, 8, 9, 12, 16) + ((20, 32) if N == 5120 else ()):
+    for M in (5, 8, 9, 12, 16) + ((20, 32, 40, 64) if N == 5120 else ()):
         assert lib.mq_quantized_matmul_workspace_size(M, N, K, gs, bits) == M * N * 32
         n0 = mq.launch_count()
         out = mq.quantized_matmul(xd[:M], *args, group_size=gs, bits=bits)
@@ -312,11 +312,11 @@ def test_qmv_split_k_slices(bits, gs, dtype, N, K):
         ob = bits16(out)
         np.testing.assert_array_equal(ob[:2], two)
         if M > 16:
-            # two 16-row A tiles: each the arithmetic of its 16-row launch
-            hi = bits16(mq.quantized_matmul(xd[16:M], *args, group_size=gs, bits=bits))
-            np.testing.assert_array_equal(ob[16:], hi)
-            np.testing.assert_array_equal(
-                ob[:16], bits16(mq.quantized_matmul(xd[:16], *args, group_size=gs, bits=bits)))
+            # 2 or 4 16-row A tiles: each the arithmetic of its 16-row launch
+            for m0 in range(0, M, 16):
+                blk = bits16(mq.quantized_matmul(xd[m0:min(M, m0 + 16)], *args, group_size=gs,
+                                                 bits=bits))
+                np.testing.assert_array_equal(ob[m0:m0 + 16], blk)
             M_ = 16
         else:
             M_ = M
@@ -479,10 +479,10 @@ def test_skinny_launches_above_16_rows(cfg2_weights, shape, M):
     out = mq.quantized_matmul(xd, *dev)
     launches, m0 = 0, 0
     while m0 < M:
-        if N == 5120 and min(32, M - m0) >= 5:
-            # the narrow matrix: up to 32 rows with the K slices on separate
+        if N == 5120 and min(64, M - m0) >= 5:
+            # the narrow matrix: up to 64 rows with the K slices on separate
             # workgroups, then the sum kernel
-            step, n = min(32, M - m0), 2
+            step, n = min(64, M - m0), 2
         else:
             step, n = (32 if N == 17408 and M - m0 > 16 else 16), 1
         launches += n
