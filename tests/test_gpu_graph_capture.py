@@ -68,3 +68,34 @@ def test_gather_replay_after_workspace_growth():
             torch.cuda.synchronize()
             np.testing.assert_array_equal(bits16(again), bits16(want))
     del big
+
+
+@pytest.mark.parametrize("M", [16, 40])
+def test_split_skinny_replays(M):
+    """The split skinny launch (K slices on separate workgroups writing float
+    planes into the stream's workspace, then the ordered sum kernel) under
+    capture: every replay, with eager calls of other widths on the same
+    stream in between, gives the eager bits."""
+    rng = np.random.default_rng(30 + M)
+    N, K = 5120, 17408                   # the down-proj shape: 320 tiles, 8 K slices
+    assert mq._lib.lib().mq_quantized_matmul_workspace_size(M, N, K, 64, 4) == M * N * 32
+    w, s, b = random_packed(rng, N, K)
+    args = (to_dev(w), to_dev(s, "bfloat16"), to_dev(b, "bfloat16"))
+    x = to_dev(act(rng, (64, K), scale=0.1), "bfloat16")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        want = mq.quantized_matmul(x[:M], *args)                    # warm-up
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            got = mq.quantized_matmul(x[:M], *args)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(bits16(got), bits16(want), f"replay {rep}")
+            other = mq.quantized_matmul(x[:64 - M], *args)          # same workspace
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(
+                bits16(other)[:8], bits16(mq.quantized_matmul(x[:8], *args)))
